@@ -1,0 +1,116 @@
+/*
+ * mi_kernels.h -- C ABI of the MI355X (gfx950) kernel_library hot path.
+ *
+ * The reference (awslabs/nki-autotune) has no native boundary: its kernels
+ * are @nki.jit Python functions that take HBM tensors positionally and
+ * allocate and return their output, and its profiler reaches them through
+ * KernelJob source text.  Each entry point below replaces one reference
+ * interface; the citation names it.  All pointers are device pointers owned
+ * by the caller; tensors are row-major and contiguous.  bf16 tensors are
+ * passed as raw 16-bit storage.  Launches are asynchronous on `stream`
+ * (a hipStream_t, NULL = default stream).  No entry point allocates device
+ * memory and no entry point throws.
+ *
+ * Return value: 0 on success; a positive MI_E_* legality code when the
+ * request is rejected before launch; a negative value (-hipError_t) when the
+ * HIP runtime reports an error.  mi_last_error() holds the message of the
+ * last failure on the calling thread.
+ */
+#ifndef MI_KERNELS_H
+#define MI_KERNELS_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Kernel identifiers (one per hot-path kernel family). */
+enum {
+  MI_KERNEL_MATMUL_LHST_RHS_BF16 = 0, /* lhsT[K,M]^T . rhs[K,N], bf16 in/out, fp32 accumulate */
+  MI_KERNEL_MATMUL_LHST_RHS_F32 = 1,  /* same product in fp32            */
+  MI_KERNEL_RMSNORM_MATMUL_BF16 = 2,  /* rmsnorm(x[M,K]) * gamma[K] . W[K,N], bf16 in/out     */
+  MI_NUM_KERNELS = 3
+};
+
+/* Legality / rejection codes (positive return values). */
+enum {
+  MI_OK = 0,
+  MI_E_NO_INSTANCE = 1,    /* the tile config was not compiled into this library     */
+  MI_E_LDS = 2,            /* LDS bytes of the config exceed 160 KiB                 */
+  MI_E_WAVE_TILE = 3,      /* a wave's share of the block is smaller than one MFMA   */
+  MI_E_ALIGN = 4,          /* M or N not a multiple of 8 (16-byte rows required)     */
+  MI_E_RANGE = 5,          /* an operand is 4 GiB or larger (32-bit buffer offsets)  */
+  MI_E_ARGS = 6,           /* null pointer, non-positive size, bad eps               */
+  MI_E_KERNEL = 7,         /* unknown kernel id                                      */
+  MI_E_SPLIT = 8           /* split_k unsupported for this kernel / shape            */
+};
+
+/*
+ * Tile meta-parameters: the CDNA4 search space that replaces the NKI block
+ * knobs (tbm/tbn/tbk, dim_order, multi-buffer counts;
+ * reference kernel_library/README.md:12-13,
+ * kernel_library/matmul/lhsT_rhs/kernel_hand_90.92mfu.py:107-112).
+ *   block_m, block_n, block_k : workgroup tile (output rows, cols, K panel)
+ *   waves                     : wavefronts (64 lanes) per workgroup
+ *   lds_stages                : LDS ring depth for K panels (1 or 2)
+ *   split_k                   : must be 1 (reserved)
+ *   group_m                   : L2 raster group height in tiles (0 = default 8)
+ *   variant                   : kernel-specific; for rmsnorm_matmul 0 applies
+ *                               1/rms to the fp32 accumulator after the K loop,
+ *                               1 computes 1/rms in a prologue and scales the
+ *                               rows while staging them into LDS.
+ */
+typedef struct {
+  int block_m, block_n, block_k, waves, lds_stages, split_k, group_m, variant;
+} mi_tile_cfg;
+
+/* Static legality of `cfg` for kernel `kernel_id` at M,N,K (no launch).
+ * Replaces the compile-time rejection of an NKI candidate
+ * (reference autotune/src/autotune/runner/compile.py:197-244, which turns a
+ * failed neuronx-cc compile into an error string). */
+int mi_cfg_check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K);
+
+/* Enumerate the configs compiled into the library for `kernel_id`.
+ * mi_num_configs returns the count; mi_get_config fills cfg for idx. */
+int mi_num_configs(int kernel_id);
+int mi_get_config(int kernel_id, int idx, mi_tile_cfg* cfg);
+
+/* The library's default (tuned) config for a kernel at a shape. */
+int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
+
+/* out[M,N] = lhsT[K,M]^T . rhs[K,N]; bf16 storage, fp32 accumulation over
+ * the whole K, one round-to-nearest-even store.
+ * Replaces matmul_lhsT_rhs_nkigym(lhs_T, rhs)
+ * (reference kernel_library/matmul/lhsT_rhs/kernel_hand_90.92mfu.py:101-131).
+ * cfg == NULL selects mi_default_config. */
+int mi_matmul_lhsT_rhs_bf16(const void* lhsT, const void* rhs, void* out, int M, int N, int K,
+                            const mi_tile_cfg* cfg, void* stream);
+
+/* fp32 variant of the same product (the fp32 CPU-simulation semantics of
+ * reference nkigym/src/nkigym/synthesis/simulate_nki.py:24-48). */
+int mi_matmul_lhsT_rhs_f32(const float* lhsT, const float* rhs, float* out, int M, int N, int K,
+                           const mi_tile_cfg* cfg, void* stream);
+
+/* out[M,N] = (x[M,K] / sqrt(mean_k x^2 + eps) * gamma[K]) . W[K,N];
+ * bf16 storage, fp32 accumulation and fp32 row statistics.
+ * gamma == NULL means gamma = 1, which is exactly the reference kernel
+ * rmsnorm_matmul_online(lhs, rhs) with EPS = 1e-6
+ * (reference kernel_library/rmsnorm_matmul/kernel_hand_online.py:195-353). */
+int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void* out, int M, int N,
+                           int K, float eps, const mi_tile_cfg* cfg, void* stream);
+
+/* Device discovery: number of visible HIP devices and the gfx arch name of
+ * device 0 (written to arch, at most arch_len bytes).  Returns 0 or -error.
+ * Replaces detect_neuron_cores()
+ * (reference autotune/src/autotune/runner/detect.py:7-20). */
+int mi_device_info(int* num_devices, char* arch, int arch_len, int* num_cus);
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* mi_last_error(void);
+
+/* Library version string. */
+const char* mi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MI_KERNELS_H */

@@ -1,0 +1,242 @@
+// mi_capi.hip -- the C ABI declared in include/mi_kernels.h.
+//
+// Stateless launchers over the instance table: look the config up, check
+// its static legality for the shape, launch on the caller's stream.  No
+// entry point allocates memory or throws; failures are return codes plus a
+// thread-local message (mi_last_error).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <vector>
+
+#include "mi_registry.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  snprintf(g_err, sizeof(g_err), "%s: %s", what, hipGetErrorString(e));
+  return -(int)e;
+}
+
+const std::vector<mi::MiEntry>& registry() {
+  static std::vector<mi::MiEntry> all;
+  static std::once_flag once;
+  std::call_once(once, [] {
+    typedef const mi::MiEntry* (*TableFn)(int*);
+    const TableFn tables[] = {mi::table_mm_bm32,  mi::table_mm_bm64,  mi::table_mm_bm128, mi::table_mm_bm256,
+                              mi::table_rms_bm64, mi::table_rms_bm128, mi::table_rms_bm256, mi::table_f32};
+    for (TableFn f : tables) {
+      int n = 0;
+      const mi::MiEntry* t = f(&n);
+      all.insert(all.end(), t, t + n);
+    }
+  });
+  return all;
+}
+
+bool same_instance(const mi_tile_cfg& a, const mi_tile_cfg& b) {
+  return a.block_m == b.block_m && a.block_n == b.block_n && a.block_k == b.block_k && a.waves == b.waves &&
+         a.lds_stages == b.lds_stages && a.variant == b.variant;
+}
+
+const mi::MiEntry* find(int kernel_id, const mi_tile_cfg& cfg) {
+  for (const mi::MiEntry& e : registry())
+    if (e.kernel_id == kernel_id && same_instance(e.cfg, cfg)) return &e;
+  return nullptr;
+}
+
+// Host restatement of mi::WaveGrid: can `waves` waves split a BM x BN block
+// into per-wave blocks that are whole 32x32 MFMA tiles?
+bool wave_grid_ok(int bm, int bn, int waves) {
+  for (int wm = 1; wm <= waves; wm *= 2) {
+    const int wn = waves / wm;
+    if (wm * wn != waves || bm % wm || bn % wn) continue;
+    const int tm = bm / wm, tn = bn / wn;
+    if (tm >= 32 && tn >= 32 && tm % 32 == 0 && tn % 32 == 0) return true;
+  }
+  return false;
+}
+
+constexpr unsigned long long kMaxOffset = 0xFFFFFFFFull;  // 32-bit buffer offsets
+constexpr int kLdsLimit = 160 * 1024;
+
+int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::MiEntry** out) {
+  if (kernel_id < 0 || kernel_id >= MI_NUM_KERNELS) return fail(MI_E_KERNEL, "unknown kernel id %d", kernel_id);
+  if (!cfg) return fail(MI_E_ARGS, "null config");
+  if (M < 0 || N < 0 || K < 0) return fail(MI_E_ARGS, "negative size M=%d N=%d K=%d", M, N, K);
+  const mi_tile_cfg& c = *cfg;
+  if (c.block_m <= 0 || c.block_n <= 0 || c.block_k <= 0 || c.waves <= 0 || c.lds_stages <= 0)
+    return fail(MI_E_ARGS, "non-positive tile parameter");
+  if (c.split_k != 1) return fail(MI_E_SPLIT, "split_k=%d unsupported (must be 1)", c.split_k);
+  if (c.group_m < 0) return fail(MI_E_ARGS, "group_m=%d negative", c.group_m);
+  if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_F32 && !wave_grid_ok(c.block_m, c.block_n, c.waves))
+    return fail(MI_E_WAVE_TILE, "%d waves cannot tile a %dx%d block in 32x32 MFMA tiles", c.waves, c.block_m,
+                c.block_n);
+  const long long lds = (long long)c.lds_stages * (c.block_m + c.block_n) * c.block_k *
+                        (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_F32 ? 4 : 2);
+  if (lds > kLdsLimit) return fail(MI_E_LDS, "LDS %lld bytes > %d", lds, kLdsLimit);
+  const mi::MiEntry* e = find(kernel_id, c);
+  if (!e)
+    return fail(MI_E_NO_INSTANCE, "no compiled instance for kernel %d bm=%d bn=%d bk=%d waves=%d stages=%d variant=%d",
+                kernel_id, c.block_m, c.block_n, c.block_k, c.waves, c.lds_stages, c.variant);
+  if (e->lds_bytes > kLdsLimit) return fail(MI_E_LDS, "instance LDS %d bytes > %d", e->lds_bytes, kLdsLimit);
+  if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_F32) {
+    if (M % 8 || N % 8) return fail(MI_E_ALIGN, "M=%d and N=%d must be multiples of 8", M, N);
+    if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 && K % 8)
+      return fail(MI_E_ALIGN, "K=%d must be a multiple of 8 for rmsnorm_matmul", K);
+    const unsigned long long kpad = (unsigned long long)K + (unsigned long long)c.block_k;
+    const unsigned long long mpad = (unsigned long long)M + (unsigned long long)c.block_m;
+    unsigned long long a_span, b_span;
+    if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16) {
+      a_span = kpad * (unsigned long long)M * 2ull;
+    } else {
+      a_span = mpad * (unsigned long long)K * 2ull;
+    }
+    b_span = kpad * (unsigned long long)N * 2ull;
+    if (a_span > kMaxOffset || b_span > kMaxOffset)
+      return fail(MI_E_RANGE, "operand spans exceed 32-bit buffer offsets (%llu, %llu bytes)", a_span, b_span);
+  }
+  if (out) *out = e;
+  g_err[0] = '\0';
+  return MI_OK;
+}
+
+int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
+  (void)K;
+  mi_tile_cfg c = {256, 256, 64, 8, 2, 1, 8, 0};
+  if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_F32) {
+    c = {64, 64, 16, 4, 1, 1, 0, 0};
+  } else if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16) {
+    if (M <= 32) c = {32, 256, 128, 4, 2, 1, 8, 0};
+    else if (M <= 64) c = {64, 256, 64, 4, 2, 1, 8, 0};
+    else if (M <= 128) c = {128, 128, 64, 4, 2, 1, 8, 0};
+    else if ((long long)M * N <= 4096LL * 4096LL) c = {128, 256, 64, 8, 2, 1, 8, 0};
+  } else if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16) {
+    if (M <= 128) c = {64, 128, 64, 4, 2, 1, 8, 0};
+    else if ((long long)M * N <= 4096LL * 4096LL) c = {128, 256, 64, 8, 2, 1, 8, 0};
+  }
+  *cfg = c;
+  return MI_OK;
+}
+
+int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, void* stream) {
+  mi_tile_cfg cfg;
+  if (cfg_in) cfg = *cfg_in;
+  else pick_default(kernel_id, args_in.M, args_in.N, args_in.K, &cfg);
+  const mi::MiEntry* e = nullptr;
+  const int rc = check(kernel_id, &cfg, args_in.M, args_in.N, args_in.K, &e);
+  if (rc != MI_OK) return rc;
+  mi::MiArgs a = args_in;
+  a.group_m = cfg.group_m > 0 ? cfg.group_m : 8;
+  const hipError_t err = e->launch(a, (hipStream_t)stream);
+  if (err != hipSuccess) return hip_fail(err, "kernel launch");
+  return MI_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_cfg_check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K) {
+  return check(kernel_id, cfg, M, N, K, nullptr);
+}
+
+int mi_num_configs(int kernel_id) {
+  int n = 0;
+  for (const mi::MiEntry& e : registry()) n += e.kernel_id == kernel_id;
+  return n;
+}
+
+int mi_get_config(int kernel_id, int idx, mi_tile_cfg* cfg) {
+  if (!cfg) return fail(MI_E_ARGS, "null config");
+  int i = 0;
+  for (const mi::MiEntry& e : registry()) {
+    if (e.kernel_id != kernel_id) continue;
+    if (i++ == idx) {
+      *cfg = e.cfg;
+      cfg->group_m = 8;
+      return MI_OK;
+    }
+  }
+  return fail(MI_E_ARGS, "config index %d out of range for kernel %d", idx, kernel_id);
+}
+
+int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
+  if (kernel_id < 0 || kernel_id >= MI_NUM_KERNELS) return fail(MI_E_KERNEL, "unknown kernel id %d", kernel_id);
+  if (!cfg) return fail(MI_E_ARGS, "null config");
+  return pick_default(kernel_id, M, N, K, cfg);
+}
+
+int mi_matmul_lhsT_rhs_bf16(const void* lhsT, const void* rhs, void* out, int M, int N, int K,
+                            const mi_tile_cfg* cfg, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return fail(MI_E_ARGS, "negative size M=%d N=%d K=%d", M, N, K);
+  if (M == 0 || N == 0) return MI_OK;
+  if (!out) return fail(MI_E_ARGS, "null output pointer");
+  if (K == 0) {
+    const hipError_t e = hipMemsetAsync(out, 0, (size_t)M * N * 2, (hipStream_t)stream);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "hipMemsetAsync");
+  }
+  if (!lhsT || !rhs) return fail(MI_E_ARGS, "null input pointer");
+  mi::MiArgs a = {lhsT, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
+  return run(MI_KERNEL_MATMUL_LHST_RHS_BF16, cfg, a, stream);
+}
+
+int mi_matmul_lhsT_rhs_f32(const float* lhsT, const float* rhs, float* out, int M, int N, int K,
+                           const mi_tile_cfg* cfg, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return fail(MI_E_ARGS, "negative size M=%d N=%d K=%d", M, N, K);
+  if (M == 0 || N == 0) return MI_OK;
+  if (!out) return fail(MI_E_ARGS, "null output pointer");
+  if (K == 0) {
+    const hipError_t e = hipMemsetAsync(out, 0, (size_t)M * N * 4, (hipStream_t)stream);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "hipMemsetAsync");
+  }
+  if (!lhsT || !rhs) return fail(MI_E_ARGS, "null input pointer");
+  mi::MiArgs a = {lhsT, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
+  return run(MI_KERNEL_MATMUL_LHST_RHS_F32, cfg, a, stream);
+}
+
+int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void* out, int M, int N, int K,
+                           float eps, const mi_tile_cfg* cfg, void* stream) {
+  if (M < 0 || N < 0 || K <= 0) return fail(MI_E_ARGS, "bad size M=%d N=%d K=%d (K must be positive)", M, N, K);
+  if (!(eps >= 0.0f) || eps > 3.0e38f) return fail(MI_E_ARGS, "eps must be finite and >= 0");
+  if (M == 0 || N == 0) return MI_OK;
+  if (!x || !W || !out) return fail(MI_E_ARGS, "null pointer");
+  mi::MiArgs a = {x, W, gamma, out, M, N, K, eps, 1.0f / (float)K, 8};
+  return run(MI_KERNEL_RMSNORM_MATMUL_BF16, cfg, a, stream);
+}
+
+int mi_device_info(int* num_devices, char* arch, int arch_len, int* num_cus) {
+  int n = 0;
+  hipError_t e = hipGetDeviceCount(&n);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDeviceCount");
+  if (num_devices) *num_devices = n;
+  if (n > 0 && (arch || num_cus)) {
+    hipDeviceProp_t p;
+    e = hipGetDeviceProperties(&p, 0);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDeviceProperties");
+    if (arch && arch_len > 0) {
+      strncpy(arch, p.gcnArchName, (size_t)arch_len - 1);
+      arch[arch_len - 1] = '\0';
+    }
+    if (num_cus) *num_cus = p.multiProcessorCount;
+  }
+  return MI_OK;
+}
+
+const char* mi_last_error(void) { return g_err; }
+
+const char* mi_version(void) { return "mi_kernels 0.1 gfx950"; }
+
+}  // extern "C"

@@ -1,0 +1,583 @@
+// mi_gemm.hpp -- gfx950 (CDNA4) kernels of the kernel_library hot path.
+//
+// Two templated kernels share one MFMA core:
+//   mm_lhsT_rhs_bf16<BM,BN,BK,WAVES,STAGES>    out = lhsT^T . rhs
+//   rmsnorm_mm_bf16<BM,BN,BK,WAVES,STAGES,PRE> out = rmsnorm(x) * gamma . W
+//
+// Both reference kernels keep the contraction axis K as the row index of
+// every operand (lhsT[K,M], rhs[K,N]; reference
+// kernel_library/matmul/lhsT_rhs/kernel_hand_90.92mfu.py:101-105), so a
+// 16-byte global load brings 8 consecutive M (or N) values of one K row.
+// The MFMA wants 8 consecutive K values per lane.  The transpose happens in
+// the LDS read: panels are copied HBM->LDS unchanged by buffer_load ... lds
+// (no VGPR staging), and each MFMA operand is assembled by two
+// ds_read_b64_tr_b16, which read a 4x16 block of 16-bit elements across a
+// 16-lane group and hand lane j the 4 values of column j.
+//
+// MFMA v_mfma_f32_32x32x16_bf16 lane layout (gfx950, checked on hardware):
+//   A (32x16): lane l holds A[l%32][8*(l/32) + 0..7]
+//   B (16x32): lane l holds B[8*(l/32) + 0..7][l%32]
+//   D (32x32): lane l, reg r holds D[8*(r/4) + 4*(l/32) + r%4][l%32]
+// The kernels issue mfma(Bfrag, Afrag), i.e. they compute out^T per 32x32
+// tile, so each lane ends with 4 consecutive N values of one output row.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+#define MI_LDS __attribute__((address_space(3)))
+
+// gfx9 buffer descriptor word 3 (raw buffer, 32-bit element format).
+constexpr int kRsrcWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+
+// s_waitcnt vmcnt(0): every outstanding vector-memory load (including the
+// LDS-direct loads) has landed.  expcnt/lgkmcnt fields are left at max.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// Wave grid: WM x WN waves, each owning a (BM/WM) x (BN/WN) block that is
+// a whole number of 32x32 MFMA tiles.  The most square wave block wins.
+template <int BM, int BN, int WAVES>
+struct WaveGrid {
+  static constexpr int pick() {
+    int best = -1, bestd = 1 << 30;
+    for (int wm = 1; wm <= WAVES; wm *= 2) {
+      const int wn = WAVES / wm;
+      if (wm * wn != WAVES || BM % wm || BN % wn) continue;
+      const int tm = BM / wm, tn = BN / wn;
+      if (tm < 32 || tn < 32 || tm % 32 || tn % 32) continue;
+      const int d = tm > tn ? tm - tn : tn - tm;
+      if (d < bestd) { bestd = d; best = wm; }
+    }
+    return best;
+  }
+  static constexpr int WM = pick();
+  static constexpr bool ok = WM > 0;
+  static constexpr int WN = ok ? WAVES / WM : 1;
+  static constexpr int WTM = ok ? BM / WM : 32;
+  static constexpr int WTN = ok ? BN / WN : 32;
+  static constexpr int TM = WTM / 32;
+  static constexpr int TN = WTN / 32;
+};
+
+// Logical tile of this workgroup.  The dispatcher hands workgroup i to XCD
+// i % 8; renumbering makes each XCD own a contiguous run of logical tiles,
+// and the grouped raster (group_m tile-rows per group, column-major inside
+// a group) makes the tiles that run together on one XCD share A and B
+// panels in that XCD's L2.
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_m, int& tm, int& tn) {
+  const int nwg = (int)gridDim.x;
+  int wg = (int)blockIdx.x;
+  const int per = nwg >> 3, rem = nwg & 7, xcd = wg & 7;
+  wg = xcd * per + (xcd < rem ? xcd : rem) + (wg >> 3);
+  const int width = group_m * tiles_n;
+  const int group = wg / width;
+  const int first_m = group * group_m;
+  const int gm = (tiles_m - first_m) < group_m ? (tiles_m - first_m) : group_m;
+  const int in_group = wg - group * width;
+  tm = first_m + in_group % gm;
+  tn = in_group / gm;
+}
+
+// XOR swizzle of 16-byte chunks inside one K row of an MN-contiguous panel
+// (row = one K index, ROWB/16 chunks).  Rows k..k+3 read together by one
+// ds_read_b64_tr_b16 group land 32 bytes apart, so the 4x32-byte read of a
+// 16-lane group covers 128 distinct bytes.
+template <int ROWB>
+__device__ __forceinline__ int mn_swz(int k) {
+  return (2 * (k & 3)) & (ROWB / 16 - 1);
+}
+
+// LDS-direct loader of one [BK][W] MN-contiguous panel (W = BM or BN):
+// the panel is CH = BK*W*2/1024 chunks of 1 KiB; one wave instruction fills
+// one chunk, lane l writing bytes [16l, 16l+16).  The lane fetches the
+// global 16 bytes that the swizzle maps to that LDS position.
+template <int BK, int W, int WAVES>
+struct PanelLoader {
+  static constexpr int ROWB = W * 2;
+  static constexpr int CH = BK * W * 2 / 1024;
+  static constexpr int PER_WAVE = (CH + WAVES - 1) / WAVES;
+  static constexpr int LANES_PER_ROW = W / 8;  // 16-byte slots per K row
+  static constexpr int ROWS_PER_CH = 1024 / ROWB;
+  static constexpr bool EVEN = CH % WAVES == 0;  // every wave issues PER_WAVE loads
+  static_assert(CH >= 1, "panel smaller than one wave load");
+  static_assert(ROWB <= 1024, "panel row wider than one wave load");
+  uint32_t voff[PER_WAVE];  // per-lane byte offset at K tile 0
+  int lds_off[PER_WAVE];    // wave-uniform LDS byte offset of the chunk
+  bool active[PER_WAVE];
+
+  __device__ __forceinline__ void init(int wave, int lane, int col0, int ld) {
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int c = wave + j * WAVES;
+      active[j] = c < CH;
+      const int row = c * ROWS_PER_CH + lane / LANES_PER_ROW;
+      const int slot = lane % LANES_PER_ROW;
+      const int q = slot ^ mn_swz<ROWB>(row);
+      voff[j] = ((uint32_t)row * (uint32_t)ld + (uint32_t)(col0 + 8 * q)) * 2u;
+      lds_off[j] = c * 1024;
+    }
+  }
+  // Issue the loads of K tile `kt` into the panel at LDS byte `base`.
+  __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, char* smem, int base, uint32_t kstep_bytes,
+                                        int kt) const {
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      if (EVEN || active[j]) {
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (MI_LDS void*)(smem + base + lds_off[j]), 16,
+                                                 voff[j] + (uint32_t)kt * kstep_bytes, 0, 0, 0);
+      }
+    }
+  }
+};
+
+// Per-lane LDS byte offsets of the MFMA operand fragments read with
+// ds_read_b64_tr_b16 from an MN-contiguous [BK][W] panel.  For fragment t
+// (32 columns starting at w0 + 32t) and K sub-step kk, half h, the address
+// is panel + (kk*16 + 4h) * ROWB + off[t].
+template <int W, int T>
+struct TrFrag {
+  static constexpr int ROWB = W * 2;
+  int off[T];
+  __device__ __forceinline__ void init(int lane, int w0) {
+    const int g = lane >> 4, i = lane & 15, r = i >> 2, c = i & 3;
+    const int krow = 8 * (g >> 1) + r;  // K row inside the 16-row sub-step
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const int col = w0 + 32 * t + 16 * (g & 1) + 4 * c;
+      off[t] = krow * ROWB + 16 * ((col >> 3) ^ mn_swz<ROWB>(krow)) + (col & 7) * 2;
+    }
+  }
+};
+
+__device__ __forceinline__ bf16x8_t read_tr_frag(const char* smem, int addr0, int addr1) {
+  const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((MI_LDS s16x4_t*)(smem + addr0));
+  const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((MI_LDS s16x4_t*)(smem + addr1));
+  typedef short s16x8_t __attribute__((ext_vector_type(8)));
+  const s16x8_t v = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const f32x2_t v = {a, b};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
+}
+
+__device__ __forceinline__ float bf16lo(uint32_t w) { return __builtin_bit_cast(float, w << 16); }
+__device__ __forceinline__ float bf16hi(uint32_t w) { return __builtin_bit_cast(float, w & 0xFFFF0000u); }
+
+// Epilogue: each wave stages one 32-row slice of its accumulator block as
+// bf16 in LDS (row stride WTN*2+16 bytes), reads it back as 16-byte row
+// chunks and stores whole rows.  `scale[mt]` multiplies every value of the
+// lane's output row in slice mt (1/rms for the fused kernel, 1 otherwise).
+template <int TM, int TN, int WAVES>
+__device__ __forceinline__ void store_tile(f32x16_t (&acc)[TM][TN], const float (&scale)[TM], char* smem, int wave,
+                                           int lane, uint16_t* __restrict__ out, int M, int N, int row0, int col0) {
+  constexpr int WTN = TN * 32;
+  constexpr int SROW = WTN * 2 + 16;
+  constexpr int CPR = WTN / 8;       // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;      // rows per read instruction
+  char* ep = smem + wave * (32 * SROW);
+#pragma unroll
+  for (int mt = 0; mt < TM; ++mt) {
+    const float s = scale[mt];
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int nl = nt * 32 + 8 * j + 4 * (lane >> 5);
+        const int ml = lane & 31;
+        u32x2_t v;
+        v.x = pack_bf16x2(acc[mt][nt][4 * j + 0] * s, acc[mt][nt][4 * j + 1] * s);
+        v.y = pack_bf16x2(acc[mt][nt][4 * j + 2] * s, acc[mt][nt][4 * j + 3] * s);
+        *(MI_LDS u32x2_t*)((MI_LDS char*)ep + ml * SROW + nl * 2) = v;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 32 / RPI; ++it) {
+      const int rl = it * RPI + lane / CPR;
+      const int cl = lane % CPR;
+      const u32x4_t v = *(MI_LDS u32x4_t*)((MI_LDS char*)ep + rl * SROW + cl * 16);
+      const int m = row0 + mt * 32 + rl;
+      const int n = col0 + cl * 8;
+      if (m < M && n < N) *(u32x4_t*)(out + (size_t)m * N + n) = v;
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// out[M,N] = lhsT[K,M]^T . rhs[K,N]
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+struct MatmulCfg {
+  using G = WaveGrid<BM, BN, WAVES>;
+  static constexpr int A_BYTES = BK * BM * 2;
+  static constexpr int B_BYTES = BK * BN * 2;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int EPI_BYTES = WAVES * 32 * (G::WTN * 2 + 16);
+  static constexpr int MAIN_BYTES = STAGES * STAGE_BYTES;
+  static constexpr int LDS_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
+};
+
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+__global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_kernel(const uint16_t* __restrict__ lhsT,
+                                                                     const uint16_t* __restrict__ rhs,
+                                                                     uint16_t* __restrict__ out, int M, int N,
+                                                                     int K, int group_m) {
+  using C = MatmulCfg<BM, BN, BK, WAVES, STAGES>;
+  using G = typename C::G;
+  static_assert(G::ok, "illegal wave grid");
+  static_assert(BK % 16 == 0, "BK must be a multiple of 16");
+  constexpr int TM = G::TM, TN = G::TN;
+  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tmi, tni;
+  tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+  const int wm0 = (wave / G::WN) * G::WTM;
+  const int wn0 = (wave % G::WN) * G::WTN;
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(lhsT, (uint32_t)K * (uint32_t)M * 2u);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(rhs, (uint32_t)K * (uint32_t)N * 2u);
+
+  PanelLoader<BK, BM, WAVES> la;
+  PanelLoader<BK, BN, WAVES> lb;
+  la.init(wave, lane, m0, M);
+  lb.init(wave, lane, n0, N);
+  const uint32_t kstep_a = (uint32_t)BK * (uint32_t)M * 2u;
+  const uint32_t kstep_b = (uint32_t)BK * (uint32_t)N * 2u;
+
+  TrFrag<BM, TM> fa;
+  TrFrag<BN, TN> fb;
+  fa.init(lane, wm0);
+  fb.init(lane, wn0);
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
+
+  auto compute = [&](int stage) {
+    const int abase = stage * C::STAGE_BYTES;
+    const int bbase = abase + C::A_BYTES;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      bf16x8_t af[TM], bf[TN];
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        af[t] = read_tr_frag(smem, abase + (kk * 16) * (BM * 2) + fa.off[t],
+                             abase + (kk * 16 + 4) * (BM * 2) + fa.off[t]);
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        bf[t] = read_tr_frag(smem, bbase + (kk * 16) * (BN * 2) + fb.off[t],
+                             bbase + (kk * 16 + 4) * (BN * 2) + fb.off[t]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  const int KT = (K + BK - 1) / BK;
+  if constexpr (STAGES == 1) {
+    for (int t = 0; t < KT; ++t) {
+      la.issue(ra, smem, 0, kstep_a, t);
+      lb.issue(rb, smem, C::A_BYTES, kstep_b, t);
+      wait_vmem();
+      __syncthreads();
+      compute(0);
+      __syncthreads();
+    }
+  } else {
+    la.issue(ra, smem, 0, kstep_a, 0);
+    lb.issue(rb, smem, C::A_BYTES, kstep_b, 0);
+    wait_vmem();
+    __syncthreads();
+    for (int t = 0; t < KT; ++t) {
+      const int cur = t & 1;
+      if (t + 1 < KT) {
+        const int nb = (cur ^ 1) * C::STAGE_BYTES;
+        la.issue(ra, smem, nb, kstep_a, t + 1);
+        lb.issue(rb, smem, nb + C::A_BYTES, kstep_b, t + 1);
+      }
+      compute(cur);
+      wait_vmem();
+      __syncthreads();
+    }
+  }
+
+  float one[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) one[i] = 1.0f;
+  store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
+}
+
+// ---------------------------------------------------------------------------
+// Fused out[M,N] = (x[M,K] * rsqrt(mean_k x^2 + eps) * gamma[K]) . W[K,N]
+// ---------------------------------------------------------------------------
+
+// Sum of v over the KC consecutive lanes that share one x row (KC = 4, 8 or
+// 16), broadcast to all of them: a DPP butterfly inside the wavefront.
+template <int KC>
+__device__ __forceinline__ float row_allreduce(float v) {
+  static_assert(KC == 4 || KC == 8 || KC == 16, "row lanes");
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+  if constexpr (KC >= 8)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x141, 0xF, 0xF, false));
+  if constexpr (KC >= 16)
+    v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x140, 0xF, 0xF, false));
+  return v;
+}
+
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+struct RmsCfg {
+  using G = WaveGrid<BM, BN, WAVES>;
+  static constexpr int NT = WAVES * 64;
+  static constexpr int KC = BK / 8;                 // 16-byte chunks per x row per K tile
+  static constexpr int CHUNKS = BM * KC;
+  static constexpr int CPT = (CHUNKS + NT - 1) / NT;  // chunks per thread
+  static constexpr int XD = (128 / BK) > 0 ? (128 / BK) : 1;
+  static constexpr int A_BYTES = BM * BK * 2;       // x panel [BM][BK], K contiguous
+  static constexpr int B_BYTES = BK * BN * 2;       // W panel [BK][BN], N contiguous
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int MAIN_BYTES = STAGES * STAGE_BYTES;
+  static constexpr int EPI_BYTES = WAVES * 32 * (G::WTN * 2 + 16);
+  static constexpr int RMS_OFF = ((MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES) + 15) / 16 * 16;
+  static constexpr int LDS_BYTES = RMS_OFF + BM * 4;
+  static_assert(NT % KC == 0, "row lanes must not straddle threads");
+};
+
+// Swizzle of the 16-byte K chunks of one x row in the K-contiguous panel:
+// the 16 lanes of one ds_read_b128 phase (16 rows, same K chunk) hit 16
+// different 16-byte bank groups.
+template <int BK>
+__device__ __forceinline__ int k_swz(int row) {
+  constexpr int XD = (128 / BK) > 0 ? (128 / BK) : 1;
+  return (row / XD) & (BK / 8 - 1);
+}
+
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool PRE>
+__global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ w,
+    uint16_t* __restrict__ out, int M, int N, int K, float inv_k, float eps, int group_m) {
+  using C = RmsCfg<BM, BN, BK, WAVES, STAGES>;
+  using G = typename C::G;
+  static_assert(G::ok, "illegal wave grid");
+  static_assert(BK % 16 == 0, "BK must be a multiple of 16");
+  constexpr int TM = G::TM, TN = G::TN, KC = C::KC, CPT = C::CPT, NT = C::NT;
+  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+  float* rms_lds = (float*)(smem + C::RMS_OFF);
+
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tmi, tni;
+  tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+  const int wm0 = (wave / G::WN) * G::WTM;
+  const int wn0 = (wave % G::WN) * G::WTN;
+  const bool has_gamma = gamma != nullptr;
+
+  const uint32_t x_bytes = (uint32_t)M * (uint32_t)K * 2u;
+  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, x_bytes);
+  const __amdgpu_buffer_rsrc_t rg = make_rsrc(has_gamma ? (const void*)gamma : (const void*)x, (uint32_t)K * 2u);
+  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)K * (uint32_t)N * 2u);
+
+  // x chunks of this thread: chunk c = i*NT + tid -> row c/KC, K chunk tid%KC.
+  const int kc = tid % KC;
+  int xrow[CPT];
+  bool xact[CPT];
+  uint32_t xoff[CPT];
+  int xlds[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int c = i * NT + tid;
+    xact[i] = c < C::CHUNKS;
+    xrow[i] = c / KC;
+    xoff[i] = ((uint32_t)(m0 + xrow[i]) * (uint32_t)K + (uint32_t)(8 * kc)) * 2u;
+    xlds[i] = xrow[i] * (BK * 2) + 16 * (kc ^ k_swz<BK>(xrow[i]));
+  }
+  auto load_x = [&](int kt, u32x4_t (&raw)[CPT], u32x4_t& g) {
+    const int k = kt * BK + 8 * kc;
+    const bool kin = k < K;
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const uint32_t off = kin ? xoff[i] + (uint32_t)kt * (uint32_t)(BK * 2) : x_bytes;
+      raw[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+    }
+    if (has_gamma) g = __builtin_amdgcn_raw_buffer_load_b128(rg, kin ? (uint32_t)k * 2u : (uint32_t)K * 2u, 0, 0);
+  };
+
+  PanelLoader<BK, BN, WAVES> lb;
+  lb.init(wave, lane, n0, N);
+  const uint32_t kstep_b = (uint32_t)BK * (uint32_t)N * 2u;
+  TrFrag<BN, TN> fb;
+  fb.init(lane, wn0);
+
+  // A fragments: ds_read_b128 of 8 consecutive K of row wm0 + 32*mt + lane%32.
+  const int xsl = ((lane & 31) / C::XD) & (KC - 1);
+  const int arow = (wm0 + (lane & 31)) * (BK * 2);
+  int akoff[BK / 16];
+#pragma unroll
+  for (int kk = 0; kk < BK / 16; ++kk) akoff[kk] = 16 * ((2 * kk + (lane >> 5)) ^ xsl);
+
+  float ss[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) ss[i] = 0.0f;
+  const int KT = (K + BK - 1) / BK;
+
+  float rs[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) rs[i] = 1.0f;
+  if constexpr (PRE) {
+    // Prologue: full-K sum of squares of this block's rows, 1/rms to LDS.
+    for (int kt = 0; kt < KT; ++kt) {
+      u32x4_t raw[CPT], g;
+      load_x(kt, raw, g);
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float lo = bf16lo(raw[i][e]), hi = bf16hi(raw[i][e]);
+          ss[i] = __builtin_fmaf(lo, lo, ss[i]);
+          ss[i] = __builtin_fmaf(hi, hi, ss[i]);
+        }
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const float t = row_allreduce<KC>(ss[i]);
+      if (xact[i] && kc == 0) rms_lds[xrow[i]] = 1.0f / __builtin_sqrtf(t * inv_k + eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) rs[i] = xact[i] ? rms_lds[xrow[i]] : 0.0f;
+  }
+
+  // Scale the raw x chunks (gamma, and 1/rms in the prologue variant),
+  // accumulate the sum of squares (epilogue variant) and write them to LDS.
+  auto stage_x = [&](const u32x4_t (&raw)[CPT], const u32x4_t& g, int abase) {
+    float gv[8];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      gv[2 * e] = has_gamma ? bf16lo(g[e]) : 1.0f;
+      gv[2 * e + 1] = has_gamma ? bf16hi(g[e]) : 1.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      if (!xact[i]) continue;
+      u32x4_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = bf16lo(raw[i][e]), hi = bf16hi(raw[i][e]);
+        if constexpr (!PRE) {
+          ss[i] = __builtin_fmaf(lo, lo, ss[i]);
+          ss[i] = __builtin_fmaf(hi, hi, ss[i]);
+        }
+        o[e] = pack_bf16x2(lo * gv[2 * e] * rs[i], hi * gv[2 * e + 1] * rs[i]);
+      }
+      *(MI_LDS u32x4_t*)((MI_LDS char*)smem + abase + xlds[i]) = o;
+    }
+  };
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
+
+  auto compute = [&](int stage) {
+    const int abase = stage * C::STAGE_BYTES;
+    const int bbase = abase + C::A_BYTES;
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      bf16x8_t af[TM], bf[TN];
+#pragma unroll
+      for (int t = 0; t < TM; ++t)
+        af[t] = __builtin_bit_cast(
+            bf16x8_t, *(MI_LDS u32x4_t*)((MI_LDS char*)smem + abase + arow + t * 32 * (BK * 2) + akoff[kk]));
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+        bf[t] = read_tr_frag(smem, bbase + (kk * 16) * (BN * 2) + fb.off[t],
+                             bbase + (kk * 16 + 4) * (BN * 2) + fb.off[t]);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[j], af[i], acc[i][j], 0, 0, 0);
+    }
+  };
+
+  if constexpr (STAGES == 1) {
+    for (int t = 0; t < KT; ++t) {
+      u32x4_t raw[CPT], g;
+      lb.issue(rw, smem, C::A_BYTES, kstep_b, t);
+      load_x(t, raw, g);
+      stage_x(raw, g, 0);
+      wait_vmem();
+      __syncthreads();
+      compute(0);
+      __syncthreads();
+    }
+  } else {
+    {
+      u32x4_t raw[CPT], g;
+      lb.issue(rw, smem, C::A_BYTES, kstep_b, 0);
+      load_x(0, raw, g);
+      stage_x(raw, g, 0);
+      wait_vmem();
+      __syncthreads();
+    }
+    for (int t = 0; t < KT; ++t) {
+      const int cur = t & 1;
+      const bool more = t + 1 < KT;
+      u32x4_t raw[CPT], g;
+      if (more) {
+        const int nb = (cur ^ 1) * C::STAGE_BYTES;
+        lb.issue(rw, smem, nb + C::A_BYTES, kstep_b, t + 1);
+        load_x(t + 1, raw, g);
+      }
+      compute(cur);
+      if (more) stage_x(raw, g, (cur ^ 1) * C::STAGE_BYTES);
+      wait_vmem();
+      __syncthreads();
+    }
+  }
+
+  float scale[TM];
+  if constexpr (!PRE) {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const float t = row_allreduce<KC>(ss[i]);
+      if (xact[i] && kc == 0) rms_lds[xrow[i]] = 1.0f / __builtin_sqrtf(t * inv_k + eps);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < TM; ++mt) scale[mt] = rms_lds[wm0 + mt * 32 + (lane & 31)];
+  } else {
+#pragma unroll
+    for (int mt = 0; mt < TM; ++mt) scale[mt] = 1.0f;
+  }
+  store_tile<TM, TN, WAVES>(acc, scale, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
+}
+
+}  // namespace mi

@@ -1,0 +1,98 @@
+// mi_registry.hpp -- table of compiled kernel instances and their launchers.
+//
+// Every tile config in the search space is a template instance compiled
+// ahead of time into libmi_kernels.so; each translation unit contributes a
+// table of MiEntry rows.  The C ABI (mi_capi.hip) looks a config up in the
+// merged table, checks its static legality and calls its launcher.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mi_kernels.h"
+#include "mi_gemm.hpp"
+
+namespace mi {
+
+struct MiArgs {
+  const void* a;      // lhsT / x
+  const void* b;      // rhs / W
+  const void* g;      // gamma (fused kernel, may be null)
+  void* out;
+  int M, N, K;
+  float eps, inv_k;
+  int group_m;
+};
+
+typedef hipError_t (*LaunchFn)(const MiArgs&, hipStream_t);
+
+struct MiEntry {
+  int kernel_id;
+  mi_tile_cfg cfg;
+  int lds_bytes;  // static LDS of the instance
+  LaunchFn launch;
+};
+
+inline int grid_tiles(int M, int N, int BM, int BN) { return ((M + BM - 1) / BM) * ((N + BN - 1) / BN); }
+
+template <int BM, int BN, int BK, int W, int S>
+hipError_t launch_mm_bf16(const MiArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((mm_lhsT_rhs_bf16_kernel<BM, BN, BK, W, S>), dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64),
+                     0, s, (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int W, int S, bool PRE>
+hipError_t launch_rms_bf16(const MiArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((rmsnorm_mm_bf16_kernel<BM, BN, BK, W, S, PRE>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                     dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
+                     (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
+  return hipGetLastError();
+}
+
+// Explicit instantiation of one config's kernel (namespace scope); every
+// table row needs its kernel instantiated in the same translation unit so
+// the host launch stub is emitted there.
+#define MI_MM_INST(BM, BN, BK, W, S)                                                                      \
+  template __global__ void mm_lhsT_rhs_bf16_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*, \
+                                                                      uint16_t*, int, int, int, int);
+#define MI_RMS_INST(BM, BN, BK, W, S, PRE)                                                                   \
+  template __global__ void rmsnorm_mm_bf16_kernel<BM, BN, BK, W, S, (PRE != 0)>(                            \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
+
+// Table rows; a config whose wave grid is illegal gets no instance.
+#define MI_MM_ROW(BM, BN, BK, W, S)                                                                  \
+  {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 0}, MatmulCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_mm_bf16<BM, BN, BK, W, S>},
+#define MI_RMS_ROW(BM, BN, BK, W, S, PRE)                                                            \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, PRE}, RmsCfg<BM, BN, BK, W, S>::LDS_BYTES,   \
+   &launch_rms_bf16<BM, BN, BK, W, S, (PRE != 0)>},
+
+// The BASELINE grid for one (BM, BN): BK in {32,64} x waves in {4,8} x
+// stages in {1,2}.  X is a row macro taking (BM, BN, BK, W, S, ...).
+#define MI_GRID_BK_W_S(X, BM, BN, ...) \
+  X(BM, BN, 32, 4, 1 __VA_ARGS__)      \
+  X(BM, BN, 32, 4, 2 __VA_ARGS__)      \
+  X(BM, BN, 64, 4, 1 __VA_ARGS__)      \
+  X(BM, BN, 64, 4, 2 __VA_ARGS__)      \
+  X(BM, BN, 32, 8, 1 __VA_ARGS__)      \
+  X(BM, BN, 32, 8, 2 __VA_ARGS__)      \
+  X(BM, BN, 64, 8, 1 __VA_ARGS__)      \
+  X(BM, BN, 64, 8, 2 __VA_ARGS__)
+#define MI_GRID_BK_W4_S(X, BM, BN, ...) \
+  X(BM, BN, 32, 4, 1 __VA_ARGS__)       \
+  X(BM, BN, 32, 4, 2 __VA_ARGS__)       \
+  X(BM, BN, 64, 4, 1 __VA_ARGS__)       \
+  X(BM, BN, 64, 4, 2 __VA_ARGS__)
+
+// Per-translation-unit tables (defined in mm_bf16_*.hip, rms_bf16_*.hip,
+// mm_f32.hip).
+const MiEntry* table_mm_bm32(int* n);
+const MiEntry* table_mm_bm64(int* n);
+const MiEntry* table_mm_bm128(int* n);
+const MiEntry* table_mm_bm256(int* n);
+const MiEntry* table_rms_bm64(int* n);
+const MiEntry* table_rms_bm128(int* n);
+const MiEntry* table_rms_bm256(int* n);
+const MiEntry* table_f32(int* n);
+
+}  // namespace mi

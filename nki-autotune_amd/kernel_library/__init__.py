@@ -1,0 +1,40 @@
+"""MI355X (gfx950) kernel_library: hand-written HIP kernels behind a C ABI.
+
+Public kernels (torch device tensors in, torch device tensor out):
+
+* :func:`matmul_lhsT_rhs` -- ``lhs_T[K,M].T @ rhs[K,N]``, bf16 or fp32
+* :func:`rmsnorm_matmul` -- ``rmsnorm(lhs) * gamma @ rhs``, bf16
+
+plus the reference names ``matmul_lhsT_rhs_nkigym`` and
+``rmsnorm_matmul_online``, and the tile search space (:class:`TileConfig`).
+"""
+
+from kernel_library.config import (
+    TileConfig,
+    baseline_grid,
+    check,
+    compiled_configs,
+    default_config,
+    legal_configs,
+)
+from kernel_library.ops import (
+    EPS,
+    matmul_lhsT_rhs,
+    matmul_lhsT_rhs_nkigym,
+    rmsnorm_matmul,
+    rmsnorm_matmul_online,
+)
+
+__all__ = [
+    "EPS",
+    "TileConfig",
+    "baseline_grid",
+    "check",
+    "compiled_configs",
+    "default_config",
+    "legal_configs",
+    "matmul_lhsT_rhs",
+    "matmul_lhsT_rhs_nkigym",
+    "rmsnorm_matmul",
+    "rmsnorm_matmul_online",
+]

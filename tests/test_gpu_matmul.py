@@ -1,0 +1,152 @@
+"""GPU parity of matmul_lhsT_rhs (bf16 and fp32) against the CPU oracle.
+
+Every call goes through the C ABI of libmi_kernels.so (kernel_library.ops
+wraps mi_matmul_lhsT_rhs_*).  Small shapes compare the whole output with the
+oracle's float64 closed form; the full BASELINE sizes use sampled rows
+against the closed form plus size-independent properties (all tile configs
+bitwise equal, exact linearity under power-of-two scaling).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import BF16_MATMUL_MAX_REL, F32_ATOL, F32_RTOL, mm_inputs
+from oracle import matmul as omm
+from oracle import metrics
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a: np.ndarray, dtype, device):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dtype).to(device)
+
+
+def _host(t) -> np.ndarray:
+    import torch
+
+    return t.to(torch.float32).cpu().numpy()
+
+
+def _kl():
+    import kernel_library
+
+    return kernel_library
+
+
+def test_c1_fp32_matches_closed_form(gpu):
+    """lhsT[512,256] . rhs[512,512], fp32 N(0,1), seed 0."""
+    import torch
+
+    d = mm_inputs(512, 256, 512, seed=0, dist="normal", dtype="float32")
+    out = _kl().matmul_lhsT_rhs(_dev(d["lhs_T"], torch.float32, gpu), _dev(d["rhs"], torch.float32, gpu))
+    expected = omm.closed_form(d["lhs_T"], d["rhs"])
+    rep = metrics.report(_host(out), expected)
+    print("c1", rep)
+    np.testing.assert_allclose(_host(out), expected, atol=F32_ATOL, rtol=F32_RTOL)
+    assert rep["max_rel"] <= F32_RTOL
+
+
+def test_128cube_fp32_reference_procedure(gpu):
+    """test/ops/test_direct_numpy_call.py:32-38: seed 0, 128^3, atol=rtol=1e-4."""
+    import torch
+
+    rng = np.random.default_rng(0)
+    lhs_T = rng.standard_normal((128, 128)).astype(np.float32)
+    rhs = rng.standard_normal((128, 128)).astype(np.float32)
+    out = _kl().matmul_lhsT_rhs(_dev(lhs_T, torch.float32, gpu), _dev(rhs, torch.float32, gpu))
+    np.testing.assert_allclose(_host(out), lhs_T.T @ rhs, atol=1e-4, rtol=1e-4)
+
+
+def test_bf16_every_config_small_fixture(gpu):
+    """The reference's small fixture shape (K=256, M=256, N=512), every compiled config."""
+    import torch
+
+    kl = _kl()
+    d = mm_inputs(256, 256, 512, seed=0)
+    a, b = _dev(d["lhs_T"], torch.bfloat16, gpu), _dev(d["rhs"], torch.bfloat16, gpu)
+    expected = omm.closed_form(d["lhs_T"], d["rhs"])
+    first = None
+    for cfg in kl.legal_configs("matmul_lhsT_rhs", 256, 512, 256):
+        out = kl.matmul_lhsT_rhs(a, b, cfg=cfg)
+        torch.cuda.synchronize()
+        rep = metrics.report(_host(out), expected)
+        assert rep["max_rel"] <= BF16_MATMUL_MAX_REL, (cfg, rep)
+        bits = out.view(torch.int16).cpu().numpy()
+        if first is None:
+            first = (cfg, bits)
+        else:
+            # Same K order in every config (ascending, 16 per MFMA): bitwise equal.
+            assert np.array_equal(bits, first[1]), (cfg, first[0])
+
+
+@pytest.mark.parametrize("M,N,K", [(264, 520, 100), (8, 8, 7), (40, 136, 33), (16, 1024, 512), (128, 96, 1000)])
+def test_bf16_ragged_shapes(gpu, M, N, K):
+    """Edge tiles in M, N and K (K not a multiple of block_k): masked stores, zero-filled K tail."""
+    import torch
+
+    kl = _kl()
+    d = mm_inputs(K, M, N, seed=3)
+    a, b = _dev(d["lhs_T"], torch.bfloat16, gpu), _dev(d["rhs"], torch.bfloat16, gpu)
+    expected = omm.closed_form(d["lhs_T"], d["rhs"])
+    cfgs = kl.legal_configs("matmul_lhsT_rhs", M, N, K)
+    assert cfgs
+    for cfg in cfgs[:: max(1, len(cfgs) // 12)]:
+        out = kl.matmul_lhsT_rhs(a, b, cfg=cfg)
+        rep = metrics.report(_host(out), expected)
+        assert rep["max_rel"] <= BF16_MATMUL_MAX_REL, (M, N, K, cfg, rep)
+
+
+def test_bf16_identity_and_brute_force(gpu):
+    """lhs_T = I gives rhs exactly; a tiny case against the brute-force loop."""
+    import torch
+
+    kl = _kl()
+    K = 64
+    rhs = mm_inputs(K, 8, 96, seed=5)["rhs"]
+    out = kl.matmul_lhsT_rhs(_dev(np.eye(K, dtype=np.float32), torch.bfloat16, gpu), _dev(rhs, torch.bfloat16, gpu))
+    assert np.array_equal(_host(out), rhs)
+    d = mm_inputs(24, 16, 32, seed=6)
+    out = kl.matmul_lhsT_rhs(_dev(d["lhs_T"], torch.bfloat16, gpu), _dev(d["rhs"], torch.bfloat16, gpu))
+    rep = metrics.report(_host(out), omm.brute_force(d["lhs_T"], d["rhs"]))
+    assert rep["max_rel"] <= BF16_MATMUL_MAX_REL
+
+
+def _sampled_check(out_host: np.ndarray, lhs_T: np.ndarray, rhs: np.ndarray, rows: np.ndarray) -> dict:
+    exp = omm.closed_form(lhs_T[:, rows], rhs)
+    return metrics.report(out_host[rows], exp)
+
+
+@pytest.mark.parametrize(
+    "M,N,K,dist",
+    [
+        (8192, 8192, 8192, "uniform"),  # C2
+        (2048, 1024, 8192, "uniform"),  # C4a
+        (4096, 14336, 1024, "uniform"),  # C4b
+        (1024, 4096, 14336, "uniform"),  # C4c
+        (16, 28672, 8192, ("normal", 0.02)),  # C5
+        (64, 28672, 8192, ("normal", 0.02)),
+        (128, 28672, 8192, ("normal", 0.02)),
+    ],
+)
+def test_bf16_baseline_shapes(gpu, M, N, K, dist):
+    """BASELINE shapes with the default (tuned) config: sampled rows vs the closed form, exact 2x linearity."""
+    import torch
+
+    kl = _kl()
+    print(f"shape M={M} N={N} K={K}", flush=True)
+    d = mm_inputs(K, M, N, seed=0, dist=dist)
+    a, b = _dev(d["lhs_T"], torch.bfloat16, gpu), _dev(d["rhs"], torch.bfloat16, gpu)
+    out = kl.matmul_lhsT_rhs(a, b)
+    host = _host(out)
+    rng = np.random.default_rng(1)
+    rows = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, size=min(M, 24))]))
+    rep = _sampled_check(host, d["lhs_T"], d["rhs"], rows)
+    print(rep)
+    assert rep["max_rel"] <= BF16_MATMUL_MAX_REL
+    assert rep["nonfinite"] == 0
+    out2 = kl.matmul_lhsT_rhs(a, b * 2)
+    assert torch.equal(out2, out * 2)

@@ -1,0 +1,115 @@
+"""GPU parity of the fused rmsnorm_matmul kernel against the CPU oracle.
+
+Calls go through mi_rmsnorm_matmul_bf16 (C ABI).  The oracle is the
+two-pass closed form in float64 on the same bf16 inputs (reference
+kernel_library/rmsnorm_matmul/kernel_hand_online.py:5-8 plus the BASELINE
+gamma).  Tolerances are explained in tests/helpers.py.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import RMS_MAX_REL, RMS_NORMWISE, rms_inputs, rms_report
+from oracle import rmsnorm as orms
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, device):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).to(device)
+
+
+def _host(t) -> np.ndarray:
+    import torch
+
+    return t.to(torch.float32).cpu().numpy()
+
+
+def _ok(rep) -> bool:
+    return rep["max_rel"] <= RMS_MAX_REL and rep["normwise"] <= RMS_NORMWISE and rep["nonfinite"] == 0
+
+
+def test_every_config_small(gpu):
+    """M=256, K=512, N=256 with gamma: every compiled config and both variants."""
+    import kernel_library as kl
+
+    d = rms_inputs(256, 512, 256, seed=0)
+    x, g, w = _dev(d["lhs"], gpu), _dev(d["gamma"], gpu), _dev(d["rhs"], gpu)
+    expected = orms.closed_form(d["lhs"], d["rhs"], d["gamma"])
+    cfgs = kl.legal_configs("rmsnorm_matmul", 256, 256, 512)
+    assert len(cfgs) > 50
+    for cfg in cfgs:
+        out = kl.rmsnorm_matmul(x, w, g, cfg=cfg)
+        rep = rms_report(_host(out), expected)
+        assert _ok(rep), (cfg, rep)
+
+
+def test_no_gamma_is_reference_kernel(gpu):
+    """gamma=None is rmsnorm_matmul_online's contract (no weight, EPS=1e-6)."""
+    import kernel_library as kl
+
+    d = rms_inputs(128, 256, 192, seed=1, with_gamma=False)
+    out = kl.rmsnorm_matmul_online(_dev(d["lhs"], gpu), _dev(d["rhs"], gpu))
+    rep = rms_report(_host(out), orms.closed_form(d["lhs"], d["rhs"]))
+    assert _ok(rep), rep
+
+
+@pytest.mark.parametrize("variant", [0, 1])
+def test_ragged_and_special_rows(gpu, variant):
+    """Edge tiles (M, N not multiples of the block), K not a multiple of block_k; a zero row gives 0."""
+    import torch
+
+    import kernel_library as kl
+
+    M, K, N = 200, 264, 136
+    d = rms_inputs(M, K, N, seed=2)
+    x = d["lhs"].copy()
+    x[7] = 0.0           # zero row: out row is exactly 0 (0 * finite rsqrt(eps))
+    x[11] = 0.25         # constant row: normalises to 1 -> gamma @ W
+    cfgs = [c for c in kl.legal_configs("rmsnorm_matmul", M, N, K) if c.variant == variant]
+    for cfg in cfgs[:: max(1, len(cfgs) // 8)]:
+        out = kl.rmsnorm_matmul(_dev(x, gpu), _dev(d["rhs"], gpu), _dev(d["gamma"], gpu), cfg=cfg)
+        host = _host(out)
+        rep = rms_report(host, orms.closed_form(x, d["rhs"], d["gamma"]))
+        assert _ok(rep), (cfg, rep)
+        assert np.all(host[7] == 0.0)
+        torch.cuda.synchronize()
+
+
+def test_scale_invariance_and_identity_weight(gpu):
+    """f(c x) = f(x) for c = 4 (exact in bf16, eps negligible); W = I gives rmsnorm(x) * gamma."""
+    import kernel_library as kl
+
+    d = rms_inputs(64, 128, 128, seed=4)
+    x, g, w = _dev(d["lhs"], gpu), _dev(d["gamma"], gpu), _dev(d["rhs"], gpu)
+    a = _host(kl.rmsnorm_matmul(x, w, g))
+    b = _host(kl.rmsnorm_matmul(x * 4, w, g))
+    assert np.max(np.abs(a - b)) <= 1e-2 * np.sqrt(np.mean(a * a))
+    eye = _dev(np.eye(128, dtype=np.float32), gpu)
+    y = _host(kl.rmsnorm_matmul(x, eye, g))
+    ref = d["lhs"] * orms.inv_rms(d["lhs"])[:, None] * d["gamma"][None, :]
+    rep = rms_report(y, ref)
+    assert _ok(rep), rep
+
+
+def test_baseline_c3_full_size(gpu):
+    """BASELINE config 3 (M=K=N=4096, gamma, eps=1e-6), both variants: sampled rows vs closed form."""
+    import kernel_library as kl
+
+    print("C3 4096^3 rmsnorm_matmul", flush=True)
+    d = rms_inputs(4096, 4096, 4096, seed=0)
+    x, g, w = _dev(d["lhs"], gpu), _dev(d["gamma"], gpu), _dev(d["rhs"], gpu)
+    rng = np.random.default_rng(7)
+    rows = np.unique(np.concatenate([[0, 4095], rng.integers(0, 4096, size=24)]))
+    expected = orms.closed_form(d["lhs"][rows], d["rhs"], d["gamma"])
+    for variant in (0, 1):
+        cfg = kl.default_config("rmsnorm_matmul", 4096, 4096, 4096)
+        cfg = kl.TileConfig(**{**cfg.asdict(), "variant": variant})
+        out = _host(kl.rmsnorm_matmul(x, w, g, cfg=cfg))
+        rep = rms_report(out[rows], expected)
+        print(variant, rep)
+        assert _ok(rep), rep
