@@ -1,0 +1,260 @@
+"""Benchmark of the kernel_library hot path on one MI355X: prints ONE JSON line.
+
+Workload (the configuration the metric is quoted on): the square bf16
+``lhsT . rhs`` matmul at 8192^3, inputs U(-1,1) from seed 0 rounded to bf16,
+fp32 accumulation, bf16 output, with the tile config chosen by the autotune
+sweep (every legal prebuilt config, hipEvent-timed, fastest kept).  A step is
+one launch of that kernel on inputs resident in HBM.
+
+* ``value``: whole-job TFLOP/s = steps * 2*M*N*K / wall seconds of the timed
+  region (bracketed by device synchronisation).
+* ``roofline``: the same kernel's algorithmic FLOPs per launch over its
+  average launch duration from HIP events recorded on the launch stream
+  around the timed region, against MI355X's dense bf16 MFMA peak
+  (2.5 PFLOP/s).  ``traffic`` is the HBM bytes per launch measured with
+  rocprofv3 PMC counters (FETCH_SIZE + WRITE_SIZE, scaled by a copy-kernel
+  calibration) when that measurement for the same config is recorded in
+  ``profiles/traffic.json``; otherwise null.
+* ``fused``: the rmsnorm_matmul kernel at 4096^3 beside
+  the plain matmul at the same shape, each with its autotuned config.
+* ``cpu_baseline``: the CPU oracle's tile-faithful emulation of the
+  reference kernel's loop nest (fp32, numpy/BLAS) on a bounded column slice
+  of the same workload, rank 0 only.
+
+Flags: ``--gpus N`` (only 1 is supported: this build runs on one GPU),
+``--steps``, ``--warmup``, ``--no-tune`` (use the tuned-config table /
+library default), ``--only-kernel`` (skip the sweep, the fused pair and the
+CPU baseline: the command profiled under rocprofv3 PMC runs),
+``--calibrate-copy-mib N`` (run one device copy of N MiB first, the PMC
+scale reference), ``--cpu-seconds`` (CPU baseline budget).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "nki-autotune_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+M = N = K = 8192
+PEAK_BF16_TFLOPS = 2500.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse() -> argparse.Namespace:
+    ap = argparse.ArgumentParser(description="kernel_library hot-path benchmark (one MI355X)")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-tune", action="store_true")
+    ap.add_argument("--only-kernel", action="store_true")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--sweep-reps", type=int, default=20)
+    return ap.parse_args()
+
+
+def sweep(func_name: str, m: int, n: int, k: int, reps: int, no_tune: bool):
+    """Autotuned config of ``func_name`` at (m, n, k) (or the table/default one with ``no_tune``)."""
+    import kernel_library as kl
+    from autotune.tune import tune
+
+    if no_tune:
+        return kl.default_config(func_name, m, n, k), None
+    res = tune(func_name, m, n, k, check=True, warmup=max(3, reps // 4), reps=reps)
+    if res.best is None:
+        raise RuntimeError(f"autotune sweep found no working config for {func_name} {m}x{n}x{k}:\n{res.output}")
+    if res.check is not None and not res.check["pass"]:
+        raise RuntimeError(f"autotuned {func_name} config {res.best.name} fails numerics: {res.check}")
+    log(f"sweep {func_name} {m}x{n}x{k}: {len(res.output.successes)} configs, best {res.best.name} "
+        f"{res.best_time_s * 1e6:.1f} us; numerics {res.check}")
+    return res.best, res
+
+
+def time_pair(a, b, cfg, launch_fn, reps: int = 50) -> float:
+    import torch
+
+    from autotune.runner.benchmark import time_launches
+
+    times = time_launches(lambda: launch_fn(a, b, cfg), 5, reps)
+    torch.cuda.synchronize()
+    return sorted(times)[len(times) // 2]
+
+
+def fused_pair(reps: int, no_tune: bool) -> dict:
+    """rmsnorm_matmul vs plain matmul at 4096^3, each autotuned."""
+    import torch
+
+    import kernel_library as kl
+    from autotune.runner.benchmark import generate_tensors, upload
+    from autotune.tune import default_dists, input_specs
+
+    s = 4096
+    dev = torch.device("cuda:0")
+    cfg_r, _ = sweep("rmsnorm_matmul", s, s, s, reps, no_tune)
+    cfg_m, _ = sweep("matmul_lhsT_rhs", s, s, s, reps, no_tune)
+    spec_r = input_specs("rmsnorm_matmul", s, s, s)
+    r = upload(generate_tensors(spec_r, 0, default_dists("rmsnorm_matmul", s)), spec_r, dev)
+    spec_m = input_specs("matmul_lhsT_rhs", s, s, s)
+    mm = upload(generate_tensors(spec_m, 0, default_dists("matmul_lhsT_rhs", s)), spec_m, dev)
+    out_r = torch.empty((s, s), dtype=torch.bfloat16, device=dev)
+    out_m = torch.empty((s, s), dtype=torch.bfloat16, device=dev)
+    t_r = time_pair(r, None, cfg_r, lambda d, _b, c: kl.rmsnorm_matmul(d["lhs"], d["rhs"], d["gamma"], cfg=c,
+                                                                       out=out_r), 100)
+    t_m = time_pair(mm, None, cfg_m, lambda d, _b, c: kl.matmul_lhsT_rhs(d["lhs_T"], d["rhs"], cfg=c, out=out_m),
+                    100)
+    fl = 2.0 * s ** 3
+    return {
+        "shape": [s, s, s],
+        "rmsnorm_matmul_tflops": round(fl / t_r / 1e12, 1),
+        "rmsnorm_matmul_config": cfg_r.name,
+        "matmul_tflops": round(fl / t_m / 1e12, 1),
+        "matmul_config": cfg_m.name,
+        "fused_over_matmul_time": round(t_r / t_m, 4),
+    }
+
+
+def cpu_baseline(budget_s: float) -> dict:
+    """The oracle's tile-faithful emulation of the reference loop nest, timed on a bounded column slice."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+
+    from oracle import matmul as omm
+
+    rng = np.random.default_rng(0)
+    lhs_T = rng.uniform(-1.0, 1.0, (K, M)).astype(np.float32)
+    # Double the slice until one emulation run takes >= budget/4 (total CPU time ~ budget/2).
+    cols = 64
+    while True:
+        rhs = rng.uniform(-1.0, 1.0, (K, cols)).astype(np.float32)
+        t0 = time.perf_counter()
+        omm.tiled(lhs_T, rhs, out_dtype="float32")
+        dt = time.perf_counter() - t0
+        flops = 2.0 * M * cols * K
+        if dt >= budget_s / 4 or cols >= N:
+            break
+        cols = min(N, cols * 2)
+    threads = max([i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"] or [1])
+    return {
+        "value": round(flops / dt / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"oracle.matmul.tiled (fp32 tile-faithful emulation of kernel_hand_90.92mfu.py:101-131) on "
+                  f"lhsT[{K},{M}] x rhs[{K},{cols}] (a {cols}-column slice of the 8192^3 workload), "
+                  f"{dt:.2f} s, BLAS threads {threads}, host cpus {len(os.sched_getaffinity(0))}",
+    }
+
+
+def recorded_traffic(cfg_name: str):
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    entry = rec.get(f"matmul_lhsT_rhs:{M}x{N}x{K}:{cfg_name}")
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py runs on exactly one GPU: this build has no multi-GPU path (use --gpus 1)", file=sys.stderr)
+        return 2
+    import torch
+
+    import kernel_library as kl
+    from autotune.runner.benchmark import generate_tensors, upload
+    from autotune.tune import default_dists, input_specs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X (no HIP device visible)", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    if args.calibrate_copy_mib:
+        nb = args.calibrate_copy_mib << 20
+        src = torch.ones(nb // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"calibration copy of {args.calibrate_copy_mib} MiB done")
+        del src, dst
+
+    cfg, _ = sweep("matmul_lhsT_rhs", M, N, K, args.sweep_reps, args.no_tune or args.only_kernel)
+    specs = input_specs("matmul_lhsT_rhs", M, N, K)
+    d = upload(generate_tensors(specs, 0, default_dists("matmul_lhsT_rhs", K)), specs, dev)
+    a, b = d["lhs_T"], d["rhs"]
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+
+    def step():
+        kl.matmul_lhsT_rhs(a, b, cfg=cfg, out=out)
+
+    for _ in range(args.warmup):
+        step()
+    stream = torch.cuda.current_stream(dev)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_s = ev0.elapsed_time(ev1) * 1e-3 / args.steps
+    flop = 2.0 * M * N * K
+    value = flop * args.steps / wall / 1e12
+    achieved = flop / kern_s / 1e12
+    log(f"timed {args.steps} steps: wall {wall * 1e3:.1f} ms, {value:.1f} TFLOP/s; kernel avg {kern_s * 1e6:.1f} us")
+
+    line = {
+        "metric": "bf16 TFLOP/s + % MFMA peak, lhsT·rhs matmul 8192³ and rmsnorm_matmul, 1 GPU",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: lhsT, rhs ~ U(-1,1) seed 0 rounded to bf16, resident in HBM",
+        "config": {
+            "workload": "lhsT[8192,8192]·rhs[8192,8192] bf16 matmul, fp32 accumulate, bf16 out (BASELINE configs[1])",
+            "kernel": "mm_lhsT_rhs_bf16",
+            "tile_config": cfg.name,
+            "autotuned": not (args.no_tune or args.only_kernel),
+            "pct_mfma_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": recorded_traffic(cfg.name),
+        },
+    }
+    if not args.only_kernel:
+        line["fused"] = fused_pair(args.sweep_reps, args.no_tune)
+        log(f"fused pair: {line['fused']}")
+        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+    print(json.dumps(line, ensure_ascii=False), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

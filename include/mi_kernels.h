@@ -41,7 +41,8 @@ enum {
   MI_E_RANGE = 5,          /* an operand is 4 GiB or larger (32-bit buffer offsets)  */
   MI_E_ARGS = 6,           /* null pointer, non-positive size, bad eps               */
   MI_E_KERNEL = 7,         /* unknown kernel id                                      */
-  MI_E_SPLIT = 8           /* split_k unsupported for this kernel / shape            */
+  MI_E_SPLIT = 8,          /* split_k unsupported for this kernel / shape            */
+  MI_E_TILE = 9            /* block sizes outside the template's power-of-two range  */
 };
 
 /*

@@ -1,1 +1,1 @@
-"""Profiling backend (hipEvent timing) of the autotune loop."""
+"""Profiling backend of the autotune loop: hipcc / prebuilt instances, hipEvent timing, results.json."""

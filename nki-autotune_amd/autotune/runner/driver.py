@@ -1,0 +1,110 @@
+"""In-process compile + benchmark pipeline on one GPU.
+
+Control flow of reference autotune/src/autotune/runner/driver.py:126-165:
+reject a batch that mixes device counts, make a scratch work dir, detect the
+device, generate seeded inputs per job, submit every build to a pool, and
+benchmark each job sequentially on the one device as its build completes
+(``as_completed``).  Differences: builds are hipcc child processes (or a
+lookup in the prebuilt library), so the pool is a thread pool; and inputs
+are generated once per distinct (specs, distributions, seed) and shared by
+every job that asks for them -- a sweep of 72 configs at 8192^3 then draws
+its 2 x 64 Mi values once instead of 72 times (same values, since every job
+of the reference draws from the same seed).
+"""
+
+from __future__ import annotations
+
+import json
+import logging
+import os
+import shutil
+from concurrent.futures import ThreadPoolExecutor, as_completed
+from pathlib import Path
+from typing import Any
+
+from autotune.runner.benchmark import benchmark_one, generate_tensors, upload
+from autotune.runner.compile import canonical_name, compile_one, default_work_dir, parse_source, problem_shape
+from autotune.runner.detect import detect_gpus
+from autotune.runner.types import CompileResult, KernelJob, OutputSpec, ProfileResult, compile_failure_result
+
+logger = logging.getLogger(__name__)
+
+_OUTPUT_TENSOR_NAME = "out"
+
+
+def _inputs_key(job: KernelJob, seed: int) -> str:
+    return json.dumps([list(map(list, [(list(s), d) for s, d in job.input_specs.values()])),
+                       list(job.input_specs), repr(sorted((job.input_dists or {}).items())), seed])
+
+
+def run_pipeline(
+    kernels: dict[str, KernelJob],
+    seed: int,
+    collect_compiler_logs: bool,
+    collect_detailed_profile: bool,
+    warmup: int = 10,
+    reps: int = 50,
+    flush_bytes: int = 0,
+    allow_jit: bool = True,
+    work_dir: str | None = None,
+) -> tuple[list[ProfileResult], dict[str, str]]:
+    """Build + time every job on GPU 0; return (results, compiler_logs)."""
+    import torch
+
+    if not kernels:
+        return [], {}
+    lncs = {int(job.lnc) for job in kernels.values()}
+    if lncs != {1}:
+        raise RuntimeError(f"lnc values {sorted(lncs)} requested; every profile run uses exactly one GPU (lnc=1)")
+    first = next(iter(kernels.values()))
+    work = Path(work_dir or default_work_dir(first.func_name))
+    shutil.rmtree(work, ignore_errors=True)
+    work.mkdir(parents=True)
+
+    n_dev, arch, cus = detect_gpus()
+    logger.info("Driver ready: %d kernels, %d CPU, %d GPU (%s, %d CUs)", len(kernels), os.cpu_count() or 1, n_dev,
+                arch, cus)
+    device = torch.device("cuda:0")
+
+    host_cache: dict[str, dict[str, Any]] = {}
+    dev_inputs: dict[str, dict[str, Any]] = {}
+    meta: dict[str, tuple] = {}
+    for kname, job in kernels.items():
+        key = _inputs_key(job, seed)
+        if key not in dev_inputs:
+            host = generate_tensors(job.input_specs, seed, job.input_dists)
+            dev_inputs[key] = upload(host, job.input_specs, device)
+            host_cache[key] = host
+        meta[kname] = (key, problem_shape(job.func_name, job.input_specs))
+    host_cache.clear()
+
+    workers = min(max((os.cpu_count() or 2) - 1, 1), len(kernels), 16)
+    compile_results: list[CompileResult] = []
+    compile_errors: list[ProfileResult] = []
+    hw_results: list[ProfileResult] = []
+    with ThreadPoolExecutor(max_workers=workers) as pool:
+        futures = [
+            pool.submit(compile_one, kname, job.source, job.func_name, job.input_specs, str(work), job.hipcc_args,
+                        allow_jit)
+            for kname, job in kernels.items()
+        ]
+        for f in as_completed(futures):
+            cr = f.result()
+            compile_results.append(cr)
+            if cr.error:
+                compile_errors.append(compile_failure_result(cr))
+                continue
+            job = kernels[cr.kernel_name]
+            key, (M, N, K) = meta[cr.kernel_name]
+            _fam, cfg = parse_source(job.source)
+            out_dtype = next(iter(job.input_specs.values()))[1]
+            out = OutputSpec(_OUTPUT_TENSOR_NAME, tuple(job.output_shape), out_dtype)
+            if tuple(job.output_shape) != (M, N):
+                hw_results.append(ProfileResult(cr.kernel_name, f"output_shape {tuple(job.output_shape)} does not "
+                                                f"match the inputs' [M, N] = [{M}, {N}]"))
+                continue
+            hw_results.append(benchmark_one(cr.kernel_name, cr.library_path, canonical_name(job.func_name), cfg,
+                                            dev_inputs[key], out, M, N, K, warmup, reps, flush_bytes,
+                                            collect_detailed_profile))
+    logs = {cr.kernel_name: cr.compile_log for cr in compile_results if collect_compiler_logs and cr.compile_log}
+    return compile_errors + hw_results, logs

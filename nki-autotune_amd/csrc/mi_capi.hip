@@ -34,12 +34,11 @@ const std::vector<mi::MiEntry>& registry() {
   static std::vector<mi::MiEntry> all;
   static std::once_flag once;
   std::call_once(once, [] {
-    typedef const mi::MiEntry* (*TableFn)(int*);
-    const TableFn tables[] = {mi::table_mm_bm32,  mi::table_mm_bm64,  mi::table_mm_bm128, mi::table_mm_bm256,
-                              mi::table_rms_bm64, mi::table_rms_bm128, mi::table_rms_bm256, mi::table_f32};
-    for (TableFn f : tables) {
+    int ntables = 0;
+    const mi::TableFn* tables = mi::table_list(&ntables);
+    for (int i = 0; i < ntables; ++i) {
       int n = 0;
-      const mi::MiEntry* t = f(&n);
+      const mi::MiEntry* t = tables[i](&n);
       all.insert(all.end(), t, t + n);
     }
   });
@@ -69,6 +68,8 @@ bool wave_grid_ok(int bm, int bn, int waves) {
   return false;
 }
 
+bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1)) == 0; }
+
 constexpr unsigned long long kMaxOffset = 0xFFFFFFFFull;  // 32-bit buffer offsets
 constexpr int kLdsLimit = 160 * 1024;
 
@@ -81,6 +82,16 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
     return fail(MI_E_ARGS, "non-positive tile parameter");
   if (c.split_k != 1) return fail(MI_E_SPLIT, "split_k=%d unsupported (must be 1)", c.split_k);
   if (c.group_m < 0) return fail(MI_E_ARGS, "group_m=%d negative", c.group_m);
+  if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_F32) {
+    // LDS panels are copied in 1 KiB wave loads and XOR-swizzled in 16-byte
+    // chunks: block_m / block_n must be powers of two in [32, 512] and
+    // block_k a power of two in [16, 128] ([32, 128] for the fused kernel,
+    // whose x rows are reduced over BK/8 lanes).
+    const int kmin = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 ? 32 : 16;
+    if (!pow2_in(c.block_m, 32, 512) || !pow2_in(c.block_n, 32, 512) || !pow2_in(c.block_k, kmin, 128))
+      return fail(MI_E_TILE, "block sizes bm=%d bn=%d bk=%d outside the template range", c.block_m, c.block_n,
+                  c.block_k);
+  }
   if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_F32 && !wave_grid_ok(c.block_m, c.block_n, c.waves))
     return fail(MI_E_WAVE_TILE, "%d waves cannot tile a %dx%d block in 32x32 MFMA tiles", c.waves, c.block_m,
                 c.block_n);

@@ -111,6 +111,7 @@ struct PanelLoader {
   static constexpr int LANES_PER_ROW = W / 8;  // 16-byte slots per K row
   static constexpr int ROWS_PER_CH = 1024 / ROWB;
   static constexpr bool EVEN = CH % WAVES == 0;  // every wave issues PER_WAVE loads
+  static_assert(W >= 32 && (W & (W - 1)) == 0, "panel width must be a power of two >= 32");
   static_assert(CH >= 1, "panel smaller than one wave load");
   static_assert(ROWB <= 1024, "panel row wider than one wave load");
   uint32_t voff[PER_WAVE];  // per-lane byte offset at K tile 0

@@ -84,6 +84,13 @@ hipError_t launch_rms_bf16(const MiArgs& a, hipStream_t s) {
   X(BM, BN, 64, 4, 1 __VA_ARGS__)       \
   X(BM, BN, 64, 4, 2 __VA_ARGS__)
 
+typedef const MiEntry* (*TableFn)(int*);
+
+// The list of instance tables the C ABI serves.  libmi_kernels.so defines it
+// in mi_tables.hip (every prebuilt table); a just-in-time autotune library
+// defines it in its one generated translation unit (one instance).
+const TableFn* table_list(int* n);
+
 // Per-translation-unit tables (defined in mm_bf16_*.hip, rms_bf16_*.hip,
 // mm_f32.hip).
 const MiEntry* table_mm_bm32(int* n);

@@ -29,6 +29,7 @@ MI_E_RANGE = 5
 MI_E_ARGS = 6
 MI_E_KERNEL = 7
 MI_E_SPLIT = 8
+MI_E_TILE = 9
 
 CODE_NAMES = {
     MI_E_NO_INSTANCE: "no compiled instance",
@@ -39,6 +40,7 @@ CODE_NAMES = {
     MI_E_ARGS: "bad arguments",
     MI_E_KERNEL: "unknown kernel",
     MI_E_SPLIT: "split_k unsupported",
+    MI_E_TILE: "block size outside the template range",
 }
 
 # Every symbol the header declares; the library must export all of them.
@@ -80,7 +82,7 @@ class KernelLibraryError(RuntimeError):
         self.message = message
 
 
-_LIB: ctypes.CDLL | None = None
+_LIBS: dict[str, ctypes.CDLL] = {}
 
 
 def _declare(lib: ctypes.CDLL) -> None:
@@ -107,20 +109,29 @@ def _declare(lib: ctypes.CDLL) -> None:
         fn.argtypes = args
 
 
+def load(path: str | os.PathLike) -> ctypes.CDLL:
+    """Load (once per path) a library exporting the C ABI of include/mi_kernels.h.
+
+    ``libmi_kernels.so`` holds every prebuilt instance; the autotune
+    pipeline also loads per-config libraries built just in time from a
+    generated instance source.  Both export the same symbols.
+    """
+    key = str(Path(path).resolve())
+    handle = _LIBS.get(key)
+    if handle is None:
+        if not Path(key).exists():
+            raise ImportError(
+                f"{key} not found: build it with `python nki-autotune_amd/build_lib.py` (there is no fallback path)"
+            )
+        handle = ctypes.CDLL(key)
+        _declare(handle)
+        _LIBS[key] = handle
+    return handle
+
+
 def lib() -> ctypes.CDLL:
     """Load (once) and return libmi_kernels.so; raise if it was never built."""
-    global _LIB
-    if _LIB is None:
-        path = Path(os.environ.get("MI_KERNELS_LIB", LIB_PATH))
-        if not path.exists():
-            raise ImportError(
-                f"libmi_kernels.so not found at {path}: build it with "
-                "`python nki-autotune_amd/build_lib.py` (there is no fallback path)"
-            )
-        handle = ctypes.CDLL(str(path))
-        _declare(handle)
-        _LIB = handle
-    return _LIB
+    return load(os.environ.get("MI_KERNELS_LIB", LIB_PATH))
 
 
 def last_error() -> str:

@@ -7,32 +7,44 @@ import numpy as np
 from oracle import inputs as oinputs
 from oracle import metrics
 
-# Parity contract: bf16 inputs against an fp32/fp64
-# reference on the same bf16-rounded inputs, max-relative-error <= 1e-2.
-# matmul: the reference's elementwise metric max(|a-e|/(|e|+5e-3))
-#   (kernel_transforms.py:594-597).  The kernel multiplies the bf16 inputs
-#   exactly and accumulates in fp32, so only the final bf16 rounding (2^-9
-#   relative) separates it from the golden.
-BF16_MATMUL_MAX_REL = 1e-2
-# fp32 kernel: the reference's fp32 contract is allclose(atol=rtol=5e-3)
-# end to end (test/codegen/test_render.py:35-49, examples/
-# tune_matmul_lhsT_rhs.py:156-172) and atol=rtol=1e-4 at 128^3
-# (test/ops/test_direct_numpy_call.py:38).
+# Pass criteria.  The reference passes a kernel with np.allclose(atol, rtol)
+# against the float golden (kernel_transforms.py:592-596; atol = rtol = 5e-3
+# for fp32, test/codegen/test_render.py:49) and reports
+# max_rel = max(|a-e| / (|e| + atol)) beside it.
+#
+# bf16 matmul: allclose with the reference's atol = 5e-3 and the BASELINE's
+#   rtol = 1e-2.  The kernel multiplies bf16 values exactly and accumulates in
+#   fp32, so the error is the final bf16 rounding (<= 2^-9 |e|) plus an fp32
+#   accumulation error (~1e-4 absolute at K = 8192, far under atol).
+BF16_ATOL = 5e-3
+BF16_RTOL = 1e-2
+# fp32 matmul: the reference's fp32 contract, allclose(atol=rtol=5e-3)
+#   (test/codegen/test_render.py:35-49); atol=rtol=1e-4 at 128^3
+#   (test/ops/test_direct_numpy_call.py:38).
 F32_ATOL = F32_RTOL = 5e-3
-# rmsnorm_matmul: the normalised rows are rounded to bf16 before the MFMA
-# (the reference kernel does the same, kernel_hand_online.py:139-149), so an
-# output near zero carries an absolute error of ~2^-9 * sqrt(K) * |y||w| that
-# no relative bound can absorb.  The gate is max-rel 1e-2 with the atol floor
-# set to the RMS of the expected output, plus the normwise max-rel 1e-2.
-RMS_MAX_REL = 1e-2
-RMS_NORMWISE = 1e-2
+# rmsnorm_matmul: the normalised rows are rounded to bf16 before the product
+#   (the reference kernel does the same, kernel_hand_online.py:139-149).  That
+#   rounding leaves an absolute error of about 2^-9/sqrt(3) * RMS(out) per
+#   output (std), ~5.5 std ~ 6e-3 * RMS(out) at the maximum over 16 M outputs.
+#   The absolute floor is therefore 1e-2 * RMS(out); rtol stays 1e-2.
+RMS_ATOL_FRAC = 1e-2
+RMS_RTOL = 1e-2
 
 
-def rms_report(actual: np.ndarray, expected: np.ndarray) -> dict:
+def mm_check(actual: np.ndarray, expected: np.ndarray) -> dict:
+    """Report for a bf16 matmul output; ``ok`` is the allclose gate."""
+    rep = metrics.report(actual, expected, atol=BF16_ATOL, rtol=BF16_RTOL)
+    rep["ok"] = rep["allclose"] and rep["nonfinite"] == 0
+    return rep
+
+
+def rms_check(actual: np.ndarray, expected: np.ndarray) -> dict:
+    """Report for an rmsnorm_matmul output; ``ok`` is the allclose gate with the RMS-scaled floor."""
     e = np.asarray(expected, dtype=np.float64)
-    floor = float(np.sqrt(np.mean(e * e))) if e.size else 1.0
-    rep = metrics.report(actual, expected, atol=floor)
+    floor = RMS_ATOL_FRAC * (float(np.sqrt(np.mean(e * e))) if e.size else 1.0)
+    rep = metrics.report(actual, expected, atol=floor, rtol=RMS_RTOL)
     rep["atol_floor"] = floor
+    rep["ok"] = rep["allclose"] and rep["nonfinite"] == 0
     return rep
 
 
