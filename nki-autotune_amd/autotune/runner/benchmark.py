@@ -43,13 +43,13 @@ def generate_tensors(input_specs: dict, seed: int, dists: dict | None = None) ->
         dist = (dists or {}).get(name, "normal")
         shape = tuple(int(s) for s in shape)
         if dist == "normal":
-            a = rng.standard_normal(shape, dtype=np.float32)
+            a = rng.standard_normal(shape).astype(np.float32)  # float64 draw, then cast (benchmark.py:168)
         elif dist == "uniform":
             a = rng.uniform(-1.0, 1.0, shape).astype(np.float32)
         elif dist == "gamma":
             a = (1.0 + 0.1 * rng.standard_normal(shape)).astype(np.float32)
         elif isinstance(dist, (tuple, list)) and dist[0] == "normal":
-            a = (float(dist[1]) * rng.standard_normal(shape, dtype=np.float32)).astype(np.float32)
+            a = (float(dist[1]) * rng.standard_normal(shape)).astype(np.float32)
         else:
             raise ValueError(f"unknown distribution {dist!r} for input {name!r}")
         out[name] = a

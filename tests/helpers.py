@@ -14,8 +14,9 @@ from oracle import metrics
 #
 # bf16 matmul: allclose with the reference's atol = 5e-3 and the BASELINE's
 #   rtol = 1e-2.  The kernel multiplies bf16 values exactly and accumulates in
-#   fp32, so the error is the final bf16 rounding (<= 2^-9 |e|) plus an fp32
-#   accumulation error (~1e-4 absolute at K = 8192, far under atol).
+#   fp32, so the error is the final bf16 rounding (<= 2^-8 |e|, 8 significant
+#   bits) plus an fp32 accumulation error (~1e-4 absolute at K = 8192, far
+#   under atol).
 BF16_ATOL = 5e-3
 BF16_RTOL = 1e-2
 # fp32 matmul: the reference's fp32 contract, allclose(atol=rtol=5e-3)
@@ -23,10 +24,12 @@ BF16_RTOL = 1e-2
 #   (test/ops/test_direct_numpy_call.py:38).
 F32_ATOL = F32_RTOL = 5e-3
 # rmsnorm_matmul: the normalised rows are rounded to bf16 before the product
-#   (the reference kernel does the same, kernel_hand_online.py:139-149).  That
-#   rounding leaves an absolute error of about 2^-9/sqrt(3) * RMS(out) per
-#   output (std), ~5.5 std ~ 6e-3 * RMS(out) at the maximum over 16 M outputs.
-#   The absolute floor is therefore 1e-2 * RMS(out); rtol stays 1e-2.
+#   (the reference kernel does the same, kernel_hand_online.py:139-149).  Each
+#   rounded element carries a relative error of at most 2^-8 (rms ~1.5e-3), so
+#   an output gets an absolute error of ~1.5e-3 * RMS(out) (std) whatever its
+#   own size; the largest over the 16 M outputs of the 4096^3 case measures
+#   ~6e-3 * RMS(out).  The absolute floor is therefore 1e-2 * RMS(out); rtol
+#   stays 1e-2.
 RMS_ATOL_FRAC = 1e-2
 RMS_RTOL = 1e-2
 

@@ -1,0 +1,121 @@
+"""CPU tests of the C ABI (libmi_kernels.so): it loads, exports every symbol of
+include/mi_kernels.h, and its host-side legality checks return the documented
+codes.  No call here launches a kernel or touches a GPU buffer.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from kernel_library import _lib
+from kernel_library.config import TileConfig, check, compiled_configs, default_config
+
+ROOT = Path(__file__).resolve().parents[1]
+MM, F32, RMS = _lib.MI_KERNEL_MATMUL_LHST_RHS_BF16, _lib.MI_KERNEL_MATMUL_LHST_RHS_F32, _lib.MI_KERNEL_RMSNORM_MATMUL_BF16
+
+
+def header_symbols() -> set[str]:
+    syms = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        syms |= set(re.findall(r"^\s*(?:int|const\s+char\s*\*)\s+(mi_\w+)\s*\(", text, flags=re.M))
+    return syms
+
+
+def test_library_exports_every_header_symbol():
+    syms = header_symbols()
+    assert syms, "no declarations parsed from include/*.h"
+    assert syms == set(_lib.EXPORTED_SYMBOLS)
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    for s in sorted(syms):
+        assert getattr(raw, s) is not None, s
+    assert _lib.lib().mi_version().decode().startswith("mi_kernels")
+
+
+def test_every_compiled_config_is_enumerable_and_legal():
+    for fam, shape in (("matmul_lhsT_rhs", (2048, 2048, 2048)), ("rmsnorm_matmul", (2048, 2048, 2048)),
+                       ("matmul_lhsT_rhs_f32", (256, 512, 512))):
+        cfgs = compiled_configs(fam)
+        assert len(cfgs) == len(set(cfgs)) > 0
+        for c in cfgs:
+            assert check(fam, c, *shape) == (0, ""), (fam, c)
+
+
+@pytest.mark.parametrize(
+    "kid,cfg,shape,code",
+    [
+        (MM, TileConfig(256, 256, 64, 8, 2), (8192, 8192, 8192), _lib.MI_OK),
+        (MM, TileConfig(256, 256, 128, 8, 2), (8192, 8192, 8192), _lib.MI_E_LDS),        # 256 KiB of panels
+        (MM, TileConfig(32, 32, 64, 8, 1), (1024, 1024, 1024), _lib.MI_E_WAVE_TILE),     # 8 waves, 1 MFMA tile
+        (MM, TileConfig(128, 192, 32, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),        # 192 not a power of 2
+        (RMS, TileConfig(128, 128, 16, 4, 1), (1024, 1024, 1024), _lib.MI_E_TILE),       # fused kernel needs bk >= 32
+        (MM, TileConfig(128, 128, 64, 4, 2, split_k=2), (1024, 1024, 1024), _lib.MI_E_SPLIT),
+        (MM, TileConfig(128, 128, 64, 4, 2), (1020, 1024, 1024), _lib.MI_E_ALIGN),       # M % 8
+        (RMS, TileConfig(128, 128, 64, 8, 2), (1024, 1024, 1020), _lib.MI_E_ALIGN),      # K % 8 (fused)
+        (MM, TileConfig(128, 128, 64, 4, 2), (65536, 65536, 65536), _lib.MI_E_RANGE),    # 8 GiB operand
+        (MM, TileConfig(128, 128, 48, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),
+        (MM, TileConfig(512, 512, 32, 8, 1), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),  # legal, not prebuilt
+        (MM, TileConfig(0, 128, 64, 4, 2), (1024, 1024, 1024), _lib.MI_E_ARGS),
+    ],
+)
+def test_cfg_check_codes(kid, cfg, shape, code):
+    c = cfg.to_c()
+    rc = _lib.lib().mi_cfg_check(kid, ctypes.byref(c), *shape)
+    assert rc == code, (rc, _lib.last_error())
+    assert (_lib.last_error() == "") == (code == 0)
+
+
+def test_cfg_check_rejects_unknown_kernel_and_null():
+    L = _lib.lib()
+    c = TileConfig().to_c()
+    assert L.mi_cfg_check(99, ctypes.byref(c), 8, 8, 8) == _lib.MI_E_KERNEL
+    assert L.mi_cfg_check(MM, None, 8, 8, 8) == _lib.MI_E_ARGS
+    assert L.mi_get_config(MM, 10_000, ctypes.byref(c)) == _lib.MI_E_ARGS
+
+
+@pytest.mark.parametrize("M,N,K", [(8192, 8192, 8192), (4096, 4096, 4096), (2048, 1024, 8192), (4096, 14336, 1024),
+                                   (1024, 4096, 14336), (16, 28672, 8192), (64, 28672, 8192), (128, 28672, 8192),
+                                   (256, 512, 512)])
+def test_default_configs_are_legal_at_baseline_shapes(M, N, K):
+    for fam in ("matmul_lhsT_rhs", "rmsnorm_matmul"):
+        cfg = default_config(fam, M, N, K)
+        assert check(fam, cfg, M, N, K)[0] == 0, (fam, cfg)
+    assert check("matmul_lhsT_rhs_f32", default_config("matmul_lhsT_rhs_f32", 256, 512, 512), 256, 512, 512)[0] == 0
+
+
+def test_entry_points_reject_bad_arguments_before_any_gpu_call():
+    """Negative sizes, null pointers and a non-finite eps are refused on the host; empty outputs are no-ops."""
+    L = _lib.lib()
+    c = TileConfig(128, 128, 64, 4, 2).to_c()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: every call below returns before a launch
+    assert L.mi_matmul_lhsT_rhs_bf16(fake, fake, fake, -1, 8, 8, ctypes.byref(c), None) == _lib.MI_E_ARGS
+    assert L.mi_matmul_lhsT_rhs_bf16(fake, fake, None, 8, 8, 8, ctypes.byref(c), None) == _lib.MI_E_ARGS
+    assert L.mi_matmul_lhsT_rhs_bf16(None, fake, fake, 8, 8, 8, ctypes.byref(c), None) == _lib.MI_E_ARGS
+    assert L.mi_matmul_lhsT_rhs_bf16(fake, fake, fake, 0, 8, 8, ctypes.byref(c), None) == _lib.MI_OK
+    assert L.mi_matmul_lhsT_rhs_f32(fake, fake, fake, 8, -8, 8, ctypes.byref(c), None) == _lib.MI_E_ARGS
+    assert L.mi_rmsnorm_matmul_bf16(fake, None, fake, fake, 8, 8, 0, 1e-6, ctypes.byref(c), None) == _lib.MI_E_ARGS
+    assert L.mi_rmsnorm_matmul_bf16(fake, None, fake, fake, 8, 8, 8, float("nan"), ctypes.byref(c),
+                                    None) == _lib.MI_E_ARGS
+    assert L.mi_rmsnorm_matmul_bf16(fake, None, fake, fake, 8, 8, 8, -1.0, ctypes.byref(c), None) == _lib.MI_E_ARGS
+    assert L.mi_rmsnorm_matmul_bf16(fake, None, None, fake, 8, 8, 8, 1e-6, ctypes.byref(c), None) == _lib.MI_E_ARGS
+    assert "null" in _lib.last_error()
+    # an illegal config is refused before the launch as well
+    bad = TileConfig(256, 256, 128, 8, 2).to_c()
+    assert L.mi_matmul_lhsT_rhs_bf16(fake, fake, fake, 8192, 8192, 8192, ctypes.byref(bad), None) == _lib.MI_E_LDS
+
+
+def test_python_wrappers_validate_on_the_host():
+    torch = pytest.importorskip("torch")
+    import kernel_library as kl
+
+    a = torch.zeros((64, 32), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="HIP device"):
+        kl.matmul_lhsT_rhs(a, a)
+    with pytest.raises(TypeError):
+        kl.matmul_lhsT_rhs([[1.0]], a)
+    with pytest.raises(ValueError):
+        kl.rmsnorm_matmul(a, a, eps=1e-6)

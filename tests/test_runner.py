@@ -1,0 +1,199 @@
+"""CPU tests of the autotune runner: results table, selection, results.json,
+the compile step and the pipeline's host-side checks.
+
+The first three tests mirror the reference's only profiler-backend tests
+(test/runner/test_output.py:21-56), which build ProfileResults by hand.
+"""
+
+from __future__ import annotations
+
+import json
+
+import pytest
+
+from autotune.runner import compile as rcompile
+from autotune.runner.benchmark import utilisation, work_of
+from autotune.runner.output import ProfileOutput, write_kernel_sources, write_results_json
+from autotune.runner.types import KernelJob, ProfileResult, profiler_percent
+from autotune.tune import input_specs, make_jobs
+from kernel_library import _lib
+from kernel_library.config import TileConfig, baseline_grid, record_tuned
+
+
+def _summary_result(name: str, total_time: float, mfu: float, cfg: TileConfig | None = None) -> ProfileResult:
+    summary = {"total_time": total_time, "mfu_estimated_percent": mfu, "tflops": 1.0 / total_time}
+    if cfg is not None:
+        summary["config"] = cfg.asdict()
+    return ProfileResult(kernel_name=name, hardware_output="[128, 512] bfloat16", profiler_summary=summary)
+
+
+def test_write_results_json_no_hosts_key(tmp_path):
+    results = [_summary_result("k_0.hip", 0.001, 0.9)]
+    write_results_json(str(tmp_path), num_kernels=1, results=results, wallclock_s=1.5)
+    data = json.loads((tmp_path / "results.json").read_text())
+    assert "hosts" not in data["metadata"]
+    assert data["metadata"] == {"num_kernels": 1, "wallclock_s": 1.5}
+    assert data["metrics"]["success"] == 1
+    assert data["kernels"][0]["kernel_name"] == "k_0.hip"
+    assert (tmp_path / "k_0" / "profile_summary.json").exists()
+
+
+def test_write_results_json_sorts_kernels_numerically(tmp_path):
+    results = [_summary_result("kernel_10.hip", 0.002, 0.5), _summary_result("kernel_2.hip", 0.001, 0.5),
+               _summary_result("zeta.hip", 0.003, 0.5)]
+    write_results_json(str(tmp_path), num_kernels=3, results=results, wallclock_s=1.0)
+    names = [k["kernel_name"] for k in json.loads((tmp_path / "results.json").read_text())["kernels"]]
+    assert names == ["kernel_2.hip", "kernel_10.hip", "zeta.hip"]
+
+
+def test_profile_output_str_has_no_hosts_line():
+    out = ProfileOutput(results=[_summary_result("k_0.hip", 0.001, 0.9)], compiler_logs={}, elapsed_s=2.0)
+    text = str(out)
+    assert "Hosts:" not in text and "Succeeded:  1/1" in text
+
+
+def test_selection_metrics_and_failure_classes(tmp_path):
+    fast = TileConfig(256, 128, 64, 8, 1)
+    results = [
+        _summary_result("a.hip", 0.003, 0.3, TileConfig(128, 128, 64, 4, 2)),
+        _summary_result("b.hip", 0.001, 0.9, fast),
+        ProfileResult("c.hip", "illegal config bm256_bn256_bk128_w8_s2 at M=8 N=8 K=8: [LDS over budget] LDS ..."),
+        ProfileResult("d.hip", "illegal config x: [alignment] M=7"),
+        ProfileResult("e.hip", "Traceback ...\nRuntimeError: hipcc failed for e.hip:\nerror: ..."),
+        ProfileResult("f.hip", "Compilation timed out after 600 s"),
+        ProfileResult("g.hip", "[1, 1] bfloat16", None),  # ran but produced no summary
+    ]
+    out = ProfileOutput(results, {}, 3.0)
+    assert [s.kernel_name for s in out.successes] == ["a.hip", "b.hip"]
+    assert out.best.kernel_name == "b.hip" and out.best.config == fast.name
+    assert {r.kernel_name for r in out.failures} == {"c.hip", "d.hip", "e.hip", "f.hip", "g.hip"}
+    text = str(out)
+    assert text.index("b.hip") < text.index("a.hip")          # table sorted by time
+    assert "5 failures:" in text and "Best:       0.001000 s (b.hip)" in text
+    write_results_json(str(tmp_path), len(results), results, 3.0)
+    m = json.loads((tmp_path / "results.json").read_text())["metrics"]
+    assert m["best_kernel"] == "b.hip" and m["worst_kernel"] == "a.hip"
+    assert m["best_config"] == fast.asdict()
+    assert m["best_mfu"] == pytest.approx(90.0) and m["worst_mfu"] == pytest.approx(30.0)
+    assert (m["success"], m["lds_over_budget"], m["illegal_config"], m["compile_error"], m["timeout"]) == (2, 1, 1, 1, 1)
+
+
+def test_profiler_percent_contract():
+    assert profiler_percent({"x": 0.5}, "x") == 50.0
+    assert profiler_percent({"x": -1.0}, "x") is None       # negative sentinel
+    assert profiler_percent({}, "x") is None and profiler_percent(None, "x") is None
+
+
+def test_work_and_utilisation_known_answers():
+    flops, nbytes = work_of("matmul_lhsT_rhs", 8192, 8192, 8192, "bfloat16")
+    assert flops == 2 * 8192**3 and nbytes == 3 * 8192 * 8192 * 2
+    f2, b2 = work_of("rmsnorm_matmul", 4096, 4096, 4096, "bfloat16", has_gamma=True)
+    assert b2 == 3 * 4096 * 4096 * 2 + 4096 * 2
+    u = utilisation(flops, nbytes, 1e-3, "bfloat16")
+    assert u["tflops"] == pytest.approx(1099.511627776)
+    assert u["mfu_estimated_percent"] == pytest.approx(1099.511627776 / 2500)
+    assert u["mbu_estimated_percent"] == pytest.approx(402.653184 / 8000)
+    assert u["mfu_max_achievable_estimated_percent"] == 1.0
+    skinny = utilisation(*work_of("matmul_lhsT_rhs", 16, 28672, 8192, "bfloat16"), 1e-4, "bfloat16")
+    assert skinny["mfu_max_achievable_estimated_percent"] < 0.06   # HBM-bound shape
+
+
+def test_render_parse_roundtrip_and_aliases():
+    for fam in ("matmul_lhsT_rhs", "rmsnorm_matmul", "matmul_lhsT_rhs_nkigym", "rmsnorm_matmul_online"):
+        cfg = TileConfig(128, 256, 64, 8, 2, variant=1 if "rms" in fam else 0)
+        src = rcompile.render_source(fam, cfg)
+        got_fam, got_cfg = rcompile.parse_source(src)
+        assert got_fam == rcompile.canonical_name(fam) and got_cfg == cfg
+        assert "#include \"mi_registry.hpp\"" in src
+    with pytest.raises(ValueError):
+        rcompile.parse_source("__global__ void k() {}")
+    assert rcompile.problem_shape("matmul_lhsT_rhs", input_specs("matmul_lhsT_rhs", 64, 96, 128)) == (64, 96, 128)
+    assert rcompile.problem_shape("rmsnorm_matmul", input_specs("rmsnorm_matmul", 64, 96, 128)) == (64, 96, 128)
+
+
+def test_compile_one_prebuilt_and_rejections(tmp_path):
+    specs = input_specs("matmul_lhsT_rhs", 1024, 1024, 1024)
+    src = rcompile.render_source("matmul_lhsT_rhs", TileConfig(256, 128, 64, 8, 1))
+    cr = rcompile.compile_one("a.hip", src, "matmul_lhsT_rhs", specs, str(tmp_path))
+    assert cr.error == "" and cr.library_path == str(_lib.LIB_PATH)
+    big = rcompile.render_source("matmul_lhsT_rhs", TileConfig(256, 256, 128, 8, 2))
+    cr = rcompile.compile_one("b.hip", big, "matmul_lhsT_rhs", specs, str(tmp_path))
+    assert "LDS over budget" in cr.error and cr.library_path == ""
+    cr = rcompile.compile_one("c.hip", src, "rmsnorm_matmul", specs, str(tmp_path))
+    assert "does not match" in cr.error
+    cr = rcompile.compile_one("d.hip", "garbage", "matmul_lhsT_rhs", specs, str(tmp_path))
+    assert "Traceback" in cr.error
+    jit = rcompile.render_source("matmul_lhsT_rhs", TileConfig(512, 128, 32, 8, 1))
+    cr = rcompile.compile_one("e.hip", jit, "matmul_lhsT_rhs", specs, str(tmp_path), allow_jit=False)
+    assert "JIT is off" in cr.error
+
+
+def test_compile_one_builds_a_non_prebuilt_instance(tmp_path):
+    """A legal config outside the prebuilt table is built by hipcc into a library with the full C ABI."""
+    specs = input_specs("matmul_lhsT_rhs", 1024, 1024, 1024)
+    cfg = TileConfig(512, 128, 32, 8, 1)
+    cr = rcompile.compile_one("jit_0.hip", rcompile.render_source("matmul_lhsT_rhs", cfg), "matmul_lhsT_rhs", specs,
+                              str(tmp_path))
+    assert cr.error == "", cr.error
+    lib = _lib.load(cr.library_path)
+    assert lib.mi_num_configs(_lib.MI_KERNEL_MATMUL_LHST_RHS_BF16) == 1
+    c = cfg.to_c()
+    import ctypes
+
+    assert lib.mi_cfg_check(_lib.MI_KERNEL_MATMUL_LHST_RHS_BF16, ctypes.byref(c), 1024, 1024, 1024) == 0
+    assert lib.mi_num_configs(_lib.MI_KERNEL_RMSNORM_MATMUL_BF16) == 0
+
+
+def test_compile_timeout_is_an_error_string(tmp_path):
+    specs = input_specs("matmul_lhsT_rhs", 1024, 1024, 1024)
+    src = rcompile.render_source("matmul_lhsT_rhs", TileConfig(512, 128, 64, 8, 1))
+    cr = rcompile.compile_one("slow.hip", src, "matmul_lhsT_rhs", specs, str(tmp_path), timeout_s=0.01)
+    assert cr.error.startswith("Compilation timed out")
+
+
+def test_pipeline_rejects_more_than_one_device(tmp_path):
+    from autotune.runner.driver import run_pipeline
+
+    job = next(iter(make_jobs("matmul_lhsT_rhs", 256, 256, 256, [TileConfig(128, 128, 64, 4, 2)]).values()))
+    with pytest.raises(RuntimeError, match="one GPU"):
+        run_pipeline({"k.hip": job._replace(lnc=2)}, 0, False, False, work_dir=str(tmp_path / "w"))
+
+
+def test_profile_requires_a_gfx950_device(tmp_path):
+    """Environment faults raise (reference detect.py:13-19); on this CPU host no HIP device is visible."""
+    torch = pytest.importorskip("torch")
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is visible")
+    from autotune.runner.api import profile
+
+    jobs = make_jobs("matmul_lhsT_rhs", 256, 256, 256, [TileConfig(128, 128, 64, 4, 2)])
+    with pytest.raises(RuntimeError, match="HIP device"):
+        profile(jobs, str(tmp_path / "cache"), 0)
+    with pytest.raises(ValueError):
+        profile(jobs, "", 0, platform_target="trn2")
+
+
+def test_make_jobs_and_cache_sources(tmp_path):
+    cfgs = [TileConfig(128, 128, 64, 4, 2), TileConfig(256, 128, 64, 8, 1)]
+    jobs = make_jobs("rmsnorm_matmul", 4096, 4096, 4096, cfgs)
+    assert list(jobs) == [c.name + ".hip" for c in cfgs]
+    job = jobs[cfgs[0].name + ".hip"]
+    assert isinstance(job, KernelJob) and job.output_shape == (4096, 4096)
+    assert list(job.input_specs) == ["lhs", "gamma", "rhs"]
+    assert job.input_dists["rhs"] == ("normal", 1 / 64)
+    write_kernel_sources(str(tmp_path), jobs)
+    text = (tmp_path / cfgs[1].name / (cfgs[1].name + ".hip")).read_text()
+    assert rcompile.parse_source(text)[1] == cfgs[1]
+
+
+def test_baseline_grid_and_tuned_table(tmp_path):
+    grid = baseline_grid()
+    assert len(grid) == 72 and len(set(grid)) == 72
+    assert len(baseline_grid((0, 1))) == 144
+    path = tmp_path / "tuned.json"
+    record_tuned("matmul_lhsT_rhs", 64, 64, 64, grid[5], path=path, extra={"tflops": 1.0})
+    record_tuned("rmsnorm_matmul", 64, 64, 64, grid[6], path=path)
+    doc = json.loads(path.read_text())
+    assert doc["configs"]["matmul_lhsT_rhs:64x64x64"] == grid[5].asdict()
+    assert doc["measurements"]["matmul_lhsT_rhs:64x64x64"] == {"tflops": 1.0}
+    assert TileConfig(**doc["configs"]["rmsnorm_matmul:64x64x64"]) == grid[6]
