@@ -87,7 +87,12 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
     // chunks: block_m / block_n must be powers of two in [32, 512] and
     // block_k a power of two in [16, 128] ([32, 128] for the fused kernel,
     // whose x rows are reduced over BK/8 lanes).
-    const int kmin = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 ? 32 : 16;
+    // The pipelined matmul (variant 1) double-buffers MFMA operands across
+    // K sub-steps of 16 and needs an even number of them.
+    const int kmin = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 || (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 &&
+                                                                   c.variant == 1)
+                         ? 32
+                         : 16;
     if (!pow2_in(c.block_m, 32, 512) || !pow2_in(c.block_n, 32, 512) || !pow2_in(c.block_k, kmin, 128))
       return fail(MI_E_TILE, "block sizes bm=%d bn=%d bk=%d outside the template range", c.block_m, c.block_n,
                   c.block_k);

@@ -46,6 +46,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint3
 // LDS-direct loads) has landed.  expcnt/lgkmcnt fields are left at max.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// s_waitcnt vmcnt(N): at most N vector-memory loads of this wave still in
+// flight (gfx9 encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14).
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
+// One LDS-direct load: 16 bytes per lane from the buffer at byte `voff` to
+// LDS at `lds` + 16 * lane (buffer_load_dwordx4 ... lds, base address in M0).
+// Issued as inline assembly so that the compiler does not treat it as a
+// store that every later LDS read must wait for: the kernels order these
+// loads against LDS reads themselves (vm_wait / wait_vmem, then a barrier).
+__device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, char* lds, uint32_t voff) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(MI_LDS char*)lds;
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
+}
+
 // Wave grid: WM x WN waves, each owning a (BM/WM) x (BN/WN) block that is
 // a whole number of 32x32 MFMA tiles.  The most square wave block wins.
 template <int BM, int BN, int WAVES>
@@ -91,12 +109,21 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_
 }
 
 // XOR swizzle of 16-byte chunks inside one K row of an MN-contiguous panel
-// (row = one K index, ROWB/16 chunks).  Rows k..k+3 read together by one
-// ds_read_b64_tr_b16 group land 32 bytes apart, so the 4x32-byte read of a
-// 16-lane group covers 128 distinct bytes.
+// (row = one K index, ROWB/16 chunks).  gfx950's LDS has 64 banks of 4 bytes
+// (a 256-byte bank window).  One ds_read_b64_tr_b16 reads, per 32 lanes,
+// K rows k0..k0+3 x 64 bytes (k0 a multiple of 4), and lanes 32..63 read
+// rows k0+8..k0+11.  The swizzle puts the four rows of one read in four
+// different 64-byte quarters of the bank window, and rows k and k+8 in
+// different 32-byte halves of a quarter, whatever the row pitch:
+//   pitch >= 256 B: every row starts at bank 0, XOR the quarter by k&3;
+//   pitch == 128 B: rows alternate window halves, XOR the quarter by bit 1;
+//   pitch ==  64 B: consecutive rows already sit in consecutive quarters.
 template <int ROWB>
 __device__ __forceinline__ int mn_swz(int k) {
-  return (2 * (k & 3)) & (ROWB / 16 - 1);
+  const int half = 2 * ((k >> 3) & 1);
+  if constexpr (ROWB >= 256) return 4 * (k & 3) ^ half;
+  else if constexpr (ROWB == 128) return 4 * ((k >> 1) & 1) ^ half;
+  else return half & (ROWB / 16 - 1);
 }
 
 // LDS-direct loader of one [BK][W] MN-contiguous panel (W = BM or BN):
@@ -131,16 +158,23 @@ struct PanelLoader {
     }
   }
   // Issue the loads of K tile `kt` into the panel at LDS byte `base`.
+  // Completion is tracked by vmcnt only: every reader waits with
+  // wait_vmem() (or vm_wait<n>) and a workgroup barrier first.
   __device__ __forceinline__ void issue(__amdgpu_buffer_rsrc_t rs, char* smem, int base, uint32_t kstep_bytes,
                                         int kt) const {
 #pragma unroll
     for (int j = 0; j < PER_WAVE; ++j) {
-      if (EVEN || active[j]) {
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (MI_LDS void*)(smem + base + lds_off[j]), 16,
-                                                 voff[j] + (uint32_t)kt * kstep_bytes, 0, 0, 0);
-      }
+      if (EVEN || active[j]) lds_dma16(rs, smem + base + lds_off[j], voff[j] + (uint32_t)kt * kstep_bytes);
     }
   }
+  // Load j (< PER_WAVE) of K tile `kt` alone, for schedules that spread a
+  // tile's loads between other instructions.
+  __device__ __forceinline__ void issue_one(int j, __amdgpu_buffer_rsrc_t rs, char* smem, int base,
+                                            uint32_t kstep_bytes, int kt) const {
+    if (EVEN || active[j]) lds_dma16(rs, smem + base + lds_off[j], voff[j] + (uint32_t)kt * kstep_bytes);
+  }
+  // Number of LDS-direct loads one wave issues per K tile.
+  static constexpr int LOADS_PER_TILE = PER_WAVE;
 };
 
 // Per-lane LDS byte offsets of the MFMA operand fragments read with
@@ -324,6 +358,187 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_kernel(const uint
       __syncthreads();
     }
   }
+
+  float one[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) one[i] = 1.0f;
+  store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
+}
+
+// Scheduling hint for one MFMA K sub-step: NM MFMAs with ND LDS reads spread
+// between them (a wave issues in order, so an MFMA stuck behind a run of LDS
+// reads -- or reads stuck behind a run of MFMAs -- idles the matrix core).
+// Masks: 0x008 MFMA, 0x100 DS read; the trailing sched_barrier closes the
+// region so the next sub-step gets its own pattern.
+template <int NM, int ND, int M = 0>
+__device__ __forceinline__ void interleave_mfma_ds() {
+  if constexpr (M < NM) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    constexpr int n = ND / NM + (M < ND % NM ? 1 : 0);
+    if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x100, n, 0);
+    interleave_mfma_ds<NM, ND, M + 1>();
+  } else {
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// out[M,N] = lhsT[K,M]^T . rhs[K,N], software-pipelined (matmul variant 1).
+//
+// STAGES LDS buffers hold K tiles t .. t+STAGES-1.  Inside a K tile the
+// MFMA operands of sub-step kk+1 are read from LDS while the MFMAs of kk
+// run (two register sets).  At the last sub-step of tile t each wave waits
+// for its own loads of tile t+1, the workgroup meets at one barrier (after
+// which tile t+1 is visible and nobody reads tile t's buffer any more), the
+// first operands of tile t+1 are read, and the loads of tile t+STAGES are
+// issued into the buffer tile t just vacated -- so one barrier per K tile,
+// and global loads run STAGES-1 tiles ahead of the MFMAs.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+struct PipeCfg {
+  using G = WaveGrid<BM, BN, WAVES>;
+  static constexpr int A_BYTES = BK * BM * 2;
+  static constexpr int B_BYTES = BK * BN * 2;
+  static constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  static constexpr int EPI_BYTES = WAVES * 32 * (G::WTN * 2 + 16);
+  static constexpr int MAIN_BYTES = STAGES * STAGE_BYTES;
+  static constexpr int LDS_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
+};
+
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+__global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const uint16_t* __restrict__ lhsT,
+                                                                          const uint16_t* __restrict__ rhs,
+                                                                          uint16_t* __restrict__ out, int M, int N,
+                                                                          int K, int group_m) {
+  using C = PipeCfg<BM, BN, BK, WAVES, STAGES>;
+  using G = typename C::G;
+  static_assert(G::ok, "illegal wave grid");
+  static_assert(BK % 32 == 0, "BK must be a multiple of 32 (even number of MFMA K steps)");
+  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
+  constexpr int TM = G::TM, TN = G::TN, KS = BK / 16;
+  using LA = PanelLoader<BK, BM, WAVES>;
+  using LB = PanelLoader<BK, BN, WAVES>;
+  // Loads of one K tile by this wave; vm_wait<n> with n > 0 needs every wave
+  // to issue the same number.
+  constexpr int LPT = LA::LOADS_PER_TILE + LB::LOADS_PER_TILE;
+  static_assert(STAGES == 2 || (LA::EVEN && LB::EVEN), "deeper pipelines need an even panel split");
+  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tmi, tni;
+  tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+  const int wm0 = (wave / G::WN) * G::WTM;
+  const int wn0 = (wave % G::WN) * G::WTN;
+
+  const __amdgpu_buffer_rsrc_t ra = make_rsrc(lhsT, (uint32_t)K * (uint32_t)M * 2u);
+  const __amdgpu_buffer_rsrc_t rb = make_rsrc(rhs, (uint32_t)K * (uint32_t)N * 2u);
+  LA la;
+  LB lb;
+  la.init(wave, lane, m0, M);
+  lb.init(wave, lane, n0, N);
+  const uint32_t kstep_a = (uint32_t)BK * (uint32_t)M * 2u;
+  const uint32_t kstep_b = (uint32_t)BK * (uint32_t)N * 2u;
+  TrFrag<BM, TM> fa;
+  TrFrag<BN, TN> fb;
+  fa.init(lane, wm0);
+  fb.init(lane, wn0);
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
+
+  bf16x8_t af[2][TM], bf[2][TN];
+  // Operand f of a K sub-step, in the order the MFMAs (row-major over
+  // (i, j)) consume them: A0, B0 .. B(TN-1), A1 .. A(TM-1).
+  constexpr int NF = TM + TN;
+  auto read_frag = [&](int stage, int kk, int buf, int f) {
+    const int abase = stage * C::STAGE_BYTES;
+    const int bbase = abase + C::A_BYTES;
+    if (f == 0 || f > TN) {
+      const int t = f == 0 ? 0 : f - TN;
+      af[buf][t] = read_tr_frag(smem, abase + (kk * 16) * (BM * 2) + fa.off[t],
+                                abase + (kk * 16 + 4) * (BM * 2) + fa.off[t]);
+    } else {
+      const int t = f - 1;
+      bf[buf][t] = read_tr_frag(smem, bbase + (kk * 16) * (BN * 2) + fb.off[t],
+                                bbase + (kk * 16 + 4) * (BN * 2) + fb.off[t]);
+    }
+  };
+  auto read_frags = [&](int stage, int kk, int buf) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) read_frag(stage, kk, buf, f);
+  };
+  auto mfmas = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[buf][j], af[buf][i], acc[i][j], 0, 0, 0);
+  };
+  // Load q (< LPT) of K tile kt into `stage`: the A loads, then the B loads.
+  auto issue_one = [&](int q, int kt, int stage) {
+    if (q < LA::LOADS_PER_TILE) la.issue_one(q, ra, smem, stage * C::STAGE_BYTES, kstep_a, kt);
+    else lb.issue_one(q - LA::LOADS_PER_TILE, rb, smem, stage * C::STAGE_BYTES + C::A_BYTES, kstep_b, kt);
+  };
+
+  const int KT = (K + BK - 1) / BK;
+  // Tiles past the end are clamped to the last one: the loads stay in
+  // bounds, every tile issues the same number of loads (so vmcnt counts are
+  // static) and the loop needs no branch.  Re-reading the last tile into a
+  // buffer that is never read again costs STAGES-1 tiles of bandwidth.
+  auto clamp = [&](int kt) { return kt < KT ? kt : KT - 1; };
+
+  // Prologue: tiles 0 .. STAGES-1 in flight, wait for tile 0.
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s)
+#pragma unroll
+    for (int q = 0; q < LPT; ++q) issue_one(q, clamp(s), s);
+  vm_wait<(STAGES - 1) * LPT>();
+  __syncthreads();
+  read_frags(0, 0, 0);
+
+  // Steady state: every tile but the last.  At the last sub-step the wave
+  // waits for tile t+1 (tiles t+2 .. t+STAGES-1 may still fly), meets the
+  // workgroup, then reads tile t+1's first operands and issues tile
+  // t+STAGES into the buffer tile t vacated, both between the MFMAs of the
+  // sub-step.
+  int cur = 0;
+  for (int t = 0; t + 1 < KT; ++t) {
+    const int nxt = cur + 1 == STAGES ? 0 : cur + 1;
+#pragma unroll
+    for (int kk = 0; kk + 1 < KS; ++kk) {
+      read_frags(cur, kk + 1, (kk + 1) & 1);
+      mfmas(kk & 1);
+      interleave_mfma_ds<TM * TN, 2 * NF>();
+    }
+    vm_wait<(STAGES - 2) * LPT>();
+    __syncthreads();
+    const int kt_new = clamp(t + STAGES);
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      read_frag(nxt, 0, 0, f);
+#pragma unroll
+      for (int q = f * LPT / NF; q < (f + 1) * LPT / NF; ++q) issue_one(q, kt_new, cur);
+    }
+    mfmas((KS - 1) & 1);
+    interleave_mfma_ds<TM * TN, 2 * NF>();
+    cur = nxt;
+  }
+  // Last tile: no further loads.
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    if (kk + 1 < KS) read_frags(cur, kk + 1, (kk + 1) & 1);
+    mfmas(kk & 1);
+    interleave_mfma_ds<TM * TN, 2 * NF>();
+  }
+  wait_vmem();
+  __syncthreads();  // the epilogue reuses the panel buffers
 
   float one[TM];
 #pragma unroll

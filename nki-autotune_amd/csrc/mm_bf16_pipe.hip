@@ -1,0 +1,31 @@
+// Instances of the software-pipelined lhsT.rhs matmul (matmul variant 1):
+// 4-wave blocks with 128x128 (or 128x64, 64x64) per wave at one wave per
+// SIMD, and 8-wave blocks at two waves per SIMD; 2 to 4 LDS stages.
+#include "mi_registry.hpp"
+
+#define MI_PIPE_CONFIGS(X)   \
+  X(256, 256, 64, 4, 2)      \
+  X(256, 256, 32, 4, 2)      \
+  X(256, 256, 32, 4, 3)      \
+  X(256, 256, 32, 4, 4)      \
+  X(256, 256, 64, 8, 2)      \
+  X(256, 256, 32, 8, 3)      \
+  X(256, 128, 64, 4, 2)      \
+  X(256, 128, 64, 4, 3)      \
+  X(128, 256, 64, 4, 2)      \
+  X(128, 256, 64, 4, 3)      \
+  X(256, 128, 64, 8, 2)      \
+  X(256, 128, 64, 8, 3)      \
+  X(128, 128, 64, 4, 2)      \
+  X(128, 128, 64, 4, 3)      \
+  X(128, 128, 64, 4, 4)
+
+namespace mi {
+MI_PIPE_CONFIGS(MI_MMP_INST)
+
+const MiEntry* table_mm_pipe(int* n) {
+  static const MiEntry t[] = {MI_PIPE_CONFIGS(MI_MMP_ROW)};
+  *n = (int)(sizeof(t) / sizeof(t[0]));
+  return t;
+}
+}  // namespace mi
