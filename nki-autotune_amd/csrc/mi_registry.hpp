@@ -57,6 +57,14 @@ hipError_t launch_rms_bf16(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int BM, int BN, int BK, int W, int S, bool PRE>
+hipError_t launch_rms_pipe(const MiArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((rmsnorm_mm_bf16_pipe_kernel<BM, BN, BK, W, S, PRE>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                     dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
+                     (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
+  return hipGetLastError();
+}
+
 // Explicit instantiation of one config's kernel (namespace scope); every
 // table row needs its kernel instantiated in the same translation unit so
 // the host launch stub is emitted there.
@@ -70,6 +78,10 @@ hipError_t launch_rms_bf16(const MiArgs& a, hipStream_t s) {
   template __global__ void rmsnorm_mm_bf16_kernel<BM, BN, BK, W, S, (PRE != 0)>(                            \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
 
+#define MI_RMSP_INST(BM, BN, BK, W, S, PRE)                                                                  \
+  template __global__ void rmsnorm_mm_bf16_pipe_kernel<BM, BN, BK, W, S, (PRE != 0)>(                       \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
+
 // Table rows; a config whose wave grid is illegal gets no instance.
 #define MI_MM_ROW(BM, BN, BK, W, S)                                                                  \
   {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 0}, MatmulCfg<BM, BN, BK, W, S>::LDS_BYTES, \
@@ -80,6 +92,10 @@ hipError_t launch_rms_bf16(const MiArgs& a, hipStream_t s) {
 #define MI_RMS_ROW(BM, BN, BK, W, S, PRE)                                                            \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, PRE}, RmsCfg<BM, BN, BK, W, S>::LDS_BYTES,   \
    &launch_rms_bf16<BM, BN, BK, W, S, (PRE != 0)>},
+
+#define MI_RMSP_ROW(BM, BN, BK, W, S, PRE)                                                              \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 2 + PRE}, RmsCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_rms_pipe<BM, BN, BK, W, S, (PRE != 0)>},
 
 // The BASELINE grid for one (BM, BN): BK in {32,64} x waves in {4,8} x
 // stages in {1,2}.  X is a row macro taking (BM, BN, BK, W, S, ...).
@@ -115,6 +131,7 @@ const MiEntry* table_mm_pipe(int* n);
 const MiEntry* table_rms_bm64(int* n);
 const MiEntry* table_rms_bm128(int* n);
 const MiEntry* table_rms_bm256(int* n);
+const MiEntry* table_rms_pipe(int* n);
 const MiEntry* table_f32(int* n);
 
 }  // namespace mi

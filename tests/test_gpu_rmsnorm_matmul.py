@@ -58,7 +58,7 @@ def test_no_gamma_is_reference_kernel(gpu):
     assert _ok(rep), rep
 
 
-@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3])
 def test_ragged_and_special_rows(gpu, variant):
     """Edge tiles (M, N not multiples of the block), K not a multiple of block_k; a zero row gives 0."""
     import torch
@@ -106,9 +106,11 @@ def test_baseline_c3_full_size(gpu):
     rng = np.random.default_rng(7)
     rows = np.unique(np.concatenate([[0, 4095], rng.integers(0, 4096, size=24)]))
     expected = orms.closed_form(d["lhs"][rows], d["rhs"], d["gamma"])
-    for variant in (0, 1):
-        cfg = kl.default_config("rmsnorm_matmul", 4096, 4096, 4096)
-        cfg = kl.TileConfig(**{**cfg.asdict(), "variant": variant})
+    cfgs = [kl.TileConfig(256, 256, 64, 8, 2, variant=0), kl.TileConfig(256, 256, 64, 8, 2, variant=1),
+            kl.TileConfig(256, 256, 32, 8, 3, variant=2), kl.TileConfig(256, 256, 32, 8, 3, variant=3),
+            kl.TileConfig(256, 256, 64, 4, 2, variant=2)]
+    for cfg in cfgs:
+        variant = cfg.variant
         out = _host(kl.rmsnorm_matmul(x, w, g, cfg=cfg))
         rep = rms_check(out[rows], expected)
         print(variant, rep)
