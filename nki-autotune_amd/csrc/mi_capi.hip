@@ -100,7 +100,11 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
   if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_F32 && !wave_grid_ok(c.block_m, c.block_n, c.waves))
     return fail(MI_E_WAVE_TILE, "%d waves cannot tile a %dx%d block in 32x32 MFMA tiles", c.waves, c.block_m,
                 c.block_n);
-  const long long lds = (long long)c.lds_stages * (c.block_m + c.block_n) * c.block_k *
+  // Matmul variant 2 keeps its K-tile ring in registers (lds_stages = ring
+  // depth, 1..8) and two LDS stages.
+  const bool reg_ring = kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && c.variant == 2;
+  if (reg_ring && c.lds_stages > 8) return fail(MI_E_ARGS, "register ring depth %d > 8", c.lds_stages);
+  const long long lds = (long long)(reg_ring ? 2 : c.lds_stages) * (c.block_m + c.block_n) * c.block_k *
                         (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_F32 ? 4 : 2);
   if (lds > kLdsLimit) return fail(MI_E_LDS, "LDS %lld bytes > %d", lds, kLdsLimit);
   const mi::MiEntry* e = find(kernel_id, c);
@@ -112,7 +116,9 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
     if (M % 8 || N % 8) return fail(MI_E_ALIGN, "M=%d and N=%d must be multiples of 8", M, N);
     if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 && K % 8)
       return fail(MI_E_ALIGN, "K=%d must be a multiple of 8 for rmsnorm_matmul", K);
-    const unsigned long long kpad = (unsigned long long)K + (unsigned long long)c.block_k;
+    // Loads run up to one tile (the ring depth, for variant 2) past K.
+    const unsigned long long kpad =
+        (unsigned long long)K + (unsigned long long)c.block_k * (unsigned long long)(reg_ring ? c.lds_stages + 1 : 1);
     const unsigned long long mpad = (unsigned long long)M + (unsigned long long)c.block_m;
     unsigned long long a_span, b_span;
     if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16) {

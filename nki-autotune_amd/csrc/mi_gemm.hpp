@@ -370,6 +370,24 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_kernel(const uint
 // reads -- or reads stuck behind a run of MFMAs -- idles the matrix core).
 // Masks: 0x008 MFMA, 0x100 DS read; the trailing sched_barrier closes the
 // region so the next sub-step gets its own pattern.
+// General form: per MFMA also a share of NV VALU instructions and NW LDS
+// writes (masks 0x002 VALU, 0x200 DS write).
+template <int NM, int NR, int NV, int NW, int M = 0>
+__device__ __forceinline__ void interleave_mfma_mix() {
+  if constexpr (M < NM) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    constexpr int r = NR / NM + (M < NR % NM ? 1 : 0);
+    constexpr int v = NV / NM + (M < NV % NM ? 1 : 0);
+    constexpr int w = NW / NM + (M < NW % NM ? 1 : 0);
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x002, v, 0);
+    if constexpr (w > 0) __builtin_amdgcn_sched_group_barrier(0x200, w, 0);
+    interleave_mfma_mix<NM, NR, NV, NW, M + 1>();
+  } else {
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 template <int NM, int ND, int M = 0>
 __device__ __forceinline__ void interleave_mfma_ds() {
   if constexpr (M < NM) {
@@ -797,246 +815,6 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_kernel(
     for (int i = 0; i < CPT; ++i) {
       const float t = row_allreduce<KC>(ss[i]);
       if (xact[i] && kc == 0) rms_lds[xrow[i]] = 1.0f / __builtin_sqrtf(t * inv_k + eps);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int mt = 0; mt < TM; ++mt) scale[mt] = rms_lds[wm0 + mt * 32 + (lane & 31)];
-  } else {
-#pragma unroll
-    for (int mt = 0; mt < TM; ++mt) scale[mt] = 1.0f;
-  }
-  store_tile<TM, TN, WAVES>(acc, scale, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
-}
-
-// ---------------------------------------------------------------------------
-// Fused rmsnorm_matmul, software-pipelined (variants 2 and 3).
-//
-// W panels take the matmul's path (LDS-direct loads, transposing reads).
-// x reaches LDS through registers, one K tile ahead: the loads of tile
-// t+STAGES+1 are issued at the end of tile t, and at the end of tile t+1
-// the registers are scaled by gamma (and 1/rms in the PRE variant), their
-// sum of squares is accumulated with v_dot2 (post variant), and they are
-// written to the LDS buffer tile t+1 vacated -- all between the MFMAs of
-// the last K sub-step, as the matmul interleaves its loads.  x tiles past K
-// load as zeros (buffer bounds), so the row statistics never count a tile
-// twice.  Variant 2 (PRE = false) applies 1/rms to the fp32 accumulators in
-// the epilogue; variant 3 (PRE = true) computes 1/rms in a prologue pass
-// over the block's rows and scales the rows before they reach LDS.
-// ---------------------------------------------------------------------------
-template <int BM, int BN, int BK, int WAVES, int STAGES, bool PRE>
-__global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_pipe_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ w,
-    uint16_t* __restrict__ out, int M, int N, int K, float inv_k, float eps, int group_m) {
-  using C = RmsCfg<BM, BN, BK, WAVES, STAGES>;
-  using G = typename C::G;
-  static_assert(G::ok, "illegal wave grid");
-  static_assert(BK % 32 == 0, "BK must be a multiple of 32 (even number of MFMA K steps)");
-  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
-  static_assert(C::CHUNKS % C::NT == 0, "every thread stages the same number of x chunks");
-  constexpr int TM = G::TM, TN = G::TN, KS = BK / 16, KC = C::KC, CPT = C::CPT, NT = C::NT;
-  using LB = PanelLoader<BK, BN, WAVES>;
-  constexpr int LPT = LB::LOADS_PER_TILE;
-  static_assert(STAGES == 2 || LB::EVEN, "deeper pipelines need an even panel split");
-  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
-  float* rms_lds = (float*)(smem + C::RMS_OFF);
-
-  const int tid = (int)threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  int tmi, tni;
-  tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
-  const int m0 = tmi * BM, n0 = tni * BN;
-  const int wm0 = (wave / G::WN) * G::WTM;
-  const int wn0 = (wave % G::WN) * G::WTN;
-  const bool has_gamma = gamma != nullptr;
-
-  const uint32_t x_bytes = (uint32_t)M * (uint32_t)K * 2u;
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, x_bytes);
-  const __amdgpu_buffer_rsrc_t rg = make_rsrc(has_gamma ? (const void*)gamma : (const void*)x, (uint32_t)K * 2u);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)K * (uint32_t)N * 2u);
-
-  // x chunks of this thread: chunk c = i*NT + tid is row c/KC, K chunk tid%KC.
-  const int kc = tid % KC;
-  int xrow[CPT];
-  uint32_t xoff[CPT];
-  int xlds[CPT];
-#pragma unroll
-  for (int i = 0; i < CPT; ++i) {
-    const int c = i * NT + tid;
-    xrow[i] = c / KC;
-    xoff[i] = ((uint32_t)(m0 + xrow[i]) * (uint32_t)K + (uint32_t)(8 * kc)) * 2u;
-    xlds[i] = xrow[i] * (BK * 2) + 16 * (kc ^ k_swz<BK>(xrow[i]));
-  }
-  auto load_x = [&](int kt, u32x4_t (&raw)[CPT], u32x4_t& g) {
-    const int k = kt * BK + 8 * kc;
-    const bool kin = k < K;
-#pragma unroll
-    for (int i = 0; i < CPT; ++i)
-      raw[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, kin ? xoff[i] + (uint32_t)kt * (uint32_t)(BK * 2) : x_bytes,
-                                                     0, 0);
-    if (has_gamma) g = __builtin_amdgcn_raw_buffer_load_b128(rg, kin ? (uint32_t)k * 2u : (uint32_t)K * 2u, 0, 0);
-  };
-
-  LB lb;
-  lb.init(wave, lane, n0, N);
-  const uint32_t kstep_b = (uint32_t)BK * (uint32_t)N * 2u;
-  TrFrag<BN, TN> fb;
-  fb.init(lane, wn0);
-  // A fragments: ds_read_b128 of 8 consecutive K of row wm0 + 32*t + lane%32.
-  const int xsl = ((lane & 31) / C::XD) & (KC - 1);
-  const int arow = (wm0 + (lane & 31)) * (BK * 2);
-  int akoff[KS];
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) akoff[kk] = 16 * ((2 * kk + (lane >> 5)) ^ xsl);
-
-  const int KT = (K + BK - 1) / BK;
-  auto clamp = [&](int kt) { return kt < KT ? kt : KT - 1; };
-
-  float ss[CPT], rs[CPT];
-#pragma unroll
-  for (int i = 0; i < CPT; ++i) {
-    ss[i] = 0.0f;
-    rs[i] = 1.0f;
-  }
-  if constexpr (PRE) {
-    // Prologue: full-K sum of squares of this block's rows, two tiles in flight.
-    u32x4_t ra[CPT], rb2[CPT], g;
-    load_x(0, ra, g);
-    for (int kt = 0; kt < KT; kt += 2) {
-      load_x(kt + 1, rb2, g);
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) ss[i] = sum_sq_chunk(ra[i], ss[i]);
-      load_x(kt + 2, ra, g);
-#pragma unroll
-      for (int i = 0; i < CPT; ++i) ss[i] = sum_sq_chunk(rb2[i], ss[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const float t = row_allreduce<KC>(ss[i]);
-      if (kc == 0) rms_lds[xrow[i]] = 1.0f / __builtin_sqrtf(t * inv_k + eps);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) rs[i] = rms_lds[xrow[i]];
-  }
-
-  // Scale the raw x chunks (gamma; and 1/rms in the PRE variant), add their
-  // squares to the row sums (post variant) and write them to LDS at abase.
-  auto stage_x = [&](const u32x4_t (&raw)[CPT], const u32x4_t& g, int abase) {
-    float gv[8];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      gv[2 * e] = has_gamma ? bf16lo(g[e]) : 1.0f;
-      gv[2 * e + 1] = has_gamma ? bf16hi(g[e]) : 1.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      if constexpr (!PRE) ss[i] = sum_sq_chunk(raw[i], ss[i]);
-      // gv = 1 without gamma: x * 1 rounds back to the same bf16, so one
-      // branch-free path serves both cases.
-      u32x4_t o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        if constexpr (PRE)
-          o[e] = pack_bf16x2(bf16lo(raw[i][e]) * rs[i] * gv[2 * e], bf16hi(raw[i][e]) * rs[i] * gv[2 * e + 1]);
-        else
-          o[e] = pack_bf16x2(bf16lo(raw[i][e]) * gv[2 * e], bf16hi(raw[i][e]) * gv[2 * e + 1]);
-      }
-      *(MI_LDS u32x4_t*)((MI_LDS char*)smem + abase + xlds[i]) = o;
-    }
-  };
-
-  f32x16_t acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
-
-  bf16x8_t af[2][TM], bf[2][TN];
-  constexpr int NF = TM + TN;
-  // Operand f of a K sub-step, in MFMA consumption order: A0, B0.., A1..
-  auto read_frag = [&](int stage, int kk, int buf, int f) {
-    const int abase = stage * C::STAGE_BYTES;
-    const int bbase = abase + C::A_BYTES;
-    if (f == 0 || f > TN) {
-      const int t = f == 0 ? 0 : f - TN;
-      af[buf][t] = __builtin_bit_cast(
-          bf16x8_t, *(MI_LDS u32x4_t*)((MI_LDS char*)smem + abase + arow + t * 32 * (BK * 2) + akoff[kk]));
-    } else {
-      const int t = f - 1;
-      bf[buf][t] = read_tr_frag(smem, bbase + (kk * 16) * (BN * 2) + fb.off[t],
-                                bbase + (kk * 16 + 4) * (BN * 2) + fb.off[t]);
-    }
-  };
-  auto read_frags = [&](int stage, int kk, int buf) {
-#pragma unroll
-    for (int f = 0; f < NF; ++f) read_frag(stage, kk, buf, f);
-  };
-  auto mfmas = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[buf][j], af[buf][i], acc[i][j], 0, 0, 0);
-  };
-  constexpr int ND = TM + 2 * TN;  // LDS reads per K sub-step
-
-  // Prologue: W tiles 0 .. STAGES-1 in flight; x tiles 0 .. STAGES-1 staged
-  // (their loads all in flight together); x tile STAGES loaded to registers.
-#pragma unroll
-  for (int s = 0; s < STAGES; ++s) lb.issue(rw, smem, s * C::STAGE_BYTES + C::A_BYTES, kstep_b, clamp(s));
-  u32x4_t xr[CPT], gr;
-  {
-    u32x4_t xp[STAGES][CPT], gp[STAGES];
-#pragma unroll
-    for (int s = 0; s < STAGES; ++s) load_x(s, xp[s], gp[s]);
-#pragma unroll
-    for (int s = 0; s < STAGES; ++s) stage_x(xp[s], gp[s], s * C::STAGE_BYTES);
-  }
-  load_x(STAGES, xr, gr);
-  // The staging waited for every x load issued with or before it, and so
-  // (in order) for the W tiles issued first; only x tile STAGES flies now.
-  __syncthreads();
-  read_frags(0, 0, 0);
-
-  int cur = 0;
-  for (int t = 0; t + 1 < KT; ++t) {
-    const int nxt = cur + 1 == STAGES ? 0 : cur + 1;
-#pragma unroll
-    for (int kk = 0; kk + 1 < KS; ++kk) {
-      read_frags(cur, kk + 1, (kk + 1) & 1);
-      mfmas(kk & 1);
-      interleave_mfma_ds<TM * TN, ND>();
-    }
-    // Tile t+1: W landed (tiles t+2 .. t+STAGES-1 may still fly), x staged
-    // by every wave at the previous boundary.
-    vm_wait<(STAGES - 2) * LPT>();
-    __syncthreads();
-    const int abase = cur * C::STAGE_BYTES;
-    read_frags(nxt, 0, 0);
-    stage_x(xr, gr, abase);                 // x tile t+STAGES
-    load_x(t + STAGES + 1, xr, gr);         // x tile t+STAGES+1 (zeros past K)
-    lb.issue(rw, smem, abase + C::A_BYTES, kstep_b, clamp(t + STAGES));
-    mfmas((KS - 1) & 1);
-    interleave_mfma_ds<TM * TN, ND>();
-    cur = nxt;
-  }
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) {
-    if (kk + 1 < KS) read_frags(cur, kk + 1, (kk + 1) & 1);
-    mfmas(kk & 1);
-    interleave_mfma_ds<TM * TN, ND>();
-  }
-  wait_vmem();
-  __syncthreads();  // the epilogue reuses the panel buffers
-
-  float scale[TM];
-  if constexpr (!PRE) {
-#pragma unroll
-    for (int i = 0; i < CPT; ++i) {
-      const float t = row_allreduce<KC>(ss[i]);
-      if (kc == 0) rms_lds[xrow[i]] = 1.0f / __builtin_sqrtf(t * inv_k + eps);
     }
     __syncthreads();
 #pragma unroll

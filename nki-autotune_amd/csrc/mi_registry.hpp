@@ -10,6 +10,8 @@
 
 #include "../../include/mi_kernels.h"
 #include "mi_gemm.hpp"
+#include "mi_rms_ring.hpp"
+#include "mi_mm_reg.hpp"
 
 namespace mi {
 
@@ -57,11 +59,24 @@ hipError_t launch_rms_bf16(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int W, int S, bool PRE>
-hipError_t launch_rms_pipe(const MiArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((rmsnorm_mm_bf16_pipe_kernel<BM, BN, BK, W, S, PRE>), dim3(grid_tiles(a.M, a.N, BM, BN)),
-                     dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
-                     (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
+template <int BM, int BN, int BK, int W, int PF>
+hipError_t launch_mm_reg(const MiArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((mm_lhsT_rhs_bf16_reg_kernel<BM, BN, BK, W, PF>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                     dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K,
+                     a.group_m);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int W, bool PRE>
+hipError_t launch_rms_ring(const MiArgs& a, hipStream_t s) {
+  if (a.g)
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_ring_kernel<BM, BN, BK, W, PRE, true>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
+                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
+  else
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_ring_kernel<BM, BN, BK, W, PRE, false>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
+                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
   return hipGetLastError();
 }
 
@@ -78,8 +93,13 @@ hipError_t launch_rms_pipe(const MiArgs& a, hipStream_t s) {
   template __global__ void rmsnorm_mm_bf16_kernel<BM, BN, BK, W, S, (PRE != 0)>(                            \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
 
-#define MI_RMSP_INST(BM, BN, BK, W, S, PRE)                                                                  \
-  template __global__ void rmsnorm_mm_bf16_pipe_kernel<BM, BN, BK, W, S, (PRE != 0)>(                       \
+#define MI_MMR_INST(BM, BN, BK, W, PF)                                                                          \
+  template __global__ void mm_lhsT_rhs_bf16_reg_kernel<BM, BN, BK, W, PF>(const uint16_t*, const uint16_t*,    \
+                                                                           uint16_t*, int, int, int, int);
+#define MI_RMSR_INST(BM, BN, BK, W, PRE)                                                                  \
+  template __global__ void rmsnorm_mm_bf16_ring_kernel<BM, BN, BK, W, (PRE != 0), true>(                 \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);       \
+  template __global__ void rmsnorm_mm_bf16_ring_kernel<BM, BN, BK, W, (PRE != 0), false>(                \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
 
 // Table rows; a config whose wave grid is illegal gets no instance.
@@ -93,9 +113,16 @@ hipError_t launch_rms_pipe(const MiArgs& a, hipStream_t s) {
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, PRE}, RmsCfg<BM, BN, BK, W, S>::LDS_BYTES,   \
    &launch_rms_bf16<BM, BN, BK, W, S, (PRE != 0)>},
 
-#define MI_RMSP_ROW(BM, BN, BK, W, S, PRE)                                                              \
-  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 2 + PRE}, RmsCfg<BM, BN, BK, W, S>::LDS_BYTES, \
-   &launch_rms_pipe<BM, BN, BK, W, S, (PRE != 0)>},
+// Register-ring matmul (variant 2): lds_stages carries the prefetch depth PF
+// (its LDS is always two stages).
+#define MI_MMR_ROW(BM, BN, BK, W, PF)                                                         \
+  {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, PF, 1, 0, 2}, 2 * (BM + BN) * BK * 2, \
+   &launch_mm_reg<BM, BN, BK, W, PF>},
+// Ring-pipelined fused kernel: the tile config names 2 stages (its A/W
+// double buffer); variant 2 + PRE.
+#define MI_RMSR_ROW(BM, BN, BK, W, PRE)                                                                 \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, 2, 1, 0, 2 + PRE}, RingCfg<BM, BN, BK, W>::LDS_BYTES, \
+   &launch_rms_ring<BM, BN, BK, W, (PRE != 0)>},
 
 // The BASELINE grid for one (BM, BN): BK in {32,64} x waves in {4,8} x
 // stages in {1,2}.  X is a row macro taking (BM, BN, BK, W, S, ...).
@@ -128,6 +155,7 @@ const MiEntry* table_mm_bm64(int* n);
 const MiEntry* table_mm_bm128(int* n);
 const MiEntry* table_mm_bm256(int* n);
 const MiEntry* table_mm_pipe(int* n);
+const MiEntry* table_mm_reg(int* n);
 const MiEntry* table_rms_bm64(int* n);
 const MiEntry* table_rms_bm128(int* n);
 const MiEntry* table_rms_bm256(int* n);

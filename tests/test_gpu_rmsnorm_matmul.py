@@ -107,8 +107,8 @@ def test_baseline_c3_full_size(gpu):
     rows = np.unique(np.concatenate([[0, 4095], rng.integers(0, 4096, size=24)]))
     expected = orms.closed_form(d["lhs"][rows], d["rhs"], d["gamma"])
     cfgs = [kl.TileConfig(256, 256, 64, 8, 2, variant=0), kl.TileConfig(256, 256, 64, 8, 2, variant=1),
-            kl.TileConfig(256, 256, 32, 8, 3, variant=2), kl.TileConfig(256, 256, 32, 8, 3, variant=3),
-            kl.TileConfig(256, 256, 64, 4, 2, variant=2)]
+            kl.TileConfig(256, 256, 32, 8, 2, variant=2), kl.TileConfig(256, 256, 32, 8, 2, variant=3),
+            kl.TileConfig(128, 256, 64, 4, 2, variant=2), kl.TileConfig(256, 256, 32, 4, 2, variant=3)]
     for cfg in cfgs:
         variant = cfg.variant
         out = _host(kl.rmsnorm_matmul(x, w, g, cfg=cfg))
