@@ -15,7 +15,7 @@ one launch of that kernel on inputs resident in HBM.
   rocprofv3 PMC counters (FETCH_SIZE + WRITE_SIZE, scaled by a copy-kernel
   calibration) when that measurement for the same config is recorded in
   ``profiles/traffic.json``; otherwise null.
-* ``fused``: the rmsnorm_matmul kernel at 4096^3 beside
+* ``fused``: the rmsnorm_matmul kernel at 4096^3 (benchmark config C3) beside
   the plain matmul at the same shape, each with its autotuned config.
 * ``cpu_baseline``: the CPU oracle's tile-faithful emulation of the
   reference kernel's loop nest (fp32, numpy/BLAS) on a bounded column slice
@@ -233,7 +233,7 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic: lhsT, rhs ~ U(-1,1) seed 0 rounded to bf16, resident in HBM",
         "config": {
-            "workload": "lhsT[8192,8192]·rhs[8192,8192] bf16 matmul, fp32 accumulate, bf16 out (BASELINE configs[1])",
+            "workload": "lhsT[8192,8192]·rhs[8192,8192] bf16 matmul, fp32 accumulate, bf16 out (benchmark config C2)",
             "kernel": "mm_lhsT_rhs_bf16",
             "tile_config": cfg.name,
             "autotuned": not (args.no_tune or args.only_kernel),

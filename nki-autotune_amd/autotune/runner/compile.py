@@ -9,7 +9,7 @@ means:
 1. parse the config back from the source header and check its static
    legality at the job's shape (LDS budget, wave tiling, alignment, 32-bit
    buffer offsets) through ``mi_cfg_check``;
-2. if ``libmi_kernels.so`` already holds the instance (the whole BASELINE
+2. if ``libmi_kernels.so`` already holds the instance (the whole 72-point
    grid is prebuilt), use it -- no hipcc run;
 3. otherwise build the source with hipcc for gfx950 into a per-config
    library that exports the same C ABI (``include/mi_kernels.h``).

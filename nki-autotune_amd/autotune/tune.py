@@ -30,14 +30,14 @@ from autotune.runner.compile import canonical_name, render_source
 from autotune.runner.output import ProfileOutput
 from autotune.runner.types import KernelJob
 
-# Default input distributions per kernel family (BASELINE configs 2 and 3).
+# Default input distributions per kernel family (benchmark configs C2 and C3).
 DEFAULT_DISTS = {
     "matmul_lhsT_rhs": {"lhs_T": "uniform", "rhs": "uniform"},
     "matmul_lhsT_rhs_f32": {},
     "rmsnorm_matmul": {"lhs": "normal", "gamma": "gamma"},
 }
 # Pass criterion: the reference's np.allclose form (kernel_transforms.py:592-596)
-# with rtol = 1e-2 (the BASELINE bound for bf16 inputs).  matmul keeps the
+# with rtol = 1e-2 (the bound the benchmark sets for bf16 inputs).  matmul keeps the
 # reference's absolute floor 5e-3; rmsnorm_matmul scales it with the output
 # (1e-2 * RMS), since rounding the normalised rows to bf16 -- which the
 # reference kernel does as well -- leaves ~1e-3 * RMS of absolute error.
@@ -159,7 +159,7 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--shape", nargs=3, type=int, metavar=("M", "N", "K"), default=[8192, 8192, 8192])
     ap.add_argument("--cache", default="", help="cache dir for sources / results.json (empty: none)")
     ap.add_argument("--grid", choices=["compiled", "baseline"], default="compiled",
-                    help="compiled: every prebuilt config; baseline: the 72-point BASELINE grid (JIT-built if needed)")
+                    help="compiled: every prebuilt config; baseline: the 72-point search grid (JIT-built if needed)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--reps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)

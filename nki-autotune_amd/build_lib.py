@@ -32,7 +32,8 @@ HIPCC_FLAGS = [
     "-O3",
     "-std=c++17",
     "-fPIC",
-    # Packed-FP32 VALU forms stay off ("build flags").
+    # Packed-FP32 VALU forms stay off: some of them have produced silently
+    # wrong results on MI355X.
     "-Xclang",
     "-target-feature",
     "-Xclang",

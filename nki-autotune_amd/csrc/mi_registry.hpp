@@ -12,6 +12,9 @@
 #include "mi_gemm.hpp"
 #include "mi_rms_ring.hpp"
 #include "mi_mm_reg.hpp"
+#include "mi_rms_xreg.hpp"
+#include "mi_rms_direct.hpp"
+#include "mi_rms_xpair.hpp"
 
 namespace mi {
 
@@ -80,6 +83,47 @@ hipError_t launch_rms_ring(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int BM, int BN, int BK, int W, int S, int XS>
+hipError_t launch_rms_xreg(const MiArgs& a, hipStream_t s) {
+  if (a.g)
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, true>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
+                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
+  else
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, false>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
+                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int W, int S, int WMX, int D>
+hipError_t launch_rms_direct(const MiArgs& a, hipStream_t s) {
+  if (a.g)
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_direct_kernel<BM, BN, BK, W, S, WMX, D, true>),
+                       dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
+                       (const uint16_t*)a.g, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps,
+                       a.group_m);
+  else
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_direct_kernel<BM, BN, BK, W, S, WMX, D, false>),
+                       dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
+                       (const uint16_t*)a.g, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps,
+                       a.group_m);
+  return hipGetLastError();
+}
+
+template <int BM, int BN, int BK, int W, int S>
+hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
+  if (a.g)
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_xpair_kernel<BM, BN, BK, W, S, true>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
+                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
+  else
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_xpair_kernel<BM, BN, BK, W, S, false>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
+                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
+  return hipGetLastError();
+}
+
 // Explicit instantiation of one config's kernel (namespace scope); every
 // table row needs its kernel instantiated in the same translation unit so
 // the host launch stub is emitted there.
@@ -100,6 +144,27 @@ hipError_t launch_rms_ring(const MiArgs& a, hipStream_t s) {
   template __global__ void rmsnorm_mm_bf16_ring_kernel<BM, BN, BK, W, (PRE != 0), true>(                 \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);       \
   template __global__ void rmsnorm_mm_bf16_ring_kernel<BM, BN, BK, W, (PRE != 0), false>(                \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
+
+// Variant 4 stages x through a 2-slot register ring, variant 5 a 3-slot one.
+#define MI_RMSX_INST(BM, BN, BK, W, S, XS)                                                            \
+  template __global__ void rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, true>(                  \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int); \
+  template __global__ void rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, false>(                 \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
+
+// x operand straight to registers: variant 6 + (D-2) + 2*(wave grid transposed).
+#define MI_RMSD_INST(BM, BN, BK, W, S, WMX, D, V)                                                     \
+  template __global__ void rmsnorm_mm_bf16_direct_kernel<BM, BN, BK, W, S, WMX, D, true>(             \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int); \
+  template __global__ void rmsnorm_mm_bf16_direct_kernel<BM, BN, BK, W, S, WMX, D, false>(            \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
+
+// x loaded two K tiles per instruction (variant 10).
+#define MI_RMSP_INST(BM, BN, BK, W, S)                                                                \
+  template __global__ void rmsnorm_mm_bf16_xpair_kernel<BM, BN, BK, W, S, true>(                      \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int); \
+  template __global__ void rmsnorm_mm_bf16_xpair_kernel<BM, BN, BK, W, S, false>(                     \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
 
 // Table rows; a config whose wave grid is illegal gets no instance.
@@ -124,7 +189,19 @@ hipError_t launch_rms_ring(const MiArgs& a, hipStream_t s) {
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, 2, 1, 0, 2 + PRE}, RingCfg<BM, BN, BK, W>::LDS_BYTES, \
    &launch_rms_ring<BM, BN, BK, W, (PRE != 0)>},
 
-// The BASELINE grid for one (BM, BN): BK in {32,64} x waves in {4,8} x
+#define MI_RMSX_ROW(BM, BN, BK, W, S, XS)                                                                   \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 2 + XS}, XregCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_rms_xreg<BM, BN, BK, W, S, XS>},
+
+#define MI_RMSD_ROW(BM, BN, BK, W, S, WMX, D, V)                                                         \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, V}, DirectCfg<BM, BN, BK, W, S, WMX>::LDS_BYTES, \
+   &launch_rms_direct<BM, BN, BK, W, S, WMX, D>},
+
+#define MI_RMSP_ROW(BM, BN, BK, W, S)                                                                \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 10}, XpairCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_rms_xpair<BM, BN, BK, W, S>},
+
+// The 72-point search grid for one (BM, BN): BK in {32,64} x waves in {4,8} x
 // stages in {1,2}.  X is a row macro taking (BM, BN, BK, W, S, ...).
 #define MI_GRID_BK_W_S(X, BM, BN, ...) \
   X(BM, BN, 32, 4, 1 __VA_ARGS__)      \
@@ -156,6 +233,9 @@ const MiEntry* table_mm_bm128(int* n);
 const MiEntry* table_mm_bm256(int* n);
 const MiEntry* table_mm_pipe(int* n);
 const MiEntry* table_mm_reg(int* n);
+const MiEntry* table_rms_xreg(int* n);
+const MiEntry* table_rms_direct(int* n);
+const MiEntry* table_rms_xpair(int* n);
 const MiEntry* table_rms_bm64(int* n);
 const MiEntry* table_rms_bm128(int* n);
 const MiEntry* table_rms_bm256(int* n);

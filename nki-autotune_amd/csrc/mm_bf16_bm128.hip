@@ -1,4 +1,4 @@
-// Instances of mm_lhsT_rhs_bf16 with block_m = 128 (BASELINE grid rows).
+// Instances of mm_lhsT_rhs_bf16 with block_m = 128 (rows of the 72-point search grid).
 #include "mi_registry.hpp"
 
 namespace mi {

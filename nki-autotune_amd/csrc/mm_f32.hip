@@ -1,4 +1,4 @@
-// mm_f32.hip -- fp32 out[M,N] = lhsT[K,M]^T . rhs[K,N].
+// mm_f32.hip -- fp32 out[M,N] = lhsT[K,M]^T . rhs[K,N] (benchmark config C1).
 //
 // This is the fp32 semantics the reference checks every kernel against
 // (simulate_fp32 rewrites all dtypes to fp32;

@@ -24,7 +24,7 @@ KERNEL_IDS = {
     "rmsnorm_matmul": _lib.MI_KERNEL_RMSNORM_MATMUL_BF16,
 }
 
-# The BASELINE search grid (72 points before legality pruning).
+# The 72-point search grid (72 points before legality pruning).
 GRID_BLOCK_MN = (64, 128, 256)
 GRID_BLOCK_K = (32, 64)
 GRID_WAVES = (4, 8)
@@ -108,7 +108,7 @@ def compiled_configs(func_name: str) -> list[TileConfig]:
 
 
 def baseline_grid(variants: tuple[int, ...] = (0,)) -> list[TileConfig]:
-    """The 72-point BASELINE grid (x variants), before legality pruning."""
+    """The 72-point search grid (x variants), before legality pruning."""
     return [
         TileConfig(bm, bn, bk, w, s, 1, 8, v)
         for bm, bn, bk, w, s, v in itertools.product(

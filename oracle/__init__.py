@@ -30,7 +30,7 @@ textbook identity (lhs_T = I, W = I, linearity, K-split associativity,
 K-permutation invariance, scale invariance, zero rows), torch's own bf16
 rounding, and committed golden vectors (tests/golden/).  The bf16 hardware
 output of the reference is never compared by the reference itself
-(benchmark.py:135,146-153), so bf16 device parity is pinned by the BASELINE
+(benchmark.py:135,146-153), so bf16 device parity is pinned by the benchmark's
 contract (max-rel <= 1e-2 against the fp32/fp64 closed form) -- no oracle
 function is left "parity unpinned".
 """

@@ -4,7 +4,7 @@ Follows the reference's generator: ``np.random.default_rng(seed)`` and one
 draw per tensor in ``input_specs`` order
 (reference autotune/src/autotune/runner/benchmark.py:156-169, which draws
 ``standard_normal`` for every tensor) and the numerics check's draw
-(examples/tune_matmul_lhsT_rhs.py:163-165).  The BASELINE configs add
+(examples/tune_matmul_lhsT_rhs.py:163-165).  The benchmark configs add
 U(-1,1), N(0, sigma) and ``gamma = 1 + 0.1 N(0,1)``; ``dist`` selects them.
 bf16 tensors are drawn in fp32 and rounded RNE (see ``oracle.bf16``).
 """

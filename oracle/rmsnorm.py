@@ -5,7 +5,7 @@ Reference kernel: kernel_library/rmsnorm_matmul/kernel_hand_online.py.
 * :func:`closed_form` is the "vanilla two-pass" of the kernel docstring
   (:5-8): ``m = sum_k lhs^2``; ``rms = 1/sqrt(m/K + eps)`` (``scale = 1/K``,
   :213; ``EPS = 1e-6``, :195; rsqrt = ``1/np.sqrt``, nkigym/src/nkigym/ops/
-  activation.py:20-28,58-64); ``O = (lhs * rms) @ rhs``.  The BASELINE
+  activation.py:20-28,58-64); ``O = (lhs * rms) @ rhs``.  The benchmark
   config adds a ``gamma[K]`` weight on the normalised row; ``gamma=None`` is
   the reference kernel exactly (it has no gamma).  float64 throughout.
 * :func:`online` restates the kernel's single-pass recurrence (:10-17) over

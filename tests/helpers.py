@@ -12,7 +12,7 @@ from oracle import metrics
 # for fp32, test/codegen/test_render.py:49) and reports
 # max_rel = max(|a-e| / (|e| + atol)) beside it.
 #
-# bf16 matmul: allclose with the reference's atol = 5e-3 and the BASELINE's
+# bf16 matmul: allclose with the reference's atol = 5e-3 and the benchmark's
 #   rtol = 1e-2.  The kernel multiplies bf16 values exactly and accumulates in
 #   fp32, so the error is the final bf16 rounding (<= 2^-8 |e|, 8 significant
 #   bits) plus an fp32 accumulation error (~1e-4 absolute at K = 8192, far

@@ -2,7 +2,7 @@
 
 Every call goes through the C ABI of libmi_kernels.so (kernel_library.ops
 wraps mi_matmul_lhsT_rhs_*).  Small shapes compare the whole output with the
-oracle's float64 closed form; the full BASELINE sizes use sampled rows
+oracle's float64 closed form; the full benchmark sizes use sampled rows
 against the closed form plus size-independent properties (all tile configs
 bitwise equal, exact linearity under power-of-two scaling).
 """
@@ -38,7 +38,7 @@ def _kl():
 
 
 def test_c1_fp32_matches_closed_form(gpu):
-    """lhsT[512,256] . rhs[512,512], fp32 N(0,1), seed 0."""
+    """benchmark config C1: lhsT[512,256] . rhs[512,512], fp32 N(0,1), seed 0."""
     import torch
 
     d = mm_inputs(512, 256, 512, seed=0, dist="normal", dtype="float32")
@@ -132,7 +132,7 @@ def _sampled_check(out_host: np.ndarray, lhs_T: np.ndarray, rhs: np.ndarray, row
     ],
 )
 def test_bf16_baseline_shapes(gpu, M, N, K, dist):
-    """BASELINE shapes with the default (tuned) config.
+    """Benchmark shapes (C2, C4, C5) with the default (tuned) config.
 
     Sampled rows against the oracle's float64 closed form; the whole output
     against a float64 torch product of the same bf16 inputs on the GPU; and

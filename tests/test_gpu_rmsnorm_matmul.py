@@ -2,7 +2,7 @@
 
 Calls go through mi_rmsnorm_matmul_bf16 (C ABI).  The oracle is the
 two-pass closed form in float64 on the same bf16 inputs (reference
-kernel_library/rmsnorm_matmul/kernel_hand_online.py:5-8 plus the BASELINE
+kernel_library/rmsnorm_matmul/kernel_hand_online.py:5-8 plus the benchmark's
 gamma).  Tolerances are explained in tests/helpers.py.
 """
 
@@ -58,7 +58,22 @@ def test_no_gamma_is_reference_kernel(gpu):
     assert _ok(rep), rep
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3])
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+def test_no_gamma_every_variant(gpu, variant):
+    """gamma=None takes each kernel's no-gamma instance; K = 576 is not a multiple of 64."""
+    import kernel_library as kl
+
+    d = rms_inputs(256, 576, 512, seed=5, with_gamma=False)
+    x, w = _dev(d["lhs"], gpu), _dev(d["rhs"], gpu)
+    expected = orms.closed_form(d["lhs"], d["rhs"])
+    cfgs = [c for c in kl.legal_configs("rmsnorm_matmul", 256, 512, 576) if c.variant == variant]
+    assert cfgs
+    for cfg in cfgs[:: max(1, len(cfgs) // 4)]:
+        rep = rms_check(_host(kl.rmsnorm_matmul(x, w, None, cfg=cfg)), expected)
+        assert _ok(rep), (cfg, rep)
+
+
+@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
 def test_ragged_and_special_rows(gpu, variant):
     """Edge tiles (M, N not multiples of the block), K not a multiple of block_k; a zero row gives 0."""
     import torch
@@ -97,7 +112,7 @@ def test_scale_invariance_and_identity_weight(gpu):
 
 
 def test_baseline_c3_full_size(gpu):
-    """BASELINE config 3 (M=K=N=4096, gamma, eps=1e-6), both variants: sampled rows vs closed form."""
+    """Benchmark config C3 (M=K=N=4096, gamma, eps=1e-6), every variant: sampled rows vs closed form."""
     import kernel_library as kl
 
     print("C3 4096^3 rmsnorm_matmul", flush=True)
@@ -108,7 +123,12 @@ def test_baseline_c3_full_size(gpu):
     expected = orms.closed_form(d["lhs"][rows], d["rhs"], d["gamma"])
     cfgs = [kl.TileConfig(256, 256, 64, 8, 2, variant=0), kl.TileConfig(256, 256, 64, 8, 2, variant=1),
             kl.TileConfig(256, 256, 32, 8, 2, variant=2), kl.TileConfig(256, 256, 32, 8, 2, variant=3),
-            kl.TileConfig(128, 256, 64, 4, 2, variant=2), kl.TileConfig(256, 256, 32, 4, 2, variant=3)]
+            kl.TileConfig(128, 256, 64, 4, 2, variant=2), kl.TileConfig(256, 256, 32, 4, 2, variant=3),
+            kl.TileConfig(256, 256, 32, 8, 3, variant=4), kl.TileConfig(256, 256, 64, 4, 2, variant=4),
+            kl.TileConfig(256, 256, 32, 8, 3, variant=5), kl.TileConfig(256, 256, 32, 8, 2, variant=5),
+            kl.TileConfig(256, 256, 32, 8, 3, variant=6), kl.TileConfig(256, 256, 32, 8, 3, variant=9),
+            kl.TileConfig(256, 256, 32, 4, 3, variant=7), kl.TileConfig(256, 256, 32, 8, 3, variant=10),
+            kl.TileConfig(128, 256, 32, 8, 3, variant=10)]
     for cfg in cfgs:
         variant = cfg.variant
         out = _host(kl.rmsnorm_matmul(x, w, g, cfg=cfg))

@@ -152,7 +152,7 @@ def test_matmul_reference_128cube_procedure():
 
 
 @pytest.mark.parametrize("K,M,N", [(512, 256, 256),   # reference small fixture (test/transforms/_fixtures.py:36-59)
-                                   (512, 256, 512),
+                                   (512, 256, 512),   # benchmark config C1
                                    (2304, 640, 1100)])  # several K blocks, ragged M/N edge tiles
 def test_matmul_tiled_fp32_matches_closed_form(K, M, N):
     """The loop-nest emulation at fp32 is the simulate_fp32 path: allclose 5e-3 (test_render.py:49)."""
