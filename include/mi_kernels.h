@@ -26,7 +26,7 @@ extern "C" {
 /* Kernel identifiers (one per hot-path kernel family). */
 enum {
   MI_KERNEL_MATMUL_LHST_RHS_BF16 = 0, /* lhsT[K,M]^T . rhs[K,N], bf16 in/out, fp32 accumulate */
-  MI_KERNEL_MATMUL_LHST_RHS_F32 = 1,  /* same product in fp32            */
+  MI_KERNEL_MATMUL_LHST_RHS_F32 = 1,  /* same product in fp32 (benchmark config C1)            */
   MI_KERNEL_RMSNORM_MATMUL_BF16 = 2,  /* rmsnorm(x[M,K]) * gamma[K] . W[K,N], bf16 in/out     */
   MI_NUM_KERNELS = 3
 };
@@ -52,13 +52,20 @@ enum {
  * kernel_library/matmul/lhsT_rhs/kernel_hand_90.92mfu.py:107-112).
  *   block_m, block_n, block_k : workgroup tile (output rows, cols, K panel)
  *   waves                     : wavefronts (64 lanes) per workgroup
- *   lds_stages                : LDS ring depth for K panels (1 or 2)
+ *   lds_stages                : LDS ring depth for K panels (1..4); for matmul
+ *                               variant 2 the depth of its register ring
  *   split_k                   : must be 1 (reserved)
  *   group_m                   : L2 raster group height in tiles (0 = default 8)
- *   variant                   : kernel-specific; for rmsnorm_matmul 0 applies
- *                               1/rms to the fp32 accumulator after the K loop,
- *                               1 computes 1/rms in a prologue and scales the
- *                               rows while staging them into LDS.
+ *   variant                   : kernel-specific pipeline (every variant computes
+ *                               the same function):
+ *     matmul         0 plain double buffer; 1 software-pipelined LDS-direct
+ *                    loads; 2 register prefetch ring (skinny shapes)
+ *     rmsnorm_matmul 0 / 1 x scaled while staged (1/rms on the accumulators /
+ *                    from a prologue pass); 2 / 3 LDS ring of raw x; 4 / 5 x
+ *                    through a 2 / 3 tile register ring on the pipelined
+ *                    matmul core; 6..9 x loaded straight into MFMA operands
+ *                    (need K <= 16384 - D*block_k); 10 x loaded two K tiles
+ *                    per instruction (block_k 32, K <= 16384 - 4*block_k)
  */
 typedef struct {
   int block_m, block_n, block_k, waves, lds_stages, split_k, group_m, variant;
