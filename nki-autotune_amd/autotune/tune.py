@@ -127,10 +127,48 @@ def check_numerics(func_name: str, cfg, M: int, N: int, K: int, seed: int = 0, d
     return rep
 
 
+def refine(func_name: str, M: int, N: int, K: int, configs, seed: int = 0, dists: dict | None = None,
+           with_gamma: bool = True, warmup: int = 10, reps: int = 30, flush_bytes: int = 0,
+           rounds: int = 5) -> dict:
+    """Re-time finalists in interleaved rounds; config name -> median of the per-round medians.
+
+    A single sequential sweep drifts with the chip's clock and power state,
+    so configs within a few percent of each other can swap places depending
+    on when they ran.  Timing every finalist once per round, over several
+    rounds, exposes them all to the same conditions.
+    """
+    import statistics
+
+    import torch
+
+    from autotune.runner.benchmark import Launcher, generate_tensors, time_launches, upload
+    from kernel_library import _lib
+
+    fam = canonical_name(func_name)
+    specs = input_specs(fam, M, N, K, with_gamma=with_gamma)
+    dev = torch.device("cuda:0")
+    inputs = upload(generate_tensors(specs, seed, default_dists(fam, K) if dists is None else dists), specs, dev)
+    out = torch.empty((M, N), dtype=torch.float32 if fam.endswith("f32") else torch.bfloat16, device=dev)
+    launchers = {c.name: Launcher(_lib.lib(), fam, c, inputs, out, M, N, K) for c in configs}
+    flush = torch.empty(flush_bytes // 4, dtype=torch.float32, device=dev).zero_ if flush_bytes else None
+    per_round: dict[str, list[float]] = {n: [] for n in launchers}
+    for r in range(rounds):
+        for name, launch in launchers.items():
+            per_round[name].append(statistics.median(time_launches(launch, warmup if r == 0 else 2, reps, flush)))
+    return {name: statistics.median(v) for name, v in per_round.items()}
+
+
 def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, cache_dir: str = "",
          check: bool = True, record: bool = False, warmup: int = 10, reps: int = 50, flush_bytes: int = 0,
-         dists: dict | None = None, with_gamma: bool = True, allow_jit: bool = True) -> TuneResult:
-    """Sweep ``configs`` (default: every legal prebuilt config) at (M, N, K) and pick the fastest."""
+         dists: dict | None = None, with_gamma: bool = True, allow_jit: bool = True,
+         finalists: int = 6, rounds: int = 5) -> TuneResult:
+    """Sweep ``configs`` (default: every legal prebuilt config) at (M, N, K) and pick the fastest.
+
+    The sweep is ``profile`` (the reference's selection is the min of its
+    single-run times, examples/tune_matmul_lhsT_rhs.py:238); the ``finalists``
+    fastest prebuilt configs are then re-timed in ``rounds`` interleaved
+    rounds (``refine``) and the winner is the fastest there.
+    """
     import kernel_library as kl
     from kernel_library.config import TileConfig, record_tuned
 
@@ -143,12 +181,23 @@ def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, ca
     best_row = output.best
     if best_row is None:
         return TuneResult(None, None, output, None)
-    summary = next(r.profiler_summary for r in output.results if r.kernel_name == best_row.kernel_name)
-    best = TileConfig(**summary["config"])
+    cfg_of = {r.kernel_name: TileConfig(**r.profiler_summary["config"]) for r in output.results
+              if r.profiler_summary and "config" in r.profiler_summary}
+    best = cfg_of[best_row.kernel_name]
+    best_time = best_row.total_time_s
+    if finalists > 1 and rounds > 0:
+        ranked = sorted((r for r in output.successes if r.kernel_name in cfg_of), key=lambda r: r.total_time_s)
+        cands = [cfg_of[r.kernel_name] for r in ranked if kl.check(fam, cfg_of[r.kernel_name], M, N, K)[0] == 0]
+        cands = cands[:finalists]
+        if len(cands) > 1:
+            med = refine(fam, M, N, K, cands, seed, dists, with_gamma, warmup, max(10, reps // 2), flush_bytes,
+                         rounds)
+            name = min(med, key=med.get)
+            best, best_time = next(c for c in cands if c.name == name), med[name]
     rep = check_numerics(fam, best, M, N, K, seed, dists, with_gamma) if check else None
     if record and (rep is None or rep["pass"]):
-        record_tuned(fam, M, N, K, best, extra={"total_time_s": best_row.total_time_s, "tflops": best_row.tflops})
-    return TuneResult(best, best_row.total_time_s, output, rep)
+        record_tuned(fam, M, N, K, best, extra={"total_time_s": best_time, "tflops": 2.0 * M * N * K / best_time / 1e12})
+    return TuneResult(best, best_time, output, rep)
 
 
 def main(argv: list[str] | None = None) -> int:

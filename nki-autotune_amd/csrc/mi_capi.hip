@@ -124,7 +124,8 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
     if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16) {
       a_span = kpad * (unsigned long long)M * 2ull;
     } else {
-      a_span = mpad * (unsigned long long)K * 2ull;
+      // x loads of the fused kernels run up to 8 tiles past K on the last rows.
+      a_span = (mpad * (unsigned long long)K + 8ull * (unsigned long long)c.block_k) * 2ull;
     }
     b_span = kpad * (unsigned long long)N * 2ull;
     if (a_span > kMaxOffset || b_span > kMaxOffset)

@@ -73,6 +73,21 @@ class TileConfig:
             s += f"_v{self.variant}"
         return s
 
+    @classmethod
+    def from_name(cls, name: str) -> "TileConfig":
+        """Inverse of ``name`` (``bm256_bn256_bk32_w8_s3[_g4][_v1]``)."""
+        fields = {"bm": "block_m", "bn": "block_n", "bk": "block_k", "w": "waves", "s": "lds_stages",
+                  "g": "group_m", "v": "variant"}
+        kw = {}
+        for part in name.split("_"):
+            key = part.rstrip("0123456789")
+            if key not in fields or key == part:
+                raise ValueError(f"bad tile config name {name!r}")
+            kw[fields[key]] = int(part[len(key):])
+        if not {"block_m", "block_n", "block_k", "waves", "lds_stages"} <= kw.keys():
+            raise ValueError(f"bad tile config name {name!r}")
+        return cls(**kw)
+
     def lds_bytes(self, elem_bytes: int = 2) -> int:
         """LDS bytes of the K-panel ring (the static-legality budget)."""
         return self.lds_stages * (self.block_m + self.block_n) * self.block_k * elem_bytes
