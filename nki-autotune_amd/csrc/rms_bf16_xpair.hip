@@ -7,7 +7,8 @@
   X(256, 128, 32, 8, 3)         \
   X(128, 256, 32, 4, 3)         \
   X(128, 256, 32, 8, 3)         \
-  X(128, 128, 32, 4, 3)
+  X(128, 128, 32, 4, 3)         \
+  X(128, 512, 32, 8, 3)
 
 namespace mi {
 MI_RMS_XPAIR_CONFIGS(MI_RMSP_INST)

@@ -16,7 +16,11 @@
   X(128, 256, 64, 4, 2, 2)     \
   X(256, 128, 32, 8, 3, 3)     \
   X(256, 128, 64, 8, 2, 2)     \
-  X(128, 128, 64, 4, 2, 2)
+  X(128, 128, 64, 4, 2, 2)     \
+  X(128, 512, 32, 8, 3, 2)     \
+  X(128, 512, 32, 8, 3, 3)     \
+  X(128, 512, 32, 8, 2, 2)     \
+  X(128, 512, 32, 4, 3, 3)
 
 namespace mi {
 MI_RMS_XREG_CONFIGS(MI_RMSX_INST)
