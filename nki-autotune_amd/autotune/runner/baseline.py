@@ -21,8 +21,13 @@ BASELINE_SEED = 42
 
 def profile_torch_baseline(M: int, N: int, K: int, dtype: str = "bfloat16", seed: int = BASELINE_SEED,
                            warmup: int = 10, reps: int = 50, dists: dict | None = None,
-                           kernel_name: str = "hipblaslt_baseline") -> ProfileResult:
-    """Time ``torch.matmul(lhs_T.t(), rhs)`` (hipBLASLt) at (M, N, K)."""
+                           kernel_name: str = "hipblaslt_baseline", flush_bytes: int = 0) -> ProfileResult:
+    """Time ``torch.matmul(lhs_T.t(), rhs)`` (hipBLASLt) at (M, N, K).
+
+    ``flush_bytes`` > 0 overwrites a buffer of that size before every timed
+    launch, as the kernel sweep does, so that neither side is timed from a
+    warm L2/MALL.
+    """
     import torch
 
     specs = {"lhs_T": ((K, M), dtype), "rhs": ((K, N), dtype)}
@@ -30,11 +35,13 @@ def profile_torch_baseline(M: int, N: int, K: int, dtype: str = "bfloat16", seed
         dev = upload(generate_tensors(specs, seed, dists), specs, torch.device("cuda:0"))
         a, b = dev["lhs_T"], dev["rhs"]
         out = torch.empty((M, N), dtype=a.dtype, device=a.device)
-        times = time_launches(lambda: torch.matmul(a.t(), b, out=out), warmup, reps)
+        flush = torch.empty(flush_bytes // 4, dtype=torch.float32, device=a.device).zero_ if flush_bytes else None
+        times = time_launches(lambda: torch.matmul(a.t(), b, out=out), warmup, reps, flush)
         med = statistics.median(times)
         flops, nbytes = work_of("matmul_lhsT_rhs", M, N, K, dtype)
         summary = {"total_time": med, "min_time": min(times), "warmup": warmup, "reps": reps, "flops": flops,
-                   "bytes": nbytes, "library": "torch.matmul (hipBLASLt)", **utilisation(flops, nbytes, med, dtype)}
+                   "bytes": nbytes, "library": "torch.matmul (hipBLASLt)", "flush_bytes": flush_bytes,
+                   **utilisation(flops, nbytes, med, dtype)}
         return ProfileResult(kernel_name, f"[{M}, {N}] {dtype}", summary)
     except Exception as exc:
         return ProfileResult(kernel_name, capture_error(exc))

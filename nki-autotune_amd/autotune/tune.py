@@ -237,7 +237,7 @@ def main(argv: list[str] | None = None) -> int:
     if args.baseline and fam != "rmsnorm_matmul":
         from autotune.runner.baseline import profile_torch_baseline
 
-        b = profile_torch_baseline(M, N, K, warmup=args.warmup, reps=args.reps)
+        b = profile_torch_baseline(M, N, K, warmup=args.warmup, reps=args.reps, flush_bytes=args.flush_mib << 20)
         s = b.profiler_summary
         if s:
             print(f"[tune] hipBLASLt baseline: {s['total_time'] * 1e6:.1f} us {s['tflops']:.1f} TFLOP/s")
