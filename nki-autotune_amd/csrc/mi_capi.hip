@@ -130,13 +130,16 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
     b_span = kpad * (unsigned long long)N * 2ull;
     if (a_span > kMaxOffset || b_span > kMaxOffset)
       return fail(MI_E_RANGE, "operand spans exceed 32-bit buffer offsets (%llu, %llu bytes)", a_span, b_span);
-    // rmsnorm_matmul variants 6..10 stage gamma in LDS: K rounded up to D
-    // tiles (variants 6..9: D = 2 or 3 x tiles in registers; variant 10:
-    // rounds of 4 tiles) must fit 16384 entries.
-    if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 && c.variant >= 6 && c.variant <= 10) {
-      const long long span = (long long)(c.variant == 10 ? 4 : 2 + ((c.variant - 6) & 1)) * c.block_k;
-      if (((long long)K + span - 1) / span * span > 16384)
-        return fail(MI_E_RANGE, "K=%d exceeds the 16384 gamma entries variant %d stages in LDS", K, c.variant);
+    // rmsnorm_matmul variants 4..10 stage gamma in LDS: K rounded up to the
+    // K step the kernel walks (variants 4/5: one tile; 6..9: D = 2 or 3
+    // tiles; 10: rounds of 4 tiles) must fit the instance's gamma entries.
+    // The limit holds with or without gamma (legality is gamma-agnostic).
+    if (e->gamma_kmax > 0) {
+      const int d = c.variant == 10 ? 4 : c.variant >= 6 ? 2 + ((c.variant - 6) & 1) : 1;
+      const long long span = (long long)d * c.block_k;
+      if (((long long)K + span - 1) / span * span > e->gamma_kmax)
+        return fail(MI_E_RANGE, "K=%d exceeds the %d gamma entries variant %d stages in LDS", K, e->gamma_kmax,
+                    c.variant);
     }
   }
   if (out) *out = e;

@@ -31,6 +31,7 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
@@ -580,46 +581,41 @@ __device__ __forceinline__ float sum_sq_chunk(const u32x4_t& w, float acc) {
   return acc;
 }
 
-// The same sum kept in NA independent partial sums (NA = 1, 2 or 4): a
-// single accumulator makes a chain of 8 dependent FMAs per chunk, which
-// stalls the wave's in-order issue between its MFMAs.
-template <int NA>
-__device__ __forceinline__ void sum_sq_chunk_n(const u32x4_t& w, float (&acc)[NA]) {
-  static_assert(NA == 1 || NA == 2 || NA == 4, "1, 2 or 4 partial sums");
+// Row sums of squares (NA partial sums) and x * gamma (HG) of the 8 bf16
+// values of one chunk, in plain fp32 VALU: unpack, FMA, multiply, round.
+// (v_dot2c_f32_bf16 does a product pair per instruction, but it issues far
+// slower than FMA/multiply next to the MFMAs, so it loses overall.)
+template <int NA, bool HG>
+__device__ __forceinline__ u32x4_t scale_sumsq_chunk(const u32x4_t& x, const u32x4_t& g, float (&acc)[NA]) {
+  u32x4_t o = x;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const float lo = bf16lo(w[e]), hi = bf16hi(w[e]);
+    const float lo = bf16lo(x[e]), hi = bf16hi(x[e]);
     acc[e % NA] = __builtin_fmaf(lo, lo, acc[e % NA]);
     acc[e % NA] = __builtin_fmaf(hi, hi, acc[e % NA]);
+    if constexpr (HG) o[e] = pack_bf16x2(lo * bf16lo(g[e]), hi * bf16hi(g[e]));
   }
-}
-// v_dot2_f32_bf16: a.lo*b.lo + a.hi*b.hi + c with the two bf16 products
-// exact in fp32.  One instruction replaces two unpacks and two FMAs.
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
-}
-template <int NA>
-__device__ __forceinline__ void sum_sq_chunk_dot2(const u32x4_t& w, float (&acc)[NA]) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) acc[e % NA] = dot2_bf16(w[e], w[e], acc[e % NA]);
-}
-// a.lo*b.lo + a.hi*b.hi in the three-operand form with an inline zero
-// accumulator (the builtin with c = 0 becomes v_mov + v_dot2c).
-__device__ __forceinline__ float dot2_bf16_z(uint32_t a, uint32_t b) {
-  float r;
-  asm("v_dot2_f32_bf16 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-// x * gamma for the 8 bf16 values of a chunk, rounded back to bf16: each
-// product is a dot2 against (gamma_lo, 0) or (0, gamma_hi), so nothing is
-// unpacked.
-__device__ __forceinline__ u32x4_t scale_chunk_dot2(const u32x4_t& x, const u32x4_t& g) {
-  u32x4_t o;
-#pragma unroll
-  for (int e = 0; e < 4; ++e)
-    o[e] = pack_bf16x2(dot2_bf16(x[e], g[e] & 0x0000FFFFu, 0.0f), dot2_bf16(x[e], g[e] & 0xFFFF0000u, 0.0f));
   return o;
 }
+// The same with gamma already unpacked to fp32 (g0: values 0..3, g1: 4..7).
+template <int NA, bool HG>
+__device__ __forceinline__ u32x4_t scale_sumsq_chunk_f32g(const u32x4_t& x, const f32x4_t& g0, const f32x4_t& g1,
+                                                          float (&acc)[NA]) {
+  u32x4_t o = x;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = bf16lo(x[e]), hi = bf16hi(x[e]);
+    acc[e % NA] = __builtin_fmaf(lo, lo, acc[e % NA]);
+    acc[e % NA] = __builtin_fmaf(hi, hi, acc[e % NA]);
+    if constexpr (HG) {
+      const float glo = e < 2 ? g0[2 * e] : g1[2 * e - 4];
+      const float ghi = e < 2 ? g0[2 * e + 1] : g1[2 * e - 3];
+      o[e] = pack_bf16x2(lo * glo, hi * ghi);
+    }
+  }
+  return o;
+}
+
 template <int NA>
 __device__ __forceinline__ float sum_parts(const float (&acc)[NA]) {
   if constexpr (NA == 4) return (acc[0] + acc[1]) + (acc[2] + acc[3]);

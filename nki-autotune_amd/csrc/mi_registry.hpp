@@ -35,6 +35,7 @@ struct MiEntry {
   mi_tile_cfg cfg;
   int lds_bytes;  // static LDS of the instance
   LaunchFn launch;
+  int gamma_kmax;  // K (rounded up to the kernel's K step) whose gamma fits in LDS; 0 = no limit
 };
 
 inline int grid_tiles(int M, int N, int BM, int BN) { return ((M + BM - 1) / BM) * ((N + BN - 1) / BN); }
@@ -191,15 +192,15 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
 
 #define MI_RMSX_ROW(BM, BN, BK, W, S, XS)                                                                   \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 2 + XS}, XregCfg<BM, BN, BK, W, S>::LDS_BYTES, \
-   &launch_rms_xreg<BM, BN, BK, W, S, XS>},
+   &launch_rms_xreg<BM, BN, BK, W, S, XS>, XregCfg<BM, BN, BK, W, S>::GK_MAX},
 
 #define MI_RMSD_ROW(BM, BN, BK, W, S, WMX, D, V)                                                         \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, V}, DirectCfg<BM, BN, BK, W, S, WMX>::LDS_BYTES, \
-   &launch_rms_direct<BM, BN, BK, W, S, WMX, D>},
+   &launch_rms_direct<BM, BN, BK, W, S, WMX, D>, DirectCfg<BM, BN, BK, W, S, WMX>::GK_MAX},
 
 #define MI_RMSP_ROW(BM, BN, BK, W, S)                                                                \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 10}, XpairCfg<BM, BN, BK, W, S>::LDS_BYTES, \
-   &launch_rms_xpair<BM, BN, BK, W, S>},
+   &launch_rms_xpair<BM, BN, BK, W, S>, XpairCfg<BM, BN, BK, W, S>::GK_MAX},
 
 // The 72-point search grid for one (BM, BN): BK in {32,64} x waves in {4,8} x
 // stages in {1,2}.  X is a row macro taking (BM, BN, BK, W, S, ...).

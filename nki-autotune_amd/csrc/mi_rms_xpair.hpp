@@ -21,7 +21,7 @@
 //   A(2u+1) <- scaled from slot u%2 during tile 2u
 //   W(t)    -> stage t%STAGES, issued at the barrier that ends tile t-STAGES
 //
-// gamma is staged in LDS once (K up to 16384 after rounding).  1/rms scales
+// gamma is staged in LDS once, as fp32 (K up to 8192 after rounding).  1/rms scales
 // the fp32 accumulators in the epilogue.  Loads are inline asm with explicit
 // vmcnt waits: at barrier t each thread issues LB W loads, then (t even)
 // LX x loads, so
@@ -49,8 +49,8 @@ struct XpairCfg {
   static constexpr int MAIN_BYTES = STAGES * STAGE_BYTES;
   static constexpr int EPI_BYTES = WAVES * 32 * (G::WTN * 2 + 16);
   static constexpr int G_OFF = ((MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES) + 15) / 16 * 16;
-  static constexpr int GK_MAX = 16384;               // gamma entries staged in LDS (K rounded up to 4*BK)
-  static constexpr int RMS_OFF = G_OFF + GK_MAX * 2;
+  static constexpr int GK_MAX = 8192;                // fp32 gamma entries staged in LDS (K rounded up to 4*BK)
+  static constexpr int RMS_OFF = G_OFF + GK_MAX * 4;
   static constexpr int LDS_BYTES = RMS_OFF + BM * 4;
   static_assert(BK == 32, "pairs of 64-byte row segments fill 128-byte lines at BK = 32");
   static_assert(CP >= 2 && CP % 2 == 0, "pair loads are swapped two by two");
@@ -94,9 +94,15 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xpair_kernel(
 
   if constexpr (HG) {
     const __amdgpu_buffer_rsrc_t rg = make_rsrc(gamma, (uint32_t)K * 2u);
-    for (int c = tid; c < KTP * BK / 8; c += WAVES * 64)
-      *(MI_LDS u32x4_t*)((MI_LDS char*)smem + C::G_OFF + 16 * c) =
-          __builtin_amdgcn_raw_buffer_load_b128(rg, 16u * (uint32_t)c, 0, 0);
+    for (int c = tid; c < KTP * BK / 8; c += WAVES * 64) {
+      const u32x4_t g = __builtin_amdgcn_raw_buffer_load_b128(rg, 16u * (uint32_t)c, 0, 0);
+      MI_LDS float* d = (MI_LDS float*)((MI_LDS char*)smem + C::G_OFF) + 8 * c;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        d[2 * e] = bf16lo(g[e]);
+        d[2 * e + 1] = bf16hi(g[e]);
+      }
+    }
   }
 
   // ---- x pair loads: load i of this wave covers rows 8*(wave*CP + i) .. +8;
@@ -161,23 +167,27 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xpair_kernel(
   for (int h = 0; h < NH; ++h)
 #pragma unroll
     for (int a = 0; a < NSA; ++a) ss[h][a] = 0.0f;
-  auto scale_one = [&](int j, int h, int H, auto slot_c, int stage) {
-    constexpr int P = decltype(slot_c)::value;
-    const u32x4_t raw = xr[P][2 * h + H];
-    sum_sq_chunk_dot2<NSA>(raw, ss[h]);
-    u32x4_t o = raw;
+  // gamma of tile j for this lane's K chunk (8 fp32): every register of a
+  // tile shares it, so it is read once per tile.
+  f32x4_t g0 = {}, g1 = {};
+  auto gamma_of = [&](int j) {
     if constexpr (HG) {
-      const u32x4_t g = *(MI_LDS u32x4_t*)((MI_LDS char*)smem + C::G_OFF + 2 * (j * BK + 8 * kc));
-      o = scale_chunk_dot2(raw, g);
+      const MI_LDS f32x4_t* gp = (const MI_LDS f32x4_t*)((MI_LDS char*)smem + C::G_OFF + 4 * (j * BK + 8 * kc));
+      g0 = gp[0];
+      g1 = gp[1];
     }
+  };
+  auto scale_one = [&](int h, int H, auto slot_c, int stage) {
+    constexpr int P = decltype(slot_c)::value;
+    const u32x4_t o = scale_sumsq_chunk_f32g<NSA, HG>(xr[P][2 * h + H], g0, g1, ss[h]);
     *(MI_LDS u32x4_t*)((MI_LDS char*)smem + stage * C::STAGE_BYTES + xlds[h]) = o;
   };
-  auto scale_step = [&](int j, int s, int H, auto slot_c, int stage) {
+  auto scale_step = [&](int s, int H, auto slot_c, int stage) {
 #pragma unroll
-    for (int h = s; h < NH; h += KS) scale_one(j, h, H, slot_c, stage);
+    for (int h = s; h < NH; h += KS) scale_one(h, H, slot_c, stage);
   };
   constexpr int CPS = (NH + KS - 1) / KS;  // registers scaled per sub-step (at most)
-  constexpr int VPC = HG ? 36 : 16;        // VALU per chunk (unpack, squares, scale, pack)
+  constexpr int VPC = HG ? 28 : 16;        // VALU per chunk (unpack, squares, scale, pack)
 
   // ---- MFMA operands (A: ds_read_b128 of 8 consecutive K of one row).
   const int xsl = ((lane & 31) / C::XD) & (KC - 1);
@@ -237,8 +247,9 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xpair_kernel(
   x_ready(S1{});
   __syncthreads();  // gamma in LDS
   swap_pair(S0{});
+  gamma_of(0);
 #pragma unroll
-  for (int s = 0; s < KS; ++s) scale_step(0, s, 0, S0{}, 0);
+  for (int s = 0; s < KS; ++s) scale_step(s, 0, S0{}, 0);
   __syncthreads();
   read_frags(0, 0, 0);
 
@@ -262,17 +273,18 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xpair_kernel(
       vm_wait<X_WAIT>();
       x_ready(SP{});
     }
+    gamma_of(t + 1);
 #pragma unroll
     for (int kk = 0; kk + 1 < KS; ++kk) {
       read_frags(cur, kk + 1, (kk + 1) & 1);
       if (kk == 0 && H == 0) swap_pair(SP{});
-      scale_step(t + 1, kk, H, SP{}, nxt);
+      scale_step(kk, H, SP{}, nxt);
       mfma_rows(kk & 1, 0, TM);
-      interleave_mfma_mix<TM * TN, ND + (HG ? CPS : 0), CPS * VPC + (H == 0 ? 4 * NH : 0), 0>();
+      interleave_mfma_mix<TM * TN, ND + (HG ? 2 : 0), CPS * VPC + (H == 0 ? 4 * NH : 0), 0>();
     }
-    scale_step(t + 1, KS - 1, H, SP{}, nxt);
+    scale_step(KS - 1, H, SP{}, nxt);
     mfma_rows((KS - 1) & 1, 0, TM / 2);
-    interleave_mfma_mix<(TM / 2) * TN, HG ? CPS : 0, CPS * VPC, 0>();
+    interleave_mfma_mix<(TM / 2) * TN, 0, CPS * VPC, 0>();
     vm_wait<B_WAIT>();  // this wave's W(t+1) landed
     __syncthreads();    // every wave's W(t+1) and A(t+1) are in LDS
     const int kw = clamp(t + STAGES);

@@ -9,7 +9,7 @@
 // an XS-slot register ring (XS = 2: variant 4, XS = 3: variant 5), so it
 // crosses LDS once, already scaled:
 //
-//   tile j's x (+ gamma chunk) -> register slot j%XS, issued at the barrier
+//   tile j's x                  -> register slot j%XS, issued at the barrier
 //                                 that ends tile j-1-XS
 //   tile j's A panel            <- x * gamma (bf16), written by every thread
 //                                 into stage j%STAGES during tile j-1, spread
@@ -20,6 +20,8 @@
 //
 // 1/rms is known only after the last tile, so it scales the fp32
 // accumulators in the epilogue (out row m = inv_rms[m] * (x*gamma . W)[m]).
+// gamma is staged in LDS once, as fp32 (K up to GK_MAX), so scaling needs
+// no unpacking of gamma and no per-tile gamma load.
 //
 // Both loads are issued as inline asm, so the compiler inserts no vmcnt
 // waits of its own: the kernel waits with exact counts (the memory system
@@ -52,8 +54,14 @@ struct XregCfg {
   static constexpr int MAIN_BYTES = STAGES * STAGE_BYTES;
   static constexpr int EPI_BYTES = WAVES * 32 * (G::WTN * 2 + 16);
   static constexpr int RMS_OFF = ((MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES) + 15) / 16 * 16;
-  static constexpr int LDS_BYTES = RMS_OFF + BM * 4;
+  static constexpr int G_OFF = RMS_OFF + BM * 4;     // fp32 gamma, GK_MAX entries
+  // fp32 gamma entries (K rounded up to BK): 8192, or what the LDS left
+  // beside the panels holds.
+  static constexpr int GK_FIT = (160 * 1024 - G_OFF) / 4 / BK * BK;
+  static constexpr int GK_MAX = GK_FIT < 8192 ? GK_FIT : 8192;
+  static constexpr int LDS_BYTES = G_OFF + GK_MAX * 4;
   static_assert(CHUNKS % NT == 0 && CPT >= 1, "every thread owns the same number of x chunks");
+  static_assert(GK_MAX % BK == 0, "gamma capacity in whole K tiles");
   static_assert(NT % KC == 0, "row lanes must not straddle threads");
 };
 
@@ -81,11 +89,11 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   using LB = PanelLoader<BK, BN, WAVES>;
   static_assert(LB::EVEN, "every wave issues the same number of W loads");
   constexpr int NLB = LB::LOADS_PER_TILE;
-  constexpr int NLX = CPT + (HG ? 1 : 0);
+  constexpr int NLX = CPT;
   constexpr int X_WAIT = (XS - 1) * (NLB + NLX);
   constexpr int B_WAIT = NLX + (STAGES - 2) * (NLB + NLX);
   static_assert(X_WAIT < 64 && B_WAIT < 64, "vmcnt is 6 bits");
-  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+  __shared__ __attribute__((aligned(1024))) char smem[HG ? C::LDS_BYTES : C::G_OFF];
   float* rms_lds = (float*)(smem + C::RMS_OFF);
 
   const int tid = (int)threadIdx.x;
@@ -100,10 +108,26 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
 
   const uint32_t x_bytes = (uint32_t)M * (uint32_t)K * 2u;
   const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, x_bytes);
-  const __amdgpu_buffer_rsrc_t rg = make_rsrc(HG ? (const void*)gamma : (const void*)x, (uint32_t)K * 2u);
   const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)K * (uint32_t)N * 2u);
   const int KT = (K + BK - 1) / BK;
   auto clamp = [&](int kt) { return kt < KT ? kt : KT - 1; };
+
+  // gamma -> LDS as fp32 (zeros past K, up to the last tile), with ordinary
+  // loads before any asynchronous load is issued; published by the barrier
+  // before the first scaling.
+  if constexpr (HG) {
+    const __amdgpu_buffer_rsrc_t rg = make_rsrc(gamma, (uint32_t)K * 2u);
+    for (int c = tid; c < KT * BK / 8; c += NT) {
+      const u32x4_t g = __builtin_amdgcn_raw_buffer_load_b128(rg, 16u * (uint32_t)c, 0, 0);
+      MI_LDS float* d = (MI_LDS float*)((MI_LDS char*)smem + C::G_OFF) + 8 * c;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        d[2 * e] = bf16lo(g[e]);
+        d[2 * e + 1] = bf16hi(g[e]);
+      }
+    }
+    __syncthreads();
+  }
 
   // ---- x chunks of this thread: c = i*NT + tid -> row c/KC, K chunk tid%KC.
   // Chunks past K (and rows past M) fall outside the buffer and read zeros.
@@ -117,23 +141,17 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
     xoff[i] = ((uint32_t)(m0 + xrow[i]) * (uint32_t)K + (uint32_t)(8 * kc)) * 2u;
     xlds[i] = xrow[i] * (BK * 2) + 16 * (kc ^ k_swz<BK>(xrow[i]));
   }
-  u32x4_t xr[XS][CPT], gr[XS];
-  // x load q (< NLX) of tile kt into register slot P: chunks, then gamma.
+  u32x4_t xr[XS][CPT];
+  // x load q (< NLX) of tile kt into register slot P.
   auto issue_x = [&](int q, int kt, auto slot_c) {
     constexpr int P = decltype(slot_c)::value;
-    const uint32_t k = (uint32_t)(kt * BK + 8 * kc);
-    const bool kin = k < (uint32_t)K;
-    if (q < CPT) {
-      xr[P][q] = vload16(rx, kin ? xoff[q] + (uint32_t)kt * (uint32_t)(BK * 2) : x_bytes);
-    } else if constexpr (HG) {
-      gr[P] = vload16(rg, kin ? k * 2u : (uint32_t)K * 2u);
-    }
+    const bool kin = kt * BK + 8 * kc < K;
+    xr[P][q] = vload16(rx, kin ? xoff[q] + (uint32_t)kt * (uint32_t)(BK * 2) : x_bytes);
   };
   auto x_ready = [&](auto slot_c) {
     constexpr int P = decltype(slot_c)::value;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) reg_ready(xr[P][i]);
-    if constexpr (HG) reg_ready(gr[P]);
   };
 
   LB lb;
@@ -154,12 +172,19 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   for (int i = 0; i < CPT; ++i)
 #pragma unroll
     for (int a = 0; a < NSA; ++a) ss[i][a] = 0.0f;
+  // gamma of tile j for this thread's K chunk (8 fp32): every chunk of the
+  // thread shares it (NT is a multiple of KC), so it is read once per tile.
+  f32x4_t g0 = {}, g1 = {};
+  auto gamma_of = [&](int j) {
+    if constexpr (HG) {
+      const MI_LDS f32x4_t* gp = (const MI_LDS f32x4_t*)((MI_LDS char*)smem + C::G_OFF + 4 * (j * BK + 8 * kc));
+      g0 = gp[0];
+      g1 = gp[1];
+    }
+  };
   auto scale_chunk = [&](int i, auto slot_c, int stage) {
     constexpr int P = decltype(slot_c)::value;
-    const u32x4_t raw = xr[P][i];
-    sum_sq_chunk_dot2<NSA>(raw, ss[i]);
-    u32x4_t o = raw;
-    if constexpr (HG) o = scale_chunk_dot2(raw, gr[P]);
+    const u32x4_t o = scale_sumsq_chunk_f32g<NSA, HG>(xr[P][i], g0, g1, ss[i]);
     *(MI_LDS u32x4_t*)((MI_LDS char*)smem + stage * C::STAGE_BYTES + xlds[i]) = o;
   };
   auto scale_step = [&](int s, auto slot_c, int stage) {
@@ -167,7 +192,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
     for (int i = s; i < CPT; i += KS) scale_chunk(i, slot_c, stage);
   };
   constexpr int CPS = (CPT + KS - 1) / KS;    // chunks per sub-step (at most)
-  constexpr int VPC = HG ? 36 : 16;           // VALU per chunk (unpack, squares, scale, pack)
+  constexpr int VPC = HG ? 28 : 16;           // VALU per chunk (unpack, squares, scale, pack)
 
   // ---- MFMA operands (A: ds_read_b128 of 8 consecutive K of one row).
   const int xsl = ((lane & 31) / C::XD) & (KC - 1);
@@ -235,6 +260,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   }
   wait_vmem();
   x_ready(S0{});
+  gamma_of(0);
 #pragma unroll
   for (int s = 0; s < KS; ++s) scale_step(s, S0{}, 0);
   __syncthreads();
@@ -254,12 +280,13 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
     // unplaced so that each follows its own VALU chain.
     vm_wait<X_WAIT>();
     x_ready(slot_c);
+    gamma_of(t + 1);
 #pragma unroll
     for (int kk = 0; kk + 1 < KS; ++kk) {
       read_frags(cur, kk + 1, (kk + 1) & 1);
       scale_step(kk, slot_c, nxt);
       mfma_rows(kk & 1, 0, TM);
-      interleave_mfma_mix<TM * TN, ND, CPS * VPC, 0>();
+      interleave_mfma_mix<TM * TN, ND + (HG ? 2 : 0), CPS * VPC, 0>();
     }
     scale_step(KS - 1, slot_c, nxt);
     mfma_rows((KS - 1) & 1, 0, TM / 2);

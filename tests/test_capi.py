@@ -59,8 +59,13 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (RMS, TileConfig(128, 128, 64, 8, 2), (1024, 1024, 1020), _lib.MI_E_ALIGN),      # K % 8 (fused)
         (MM, TileConfig(128, 128, 64, 4, 2), (65536, 65536, 65536), _lib.MI_E_RANGE),    # 8 GiB operand
         (RMS, TileConfig(256, 256, 32, 8, 3, variant=6), (1024, 1024, 16392), _lib.MI_E_RANGE),   # gamma > LDS
-        (RMS, TileConfig(256, 256, 32, 8, 3, variant=10), (1024, 1024, 16392), _lib.MI_E_RANGE),
-        (RMS, TileConfig(256, 256, 32, 8, 3, variant=10), (1024, 1024, 16384), _lib.MI_OK),
+        (RMS, TileConfig(256, 256, 32, 8, 3, variant=10), (1024, 1024, 8200), _lib.MI_E_RANGE),   # 8192 fp32
+        (RMS, TileConfig(256, 256, 32, 8, 3, variant=10), (1024, 1024, 8192), _lib.MI_OK),
+        (RMS, TileConfig(256, 256, 32, 8, 3, variant=5), (1024, 1024, 8200), _lib.MI_E_RANGE),
+        (RMS, TileConfig(256, 256, 32, 8, 3, variant=5), (1024, 1024, 8192), _lib.MI_OK),
+        # four 32 KiB stages leave room for 7936 fp32 gamma entries
+        (RMS, TileConfig(256, 256, 32, 8, 4, variant=4), (1024, 1024, 7968), _lib.MI_E_RANGE),
+        (RMS, TileConfig(256, 256, 32, 8, 4, variant=4), (1024, 1024, 7936), _lib.MI_OK),
         (MM, TileConfig(128, 128, 48, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),
         (MM, TileConfig(512, 512, 32, 8, 1), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),  # legal, not prebuilt
         (MM, TileConfig(0, 128, 64, 4, 2), (1024, 1024, 1024), _lib.MI_E_ARGS),
