@@ -24,6 +24,10 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <numeric>
+#include <type_traits>
+#include <utility>
+
 namespace mi {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -41,6 +45,36 @@ typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kRsrcWord3 = 0x00020000;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, kRsrcWord3);
+}
+// f(std::integral_constant<int, i>{}) for i = 0 .. N-1, unrolled: loop
+// bodies whose LDS stage is a compile-time constant address their operands
+// with immediate offsets.
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+// f(integral_constant<I>) for I = 0, 1, ... while it returns true (at most
+// N calls).  The calls nest, so no control-flow path runs call i+1 after
+// skipping call i (wait counts that assume every earlier call hold on
+// every path).
+template <int N, int I = 0, class F>
+__device__ __forceinline__ void static_while(F&& f) {
+  if constexpr (I < N) {
+    if (f(std::integral_constant<int, I>{})) static_while<N, I + 1>(f);
+  }
+}
+
+// Descriptor of bytes [off, bytes) of p (off <= bytes, wave-uniform).  A
+// K tile's offset rides in the scalar base address, so the per-lane offsets
+// stay the same for every tile and a load needs no vector add; loads past
+// the end still read zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc_from(const void* p, uint32_t bytes, uint32_t off) {
+  off = __builtin_amdgcn_readfirstlane(off);  // keeps the descriptor in SGPRs
+  return make_rsrc((const char*)p + off, bytes - off);
 }
 
 // s_waitcnt vmcnt(0): every outstanding vector-memory load (including the
@@ -173,6 +207,11 @@ struct PanelLoader {
   __device__ __forceinline__ void issue_one(int j, __amdgpu_buffer_rsrc_t rs, char* smem, int base,
                                             uint32_t kstep_bytes, int kt) const {
     if (EVEN || active[j]) lds_dma16(rs, smem + base + lds_off[j], voff[j] + (uint32_t)kt * kstep_bytes);
+  }
+  // Load j of the K tile that the descriptor `rs_kt` starts at
+  // (make_rsrc_from with the tile's byte offset).
+  __device__ __forceinline__ void issue_at(int j, __amdgpu_buffer_rsrc_t rs_kt, char* smem, int base) const {
+    if (EVEN || active[j]) lds_dma16(rs_kt, smem + base + lds_off[j], voff[j]);
   }
   // Number of LDS-direct loads one wave issues per K tile.
   static constexpr int LOADS_PER_TILE = PER_WAVE;
@@ -453,8 +492,8 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
   const int wm0 = (wave / G::WN) * G::WTM;
   const int wn0 = (wave % G::WN) * G::WTN;
 
-  const __amdgpu_buffer_rsrc_t ra = make_rsrc(lhsT, (uint32_t)K * (uint32_t)M * 2u);
-  const __amdgpu_buffer_rsrc_t rb = make_rsrc(rhs, (uint32_t)K * (uint32_t)N * 2u);
+  const uint32_t a_bytes = (uint32_t)K * (uint32_t)M * 2u;
+  const uint32_t b_bytes = (uint32_t)K * (uint32_t)N * 2u;
   LA la;
   LB lb;
   la.init(wave, lane, m0, M);
@@ -502,8 +541,11 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
   };
   // Load q (< LPT) of K tile kt into `stage`: the A loads, then the B loads.
   auto issue_one = [&](int q, int kt, int stage) {
-    if (q < LA::LOADS_PER_TILE) la.issue_one(q, ra, smem, stage * C::STAGE_BYTES, kstep_a, kt);
-    else lb.issue_one(q - LA::LOADS_PER_TILE, rb, smem, stage * C::STAGE_BYTES + C::A_BYTES, kstep_b, kt);
+    if (q < LA::LOADS_PER_TILE)
+      la.issue_at(q, make_rsrc_from(lhsT, a_bytes, (uint32_t)kt * kstep_a), smem, stage * C::STAGE_BYTES);
+    else
+      lb.issue_at(q - LA::LOADS_PER_TILE, make_rsrc_from(rhs, b_bytes, (uint32_t)kt * kstep_b), smem,
+                  stage * C::STAGE_BYTES + C::A_BYTES);
   };
 
   const int KT = (K + BK - 1) / BK;
@@ -527,9 +569,11 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
   // workgroup, then reads tile t+1's first operands and issues tile
   // t+STAGES into the buffer tile t vacated, both between the MFMAs of the
   // sub-step.
-  int cur = 0;
-  for (int t = 0; t + 1 < KT; ++t) {
-    const int nxt = cur + 1 == STAGES ? 0 : cur + 1;
+  // Tile t sits in stage t % STAGES; the loop is unrolled STAGES times so
+  // that the stage is a compile-time constant in every body.
+  auto tile = [&](int t, auto cur_c) __attribute__((always_inline)) {
+    constexpr int cur = decltype(cur_c)::value;
+    constexpr int nxt = cur + 1 == STAGES ? 0 : cur + 1;
 #pragma unroll
     for (int kk = 0; kk + 1 < KS; ++kk) {
       read_frags(cur, kk + 1, (kk + 1) & 1);
@@ -547,8 +591,16 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
     }
     mfmas((KS - 1) & 1);
     interleave_mfma_ds<TM * TN, 2 * NF>();
-    cur = nxt;
-  }
+  };
+  int t0 = 0;
+  for (; t0 + STAGES < KT; t0 += STAGES)
+    static_for<STAGES>([&](auto s_c) __attribute__((always_inline)) { tile(t0 + s_c(), s_c); });
+  static_while<STAGES>([&](auto s_c) __attribute__((always_inline)) {
+    if (t0 + s_c() + 1 >= KT) return false;
+    tile(t0 + s_c(), s_c);
+    return true;
+  });
+  const int cur = (KT - 1) % STAGES;
   // Last tile: no further loads.
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {

@@ -107,8 +107,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   const int wn0 = (wave % G::WN) * G::WTN;
 
   const uint32_t x_bytes = (uint32_t)M * (uint32_t)K * 2u;
-  const __amdgpu_buffer_rsrc_t rx = make_rsrc(x, x_bytes);
-  const __amdgpu_buffer_rsrc_t rw = make_rsrc(w, (uint32_t)K * (uint32_t)N * 2u);
+  const uint32_t w_bytes = (uint32_t)K * (uint32_t)N * 2u;
   const int KT = (K + BK - 1) / BK;
   auto clamp = [&](int kt) { return kt < KT ? kt : KT - 1; };
 
@@ -145,8 +144,11 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   // x load q (< NLX) of tile kt into register slot P.
   auto issue_x = [&](int q, int kt, auto slot_c) {
     constexpr int P = decltype(slot_c)::value;
+    // Tiles past the end take the last tile's descriptor (offset <= size)
+    // and an offset past every descriptor's end.
     const bool kin = kt * BK + 8 * kc < K;
-    xr[P][q] = vload16(rx, kin ? xoff[q] + (uint32_t)kt * (uint32_t)(BK * 2) : x_bytes);
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc_from(x, x_bytes, (uint32_t)clamp(kt) * (uint32_t)(BK * 2));
+    xr[P][q] = vload16(rs, kin ? xoff[q] : x_bytes);
   };
   auto x_ready = [&](auto slot_c) {
     constexpr int P = decltype(slot_c)::value;
@@ -158,7 +160,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   lb.init(wave, lane, n0, N);
   const uint32_t kstep_b = (uint32_t)BK * (uint32_t)N * 2u;
   auto issue_w = [&](int q, int kt, int stage) {
-    lb.issue_one(q, rw, smem, stage * C::STAGE_BYTES + C::A_BYTES, kstep_b, kt);
+    lb.issue_at(q, make_rsrc_from(w, w_bytes, (uint32_t)kt * kstep_b), smem, stage * C::STAGE_BYTES + C::A_BYTES);
   };
   TrFrag<BN, TN> fb;
   fb.init(lane, wn0);
@@ -269,11 +271,12 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   issue_x_tile(XS);
   read_frags(0, 0, 0);
 
-  // ---- steady state.  Tile t consumes register slot (t+1)%XS (x of tile
-  // t+1) and refills it with x of tile t+1+XS at its closing barrier.
-  int cur = 0;
-  auto tile = [&](int t, auto slot_c) {
-    const int nxt = cur + 1 == STAGES ? 0 : cur + 1;
+  // ---- steady state.  Tile t sits in LDS stage t%STAGES, consumes
+  // register slot (t+1)%XS (x of tile t+1) and refills it with x of tile
+  // t+1+XS at its closing barrier.
+  auto tile = [&](int t, auto slot_c, auto stage_c) __attribute__((always_inline)) {
+    constexpr int cur = decltype(stage_c)::value;
+    constexpr int nxt = cur + 1 == STAGES ? 0 : cur + 1;
     // The wait sits at the top of the tile so that the scaling VALU, the
     // operand reads and the MFMAs of each sub-step share one scheduling
     // region (an asm statement ends a region); the LDS writes are left
@@ -307,28 +310,23 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
     }
     mfma_rows((KS - 1) & 1, TM / 2, TM);
     interleave_mfma_ds<(TM - TM / 2) * TN, ND>();
-    cur = nxt;
   };
-  // Unrolled XS times so that every slot index is a compile-time constant;
-  // tile t + s of a round consumes slot (s+1)%XS.
-  int t = 0;
-  if constexpr (XS == 2) {
-    for (; t + 2 < KT; t += 2) {
-      tile(t, S1{});
-      tile(t + 1, S0{});
-    }
-    if (t + 1 < KT) tile(t, S1{});
-  } else {
-    for (; t + 3 < KT; t += 3) {
-      tile(t, S1{});
-      tile(t + 1, S2{});
-      tile(t + 2, S0{});
-    }
-    if (t + 1 < KT) {
-      tile(t, S1{});
-      if (t + 2 < KT) tile(t + 1, S2{});
-    }
-  }
+  // Unrolled lcm(XS, STAGES) times so that every slot and stage index is a
+  // compile-time constant (LDS operands then take immediate offsets).
+  constexpr int UR = std::lcm(XS, STAGES);
+  auto round_tile = [&](int t, auto i_c) __attribute__((always_inline)) {
+    constexpr int i = decltype(i_c)::value;
+    tile(t, std::integral_constant<int, (i + 1) % XS>{}, std::integral_constant<int, i % STAGES>{});
+  };
+  int t0 = 0;
+  for (; t0 + UR < KT; t0 += UR)
+    static_for<UR>([&](auto i_c) __attribute__((always_inline)) { round_tile(t0 + i_c(), i_c); });
+  static_while<UR>([&](auto i_c) __attribute__((always_inline)) {
+    if (t0 + i_c() + 1 >= KT) return false;
+    round_tile(t0 + i_c(), i_c);
+    return true;
+  });
+  const int cur = (KT - 1) % STAGES;
   // Last tile: nothing left to scale or load.
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {

@@ -1,6 +1,7 @@
 """The asynchronous register loads of the fused kernels stay untouched until
 their wait (see tests/asm_loads.py), in the gfx950 code hipcc emits for the
-shipped instance files.  Needs hipcc, not a GPU."""
+shipped instance files; and the pipelined kernels compile to straight-line
+kernel code (no outlined calls, no scratch spills).  Needs hipcc, not a GPU."""
 
 from __future__ import annotations
 
@@ -25,15 +26,29 @@ def _hipcc():
     pytest.skip("hipcc not available")
 
 
-@pytest.mark.parametrize("unit", ["rms_bf16_xreg.hip", "rms_bf16_direct.hip", "rms_bf16_xpair.hip"])
-def test_async_register_loads_untouched_until_waited(unit, tmp_path):
+@pytest.fixture(scope="module")
+def asm_of(tmp_path_factory):
+    """unit -> gfx950 assembly text, compiled once per module."""
     import build_lib
 
-    out = tmp_path / "k.s"
-    flags = [f for f in build_lib.HIPCC_FLAGS if f != "-fPIC"]
-    subprocess.run([_hipcc(), *flags, f"-I{build_lib.INCLUDE}", "--cuda-device-only", "-S", str(CSRC / unit),
-                    "-o", str(out)], check=True, capture_output=True)
-    ks = kernels(out.read_text())
+    cache: dict[str, str] = {}
+    tmp = tmp_path_factory.mktemp("asm")
+
+    def get(unit: str) -> str:
+        if unit not in cache:
+            out = tmp / (unit + ".s")
+            flags = [f for f in build_lib.HIPCC_FLAGS if f != "-fPIC"]
+            subprocess.run([_hipcc(), *flags, f"-I{build_lib.INCLUDE}", "--cuda-device-only", "-S",
+                            str(CSRC / unit), "-o", str(out)], check=True, capture_output=True)
+            cache[unit] = out.read_text()
+        return cache[unit]
+
+    return get
+
+
+@pytest.mark.parametrize("unit", ["rms_bf16_xreg.hip", "rms_bf16_direct.hip", "rms_bf16_xpair.hip"])
+def test_async_register_loads_untouched_until_waited(unit, asm_of):
+    ks = kernels(asm_of(unit))
     assert ks
     total = 0
     for name, lines in ks.items():
@@ -41,3 +56,15 @@ def test_async_register_loads_untouched_until_waited(unit, tmp_path):
         total += n
         assert not bad, (name, bad[:3])
     assert total > 0
+
+
+@pytest.mark.parametrize("unit", ["mm_bf16_pipe.hip", "mm_bf16_reg.hip", "rms_bf16_xreg.hip", "rms_bf16_direct.hip",
+                                  "rms_bf16_xpair.hip"])
+def test_kernels_straight_line(unit, asm_of):
+    """The unrolled tile lambdas are inlined: a device-function call would
+    pass buffer descriptors in VGPRs and read captures through flat loads."""
+    ks = kernels(asm_of(unit))
+    assert ks
+    for name, lines in ks.items():
+        bad = [ln for ln in lines if ln.strip().startswith(("s_swappc", "s_setpc", "flat_load", "scratch_"))]
+        assert not bad, (name, bad[:3])
