@@ -142,7 +142,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   }
   u32x4_t xr[XS][CPT];
   // x load q (< NLX) of tile kt into register slot P.
-  auto issue_x = [&](int q, int kt, auto slot_c) {
+  auto issue_x = [&](int q, int kt, auto slot_c) __attribute__((always_inline)) {
     constexpr int P = decltype(slot_c)::value;
     // Tiles past the end take the last tile's descriptor (offset <= size)
     // and an offset past every descriptor's end.
@@ -150,7 +150,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
     const __amdgpu_buffer_rsrc_t rs = make_rsrc_from(x, x_bytes, (uint32_t)clamp(kt) * (uint32_t)(BK * 2));
     xr[P][q] = vload16(rs, kin ? xoff[q] : x_bytes);
   };
-  auto x_ready = [&](auto slot_c) {
+  auto x_ready = [&](auto slot_c) __attribute__((always_inline)) {
     constexpr int P = decltype(slot_c)::value;
 #pragma unroll
     for (int i = 0; i < CPT; ++i) reg_ready(xr[P][i]);
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   // scaled and the last group is issued after the barrier.
   //   barrier u (u = -U0 .. -1) issues W(u+STAGES), x(u+1+XS)
   constexpr int U0 = STAGES > XS + 1 ? STAGES : XS + 1;
-  auto issue_x_tile = [&](int j) {
+  auto issue_x_tile = [&](int j) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < NLX; ++q) {
       if (j % XS == 0) issue_x(q, j, S0{});

@@ -12,6 +12,7 @@
   X(256, 256, 32, 4, 4)      \
   X(256, 256, 64, 8, 2)      \
   X(256, 256, 32, 8, 3)      \
+  X(128, 512, 32, 8, 3)      \
   X(256, 128, 64, 4, 2)      \
   X(256, 128, 64, 4, 3)      \
   X(128, 256, 64, 4, 2)      \
