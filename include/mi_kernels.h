@@ -28,7 +28,8 @@ enum {
   MI_KERNEL_MATMUL_LHST_RHS_BF16 = 0, /* lhsT[K,M]^T . rhs[K,N], bf16 in/out, fp32 accumulate */
   MI_KERNEL_MATMUL_LHST_RHS_F32 = 1,  /* same product in fp32 (benchmark config C1)            */
   MI_KERNEL_RMSNORM_MATMUL_BF16 = 2,  /* rmsnorm(x[M,K]) * gamma[K] . W[K,N], bf16 in/out     */
-  MI_NUM_KERNELS = 3
+  MI_KERNEL_MATMUL_LHS_RHS_BF16 = 3,  /* lhs[M,K] . rhs[K,N], lhs K-contiguous, bf16 in/out   */
+  MI_NUM_KERNELS = 4
 };
 
 /* Legality / rejection codes (positive return values). */
@@ -37,7 +38,7 @@ enum {
   MI_E_NO_INSTANCE = 1,    /* the tile config was not compiled into this library     */
   MI_E_LDS = 2,            /* LDS bytes of the config exceed 160 KiB                 */
   MI_E_WAVE_TILE = 3,      /* a wave's share of the block is smaller than one MFMA   */
-  MI_E_ALIGN = 4,          /* M or N not a multiple of 8 (16-byte rows required)     */
+  MI_E_ALIGN = 4,          /* M or N (or K of a K-contiguous operand) not a multiple of 8 */
   MI_E_RANGE = 5,          /* an operand is 4 GiB or larger (32-bit buffer offsets)  */
   MI_E_ARGS = 6,           /* null pointer, non-positive size, bad eps               */
   MI_E_KERNEL = 7,         /* unknown kernel id                                      */
@@ -60,6 +61,7 @@ enum {
  *                               the same function):
  *     matmul         0 plain double buffer; 1 software-pipelined LDS-direct
  *                    loads; 2 register prefetch ring (skinny shapes)
+ *     matmul_lhs_rhs 0 the software-pipelined core (block_k >= 32, 2..4 stages)
  *     rmsnorm_matmul 0 / 1 x scaled while staged (1/rms on the accumulators /
  *                    from a prologue pass); 2 / 3 LDS ring of raw x; 4 / 5 x
  *                    through a 2 / 3 tile register ring on the pipelined
@@ -93,7 +95,15 @@ int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
 int mi_matmul_lhsT_rhs_bf16(const void* lhsT, const void* rhs, void* out, int M, int N, int K,
                             const mi_tile_cfg* cfg, void* stream);
 
-/* fp32 variant of the same product (the fp32 CPU-simulation semantics of
+/* out[M,N] = lhs[M,K] . rhs[K,N] with lhs row-major (K contiguous); bf16
+ * storage, fp32 accumulation over the whole K.  K must be a multiple of 8.
+ * Replaces matmul_lhs_rhs_nkigym(lhs, rhs)
+ * (reference kernel_library/matmul/lhs_rhs/kernel_handtuned_89.26mfu.py:226-287).
+ * cfg == NULL selects mi_default_config; the pipelined core is variant 0. */
+int mi_matmul_lhs_rhs_bf16(const void* lhs, const void* rhs, void* out, int M, int N, int K,
+                           const mi_tile_cfg* cfg, void* stream);
+
+/* fp32 variant of the lhsT product (the fp32 CPU-simulation semantics of
  * reference nkigym/src/nkigym/synthesis/simulate_nki.py:24-48). */
 int mi_matmul_lhsT_rhs_f32(const float* lhsT, const float* rhs, float* out, int M, int N, int K,
                            const mi_tile_cfg* cfg, void* stream);

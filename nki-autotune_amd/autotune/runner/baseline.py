@@ -21,22 +21,28 @@ BASELINE_SEED = 42
 
 def profile_torch_baseline(M: int, N: int, K: int, dtype: str = "bfloat16", seed: int = BASELINE_SEED,
                            warmup: int = 10, reps: int = 50, dists: dict | None = None,
-                           kernel_name: str = "hipblaslt_baseline", flush_bytes: int = 0) -> ProfileResult:
-    """Time ``torch.matmul(lhs_T.t(), rhs)`` (hipBLASLt) at (M, N, K).
+                           kernel_name: str = "hipblaslt_baseline", flush_bytes: int = 0,
+                           lhs_layout: str = "KM") -> ProfileResult:
+    """Time ``torch.matmul`` (hipBLASLt) of the left operand and rhs at (M, N, K).
 
-    ``flush_bytes`` > 0 overwrites a buffer of that size before every timed
-    launch, as the kernel sweep does, so that neither side is timed from a
-    warm L2/MALL.
+    ``lhs_layout`` "KM" stores the left operand as lhs_T[K,M] (the
+    matmul_lhsT_rhs layout), "MK" as lhs[M,K] (matmul_lhs_rhs: the product
+    is ``torch.matmul(lhs, rhs)``).  ``flush_bytes`` > 0 overwrites a buffer
+    of that size before every timed launch, as the kernel sweep does, so that
+    neither side is timed from a warm L2/MALL.
     """
     import torch
 
-    specs = {"lhs_T": ((K, M), dtype), "rhs": ((K, N), dtype)}
+    if lhs_layout not in ("KM", "MK"):
+        raise ValueError(f"lhs_layout must be 'KM' or 'MK', got {lhs_layout!r}")
+    specs = {"lhs_T": ((K, M), dtype)} if lhs_layout == "KM" else {"lhs": ((M, K), dtype)}
+    specs["rhs"] = ((K, N), dtype)
     try:
         dev = upload(generate_tensors(specs, seed, dists), specs, torch.device("cuda:0"))
-        a, b = dev["lhs_T"], dev["rhs"]
+        a, b = (dev["lhs_T"].t(), dev["rhs"]) if lhs_layout == "KM" else (dev["lhs"], dev["rhs"])
         out = torch.empty((M, N), dtype=a.dtype, device=a.device)
         flush = torch.empty(flush_bytes // 4, dtype=torch.float32, device=a.device).zero_ if flush_bytes else None
-        times = time_launches(lambda: torch.matmul(a.t(), b, out=out), warmup, reps, flush)
+        times = time_launches(lambda: torch.matmul(a, b, out=out), warmup, reps, flush)
         med = statistics.median(times)
         flops, nbytes = work_of("matmul_lhsT_rhs", M, N, K, dtype)
         summary = {"total_time": med, "min_time": min(times), "warmup": warmup, "reps": reps, "flops": flops,

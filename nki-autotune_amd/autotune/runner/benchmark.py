@@ -116,6 +116,10 @@ class Launcher:
             self.fn = library.mi_rmsnorm_matmul_bf16
             self.args = (x.data_ptr(), g.data_ptr() if g is not None else None, w.data_ptr(), out.data_ptr(), M, N,
                          K, float(eps), ctypes.byref(self.cfg_c), self.stream)
+        elif self.fam == "matmul_lhs_rhs":
+            a, b = vals[0], vals[1]
+            self.fn = library.mi_matmul_lhs_rhs_bf16
+            self.args = (a.data_ptr(), b.data_ptr(), out.data_ptr(), M, N, K, ctypes.byref(self.cfg_c), self.stream)
         else:
             a, b = vals[0], vals[1]
             fp32 = a.dtype == torch.float32

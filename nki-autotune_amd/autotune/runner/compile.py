@@ -38,13 +38,41 @@ COMPILE_TIMEOUT_S = 600
 # func_name aliases: the reference's kernel names map onto the MI355X families.
 ALIASES = {
     "matmul_lhsT_rhs_nkigym": "matmul_lhsT_rhs",
+    "matmul_lhs_rhs_nkigym": "matmul_lhs_rhs",
     "rmsnorm_matmul_online": "rmsnorm_matmul",
 }
 
-_INSTANCE_MACRO = {
-    "matmul_lhsT_rhs": ("MI_MM_INST", "MI_MM_ROW"),
-    "rmsnorm_matmul": ("MI_RMS_INST", "MI_RMS_ROW"),
-}
+# Kernel families a single-config library can be generated for (fp32: no).
+_JIT_FAMILIES = ("matmul_lhsT_rhs", "matmul_lhs_rhs", "rmsnorm_matmul")
+
+
+def _instance(fam: str, cfg) -> tuple[str, str, str] | None:
+    """(instantiation macro, table-row macro, macro arguments) of ``cfg``.
+
+    Mirrors the instance files under csrc/: each variant of a family is a
+    different kernel template (mi_registry.hpp).  None for a variant with no
+    template.
+    """
+    bm, bn, bk, w, s, v = cfg.block_m, cfg.block_n, cfg.block_k, cfg.waves, cfg.lds_stages, int(cfg.variant)
+    base = f"{bm}, {bn}, {bk}, {w}"
+    if fam == "matmul_lhsT_rhs":
+        macro = {0: "MI_MM", 1: "MI_MMP", 2: "MI_MMR"}.get(v)
+        return (f"{macro}_INST", f"{macro}_ROW", f"{base}, {s}") if macro else None
+    if fam == "matmul_lhs_rhs":
+        return ("MI_MMK_INST", "MI_MMK_ROW", f"{base}, {s}") if v == 0 else None
+    if fam == "rmsnorm_matmul":
+        if v in (0, 1):
+            return "MI_RMS_INST", "MI_RMS_ROW", f"{base}, {s}, {v}"
+        if v in (2, 3):  # two LDS stages are part of the template
+            return ("MI_RMSR_INST", "MI_RMSR_ROW", f"{base}, {v - 2}") if s == 2 else None
+        if v in (4, 5):
+            return "MI_RMSX_INST", "MI_RMSX_ROW", f"{base}, {s}, {v - 2}"
+        if 6 <= v <= 9:
+            d, wmx = 2 + ((v - 6) & 1), (v - 6) >> 1
+            return "MI_RMSD_INST", "MI_RMSD_ROW", f"{base}, {s}, {wmx}, {d}, {v}"
+        if v == 10:
+            return "MI_RMSP_INST", "MI_RMSP_ROW", f"{base}, {s}"
+    return None
 
 
 def canonical_name(func_name: str) -> str:
@@ -62,13 +90,11 @@ def render_source(func_name: str, cfg) -> str:
     """
     fam = canonical_name(func_name)
     head = HEADER_TAG + json.dumps({"func_name": fam, "config": cfg.asdict()}, sort_keys=True)
-    if fam not in _INSTANCE_MACRO:
-        # fp32 path: prebuilt instances only; the source is the header alone.
-        return head + "\n// prebuilt-only kernel family: no generated unit\n"
-    inst, row = _INSTANCE_MACRO[fam]
-    args = f"{cfg.block_m}, {cfg.block_n}, {cfg.block_k}, {cfg.waves}, {cfg.lds_stages}"
-    if fam == "rmsnorm_matmul":
-        args += f", {int(cfg.variant)}"
+    spec = _instance(fam, cfg) if fam in _JIT_FAMILIES else None
+    if spec is None:
+        # fp32 path, or a variant without a template: prebuilt instances only.
+        return head + "\n// prebuilt-only kernel family or variant: no generated unit\n"
+    inst, row, args = spec
     return "\n".join(
         [
             head,
@@ -155,6 +181,8 @@ def problem_shape(func_name: str, input_specs: dict) -> tuple[int, int, int]:
     fam = canonical_name(func_name)
     if fam in ("matmul_lhsT_rhs", "matmul_lhsT_rhs_f32"):
         (K, M), (K2, N) = shapes[0], shapes[1]
+    elif fam == "matmul_lhs_rhs":
+        (M, K), (K2, N) = shapes[0], shapes[1]
     elif fam == "rmsnorm_matmul":
         (M, K), (K2, N) = shapes[0], shapes[-1]
     else:
@@ -187,8 +215,11 @@ def compile_one(kernel_name: str, source: str, func_name: str, input_specs: dict
         if rc != _lib.MI_E_NO_INSTANCE:
             return CompileResult(kernel_name, src_path, "", f"illegal config {cfg.name} at M={M} N={N} K={K}: "
                                  f"[{_lib.CODE_NAMES.get(rc, rc)}] {msg}")
-        if not allow_jit or fam not in _INSTANCE_MACRO:
+        if not allow_jit:
             return CompileResult(kernel_name, src_path, "", f"config {cfg.name} is not prebuilt and JIT is off: {msg}")
+        if fam not in _JIT_FAMILIES or _instance(fam, cfg) is None:
+            return CompileResult(kernel_name, src_path, "", f"config {cfg.name} is not prebuilt and has no template "
+                                 f"to build it from: {msg}")
         out_dir = Path(work_dir) / _stem(kernel_name)
         lib, log = build_instance(source, out_dir, "mi_" + _stem(kernel_name).replace(".", "_"), hipcc_args,
                                   timeout_s)

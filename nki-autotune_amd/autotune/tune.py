@@ -33,6 +33,7 @@ from autotune.runner.types import KernelJob
 # Default input distributions per kernel family (benchmark configs C2 and C3).
 DEFAULT_DISTS = {
     "matmul_lhsT_rhs": {"lhs_T": "uniform", "rhs": "uniform"},
+    "matmul_lhs_rhs": {"lhs": "uniform", "rhs": "uniform"},
     "matmul_lhsT_rhs_f32": {},
     "rmsnorm_matmul": {"lhs": "normal", "gamma": "gamma"},
 }
@@ -59,6 +60,8 @@ def input_specs(func_name: str, M: int, N: int, K: int, dtype: str = "bfloat16",
     if fam in ("matmul_lhsT_rhs", "matmul_lhsT_rhs_f32"):
         dt = "float32" if fam.endswith("f32") else dtype
         return {"lhs_T": ((K, M), dt), "rhs": ((K, N), dt)}
+    if fam == "matmul_lhs_rhs":
+        return {"lhs": ((M, K), dtype), "rhs": ((K, N), dtype)}
     if fam == "rmsnorm_matmul":
         specs = {"lhs": ((M, K), dtype)}
         if with_gamma:
@@ -109,6 +112,11 @@ def check_numerics(func_name: str, cfg, M: int, N: int, K: int, seed: int = 0, d
             y = y * g.double()[None, :]
         exp = y @ w.double()
         atol = RMS_ATOL_FRAC * float(exp.square().mean().sqrt())
+    elif fam == "matmul_lhs_rhs":
+        a, b = dev["lhs"], dev["rhs"]
+        out = kl.matmul_lhs_rhs(a, b, cfg=cfg)
+        exp = a.double() @ b.double()
+        atol = ATOL
     else:
         a, b = dev["lhs_T"], dev["rhs"]
         out = kl.matmul_lhsT_rhs(a, b, cfg=cfg)
@@ -203,8 +211,8 @@ def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, ca
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description="Sweep tile configs of a kernel_library kernel on this MI355X.")
     ap.add_argument("--kernel", default="matmul_lhsT_rhs",
-                    choices=["matmul_lhsT_rhs", "matmul_lhsT_rhs_f32", "rmsnorm_matmul", "matmul_lhsT_rhs_nkigym",
-                             "rmsnorm_matmul_online"])
+                    choices=["matmul_lhsT_rhs", "matmul_lhsT_rhs_f32", "rmsnorm_matmul", "matmul_lhs_rhs",
+                             "matmul_lhsT_rhs_nkigym", "rmsnorm_matmul_online", "matmul_lhs_rhs_nkigym"])
     ap.add_argument("--shape", nargs=3, type=int, metavar=("M", "N", "K"), default=[8192, 8192, 8192])
     ap.add_argument("--cache", default="", help="cache dir for sources / results.json (empty: none)")
     ap.add_argument("--grid", choices=["compiled", "baseline"], default="compiled",
@@ -237,7 +245,8 @@ def main(argv: list[str] | None = None) -> int:
     if args.baseline and fam != "rmsnorm_matmul":
         from autotune.runner.baseline import profile_torch_baseline
 
-        b = profile_torch_baseline(M, N, K, warmup=args.warmup, reps=args.reps, flush_bytes=args.flush_mib << 20)
+        b = profile_torch_baseline(M, N, K, warmup=args.warmup, reps=args.reps, flush_bytes=args.flush_mib << 20,
+                                   lhs_layout="MK" if fam == "matmul_lhs_rhs" else "KM")
         s = b.profiler_summary
         if s:
             print(f"[tune] hipBLASLt baseline: {s['total_time'] * 1e6:.1f} us {s['tflops']:.1f} TFLOP/s")

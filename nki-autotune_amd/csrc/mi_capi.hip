@@ -89,8 +89,8 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
     // whose x rows are reduced over BK/8 lanes).
     // The pipelined matmul (variant 1) double-buffers MFMA operands across
     // K sub-steps of 16 and needs an even number of them.
-    const int kmin = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 || (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 &&
-                                                                   c.variant == 1)
+    const int kmin = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 || kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 ||
+                             (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && c.variant == 1)
                          ? 32
                          : 16;
     if (!pow2_in(c.block_m, 32, 512) || !pow2_in(c.block_n, 32, 512) || !pow2_in(c.block_k, kmin, 128))
@@ -114,8 +114,9 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
   if (e->lds_bytes > kLdsLimit) return fail(MI_E_LDS, "instance LDS %d bytes > %d", e->lds_bytes, kLdsLimit);
   if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_F32) {
     if (M % 8 || N % 8) return fail(MI_E_ALIGN, "M=%d and N=%d must be multiples of 8", M, N);
-    if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 && K % 8)
-      return fail(MI_E_ALIGN, "K=%d must be a multiple of 8 for rmsnorm_matmul", K);
+    const bool k_rows = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 || kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16;
+    if (k_rows && K % 8)
+      return fail(MI_E_ALIGN, "K=%d must be a multiple of 8 (16-byte rows of the K-contiguous operand)", K);
     // Loads run up to one tile (the ring depth, for variant 2) past K.
     const unsigned long long kpad =
         (unsigned long long)K + (unsigned long long)c.block_k * (unsigned long long)(reg_ring ? c.lds_stages + 1 : 1);
@@ -124,7 +125,8 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
     if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16) {
       a_span = kpad * (unsigned long long)M * 2ull;
     } else {
-      // x loads of the fused kernels run up to 8 tiles past K on the last rows.
+      // K-contiguous A (x of the fused kernels, lhs of matmul_lhs_rhs): loads
+      // run up to 8 tiles past K on the last rows.
       a_span = (mpad * (unsigned long long)K + 8ull * (unsigned long long)c.block_k) * 2ull;
     }
     b_span = kpad * (unsigned long long)N * 2ull;
@@ -157,6 +159,10 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
     else if (M <= 64) c = {64, 256, 64, 4, 2, 1, 8, 0};
     else if (M <= 128) c = {128, 128, 64, 4, 2, 1, 8, 0};
     else if ((long long)M * N <= 4096LL * 4096LL) c = {128, 256, 64, 8, 2, 1, 8, 0};
+  } else if (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16) {
+    c = {256, 256, 32, 4, 3, 1, 8, 0};
+    if (M <= 64) c = {64, 128, 64, 4, 4, 1, 8, 0};
+    else if (M <= 128) c = {128, 128, 64, 4, 3, 1, 8, 0};
   } else if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16) {
     if (M <= 128) c = {64, 128, 64, 4, 2, 1, 8, 0};
     else if ((long long)M * N <= 4096LL * 4096LL) c = {128, 256, 64, 8, 2, 1, 8, 0};
@@ -225,6 +231,20 @@ int mi_matmul_lhsT_rhs_bf16(const void* lhsT, const void* rhs, void* out, int M,
   if (!lhsT || !rhs) return fail(MI_E_ARGS, "null input pointer");
   mi::MiArgs a = {lhsT, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
   return run(MI_KERNEL_MATMUL_LHST_RHS_BF16, cfg, a, stream);
+}
+
+int mi_matmul_lhs_rhs_bf16(const void* lhs, const void* rhs, void* out, int M, int N, int K,
+                           const mi_tile_cfg* cfg, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return fail(MI_E_ARGS, "negative size M=%d N=%d K=%d", M, N, K);
+  if (M == 0 || N == 0) return MI_OK;
+  if (!out) return fail(MI_E_ARGS, "null output pointer");
+  if (K == 0) {
+    const hipError_t e = hipMemsetAsync(out, 0, (size_t)M * N * 2, (hipStream_t)stream);
+    return e == hipSuccess ? MI_OK : hip_fail(e, "hipMemsetAsync");
+  }
+  if (!lhs || !rhs) return fail(MI_E_ARGS, "null input pointer");
+  mi::MiArgs a = {lhs, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
+  return run(MI_KERNEL_MATMUL_LHS_RHS_BF16, cfg, a, stream);
 }
 
 int mi_matmul_lhsT_rhs_f32(const float* lhsT, const float* rhs, float* out, int M, int N, int K,

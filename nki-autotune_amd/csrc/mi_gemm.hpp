@@ -217,6 +217,61 @@ struct PanelLoader {
   static constexpr int LOADS_PER_TILE = PER_WAVE;
 };
 
+// Swizzle of the 16-byte K chunks of one row in a K-contiguous panel:
+// the 16 lanes of one ds_read_b128 phase (16 rows, same K chunk) hit 16
+// different 16-byte bank groups.
+template <int BK>
+__device__ __forceinline__ int k_swz(int row) {
+  constexpr int XD = (128 / BK) > 0 ? (128 / BK) : 1;
+  return (row / XD) & (BK / 8 - 1);
+}
+
+// LDS-direct loader of a K-contiguous panel: rows row0 .. row0+ROWS-1 of a
+// row-major [rows][ld] bf16 matrix, BK columns per K tile, into an LDS panel
+// [ROWS][BK] (row stride BK*2 bytes) whose 16-byte chunks are XOR-swizzled
+// by k_swz: LDS slot s of row r holds K chunk s ^ k_swz(r).  Lane l of a
+// 1 KiB wave load lands at byte 16*l of its chunk, so each lane fetches the
+// global chunk that its LDS slot must hold.  The K tile offset rides in the
+// buffer descriptor (make_rsrc_from).  In the last K tile, chunks past K
+// read zeros (voff_tail).
+template <int BK, int ROWS, int WAVES>
+struct KPanelLoader {
+  static constexpr int ROWB = BK * 2;
+  static constexpr int CH = ROWS * ROWB / 1024;
+  static constexpr int PER_WAVE = (CH + WAVES - 1) / WAVES;
+  static constexpr int LANES_PER_ROW = BK / 8;
+  static constexpr int ROWS_PER_CH = 1024 / ROWB;
+  static constexpr bool EVEN = CH % WAVES == 0;
+  static_assert(BK >= 16 && BK <= 128 && (BK & (BK - 1)) == 0, "K tile of 16..128 columns");
+  static_assert(CH >= 1, "panel smaller than one wave load");
+  uint32_t voff[PER_WAVE];       // per-lane byte offset inside a K tile
+  uint32_t voff_tail[PER_WAVE];  // the same for the last K tile (past K: out of range)
+  int lds_off[PER_WAVE];
+  bool active[PER_WAVE];
+
+  // oob: any offset at or past the end of the whole buffer.
+  __device__ __forceinline__ void init(int wave, int lane, int row0, int ld, int k_last, uint32_t oob) {
+#pragma unroll
+    for (int j = 0; j < PER_WAVE; ++j) {
+      const int c = wave + j * WAVES;
+      active[j] = c < CH;
+      const int row = c * ROWS_PER_CH + lane / LANES_PER_ROW;
+      const int q = (lane % LANES_PER_ROW) ^ k_swz<BK>(row);
+      voff[j] = ((uint32_t)(row0 + row) * (uint32_t)ld + (uint32_t)(8 * q)) * 2u;
+      voff_tail[j] = 8 * q < k_last ? voff[j] : oob;
+      lds_off[j] = c * 1024;
+    }
+  }
+  __device__ __forceinline__ void issue_at(int j, __amdgpu_buffer_rsrc_t rs_kt, char* smem, int base,
+                                           bool tail) const {
+    if (EVEN || active[j]) {
+      if (tail) lds_dma16(rs_kt, smem + base + lds_off[j], voff_tail[j]);
+      else lds_dma16(rs_kt, smem + base + lds_off[j], voff[j]);
+    }
+  }
+  static constexpr int LOADS_PER_TILE = PER_WAVE;
+};
+
 // Per-lane LDS byte offsets of the MFMA operand fragments read with
 // ds_read_b64_tr_b16 from an MN-contiguous [BK][W] panel.  For fragment t
 // (32 columns starting at w0 + 32t) and K sub-step kk, half h, the address
@@ -463,24 +518,26 @@ struct PipeCfg {
   static constexpr int LDS_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
 };
 
-template <int BM, int BN, int BK, int WAVES, int STAGES>
-__global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const uint16_t* __restrict__ lhsT,
-                                                                          const uint16_t* __restrict__ rhs,
-                                                                          uint16_t* __restrict__ out, int M, int N,
-                                                                          int K, int group_m) {
+// The pipelined body, for two layouts of the A operand: AK = false takes
+// lhsT[K,M] (M contiguous; MN-swizzled panel, transposing operand reads),
+// AK = true takes lhs[M,K] (K contiguous; K-swizzled panel, one
+// ds_read_b128 per operand fragment, no transpose).
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool AK>
+__device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, const uint16_t* __restrict__ rhs,
+                                             uint16_t* __restrict__ out, int M, int N, int K, int group_m,
+                                             char* smem) {
   using C = PipeCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
   static_assert(G::ok, "illegal wave grid");
   static_assert(BK % 32 == 0, "BK must be a multiple of 32 (even number of MFMA K steps)");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
   constexpr int TM = G::TM, TN = G::TN, KS = BK / 16;
-  using LA = PanelLoader<BK, BM, WAVES>;
+  using LA = std::conditional_t<AK, KPanelLoader<BK, BM, WAVES>, PanelLoader<BK, BM, WAVES>>;
   using LB = PanelLoader<BK, BN, WAVES>;
   // Loads of one K tile by this wave; vm_wait<n> with n > 0 needs every wave
   // to issue the same number.
   constexpr int LPT = LA::LOADS_PER_TILE + LB::LOADS_PER_TILE;
   static_assert(STAGES == 2 || (LA::EVEN && LB::EVEN), "deeper pipelines need an even panel split");
-  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
 
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63;
@@ -494,16 +551,25 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
 
   const uint32_t a_bytes = (uint32_t)K * (uint32_t)M * 2u;
   const uint32_t b_bytes = (uint32_t)K * (uint32_t)N * 2u;
+  const int KT = (K + BK - 1) / BK;
   LA la;
   LB lb;
-  la.init(wave, lane, m0, M);
+  if constexpr (AK) la.init(wave, lane, m0, K, K - (KT - 1) * BK, a_bytes);
+  else la.init(wave, lane, m0, M);
   lb.init(wave, lane, n0, N);
-  const uint32_t kstep_a = (uint32_t)BK * (uint32_t)M * 2u;
+  const uint32_t kstep_a = AK ? (uint32_t)BK * 2u : (uint32_t)BK * (uint32_t)M * 2u;
   const uint32_t kstep_b = (uint32_t)BK * (uint32_t)N * 2u;
   TrFrag<BM, TM> fa;
   TrFrag<BN, TN> fb;
-  fa.init(lane, wm0);
+  if constexpr (!AK) fa.init(lane, wm0);
   fb.init(lane, wn0);
+  // K-contiguous A operand: lane l reads row l%32 of the fragment, K chunk
+  // 2*kk + l/32 of the sub-step, at its k_swz slot (the same for every
+  // 32-row fragment of the wave).
+  const int arow = (wm0 + (lane & 31)) * (BK * 2);
+  int akoff[KS];
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) akoff[kk] = 16 * ((2 * kk + (lane >> 5)) ^ k_swz<BK>(wm0 + (lane & 31)));
 
   f32x16_t acc[TM][TN];
 #pragma unroll
@@ -520,8 +586,12 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
     const int bbase = abase + C::A_BYTES;
     if (f == 0 || f > TN) {
       const int t = f == 0 ? 0 : f - TN;
-      af[buf][t] = read_tr_frag(smem, abase + (kk * 16) * (BM * 2) + fa.off[t],
-                                abase + (kk * 16 + 4) * (BM * 2) + fa.off[t]);
+      if constexpr (AK)
+        af[buf][t] = __builtin_bit_cast(
+            bf16x8_t, *(MI_LDS u32x4_t*)((MI_LDS char*)smem + abase + arow + t * 32 * (BK * 2) + akoff[kk]));
+      else
+        af[buf][t] = read_tr_frag(smem, abase + (kk * 16) * (BM * 2) + fa.off[t],
+                                  abase + (kk * 16 + 4) * (BM * 2) + fa.off[t]);
     } else {
       const int t = f - 1;
       bf[buf][t] = read_tr_frag(smem, bbase + (kk * 16) * (BN * 2) + fb.off[t],
@@ -541,14 +611,17 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
   };
   // Load q (< LPT) of K tile kt into `stage`: the A loads, then the B loads.
   auto issue_one = [&](int q, int kt, int stage) {
-    if (q < LA::LOADS_PER_TILE)
-      la.issue_at(q, make_rsrc_from(lhsT, a_bytes, (uint32_t)kt * kstep_a), smem, stage * C::STAGE_BYTES);
-    else
+    if (q < LA::LOADS_PER_TILE) {
+      if constexpr (AK)
+        la.issue_at(q, make_rsrc_from(a, a_bytes, (uint32_t)kt * kstep_a), smem, stage * C::STAGE_BYTES,
+                    kt == KT - 1);
+      else
+        la.issue_at(q, make_rsrc_from(a, a_bytes, (uint32_t)kt * kstep_a), smem, stage * C::STAGE_BYTES);
+    } else
       lb.issue_at(q - LA::LOADS_PER_TILE, make_rsrc_from(rhs, b_bytes, (uint32_t)kt * kstep_b), smem,
                   stage * C::STAGE_BYTES + C::A_BYTES);
   };
 
-  const int KT = (K + BK - 1) / BK;
   // Tiles past the end are clamped to the last one: the loads stay in
   // bounds, every tile issues the same number of loads (so vmcnt counts are
   // static) and the loop needs no branch.  Re-reading the last tile into a
@@ -615,6 +688,25 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
 #pragma unroll
   for (int i = 0; i < TM; ++i) one[i] = 1.0f;
   store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
+}
+
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+__global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const uint16_t* __restrict__ lhsT,
+                                                                          const uint16_t* __restrict__ rhs,
+                                                                          uint16_t* __restrict__ out, int M, int N,
+                                                                          int K, int group_m) {
+  __shared__ __attribute__((aligned(1024))) char smem[PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
+  mm_pipe_body<BM, BN, BK, WAVES, STAGES, false>(lhsT, rhs, out, M, N, K, group_m, smem);
+}
+
+// out[M,N] = lhs[M,K] . rhs[K,N] with lhs K-contiguous (matmul_lhs_rhs).
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+__global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pipe_kernel(const uint16_t* __restrict__ lhs,
+                                                                         const uint16_t* __restrict__ rhs,
+                                                                         uint16_t* __restrict__ out, int M, int N,
+                                                                         int K, int group_m) {
+  __shared__ __attribute__((aligned(1024))) char smem[PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
+  mm_pipe_body<BM, BN, BK, WAVES, STAGES, true>(lhs, rhs, out, M, N, K, group_m, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -707,14 +799,6 @@ struct RmsCfg {
   static_assert(NT % KC == 0, "row lanes must not straddle threads");
 };
 
-// Swizzle of the 16-byte K chunks of one x row in the K-contiguous panel:
-// the 16 lanes of one ds_read_b128 phase (16 rows, same K chunk) hit 16
-// different 16-byte bank groups.
-template <int BK>
-__device__ __forceinline__ int k_swz(int row) {
-  constexpr int XD = (128 / BK) > 0 ? (128 / BK) : 1;
-  return (row / XD) & (BK / 8 - 1);
-}
 
 template <int BM, int BN, int BK, int WAVES, int STAGES, bool PRE>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_kernel(

@@ -55,6 +55,14 @@ hipError_t launch_mm_pipe(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int BM, int BN, int BK, int W, int S>
+hipError_t launch_mm_lhs(const MiArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                     dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K,
+                     a.group_m);
+  return hipGetLastError();
+}
+
 template <int BM, int BN, int BK, int W, int S, bool PRE>
 hipError_t launch_rms_bf16(const MiArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((rmsnorm_mm_bf16_kernel<BM, BN, BK, W, S, PRE>), dim3(grid_tiles(a.M, a.N, BM, BN)),
@@ -134,6 +142,9 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
 #define MI_MMP_INST(BM, BN, BK, W, S)                                                                          \
   template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*,  \
                                                                            uint16_t*, int, int, int, int);
+#define MI_MMK_INST(BM, BN, BK, W, S)                                                                         \
+  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*,    \
+                                                                          uint16_t*, int, int, int, int);
 #define MI_RMS_INST(BM, BN, BK, W, S, PRE)                                                                   \
   template __global__ void rmsnorm_mm_bf16_kernel<BM, BN, BK, W, S, (PRE != 0)>(                            \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
@@ -175,6 +186,10 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
 #define MI_MMP_ROW(BM, BN, BK, W, S)                                                               \
   {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 1}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
    &launch_mm_pipe<BM, BN, BK, W, S>},
+// matmul_lhs_rhs (K-contiguous lhs) on the pipelined core: variant 0.
+#define MI_MMK_ROW(BM, BN, BK, W, S)                                                                \
+  {MI_KERNEL_MATMUL_LHS_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 0}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_mm_lhs<BM, BN, BK, W, S>},
 #define MI_RMS_ROW(BM, BN, BK, W, S, PRE)                                                            \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, PRE}, RmsCfg<BM, BN, BK, W, S>::LDS_BYTES,   \
    &launch_rms_bf16<BM, BN, BK, W, S, (PRE != 0)>},
@@ -234,6 +249,7 @@ const MiEntry* table_mm_bm128(int* n);
 const MiEntry* table_mm_bm256(int* n);
 const MiEntry* table_mm_pipe(int* n);
 const MiEntry* table_mm_reg(int* n);
+const MiEntry* table_mm_lhs(int* n);
 const MiEntry* table_rms_xreg(int* n);
 const MiEntry* table_rms_direct(int* n);
 const MiEntry* table_rms_xpair(int* n);

@@ -3,9 +3,10 @@
 Public kernels (torch device tensors in, torch device tensor out):
 
 * :func:`matmul_lhsT_rhs` -- ``lhs_T[K,M].T @ rhs[K,N]``, bf16 or fp32
+* :func:`matmul_lhs_rhs` -- ``lhs[M,K] @ rhs[K,N]``, bf16
 * :func:`rmsnorm_matmul` -- ``rmsnorm(lhs) * gamma @ rhs``, bf16
 
-plus the reference names ``matmul_lhsT_rhs_nkigym`` and
+plus the reference names ``matmul_lhsT_rhs_nkigym``, ``matmul_lhs_rhs_nkigym`` and
 ``rmsnorm_matmul_online``, and the tile search space (:class:`TileConfig`).
 """
 
@@ -19,6 +20,8 @@ from kernel_library.config import (
 )
 from kernel_library.ops import (
     EPS,
+    matmul_lhs_rhs,
+    matmul_lhs_rhs_nkigym,
     matmul_lhsT_rhs,
     matmul_lhsT_rhs_nkigym,
     rmsnorm_matmul,
@@ -33,6 +36,8 @@ __all__ = [
     "compiled_configs",
     "default_config",
     "legal_configs",
+    "matmul_lhs_rhs",
+    "matmul_lhs_rhs_nkigym",
     "matmul_lhsT_rhs",
     "matmul_lhsT_rhs_nkigym",
     "rmsnorm_matmul",

@@ -17,7 +17,8 @@ LIB_PATH = Path(__file__).resolve().parent / "libmi_kernels.so"
 MI_KERNEL_MATMUL_LHST_RHS_BF16 = 0
 MI_KERNEL_MATMUL_LHST_RHS_F32 = 1
 MI_KERNEL_RMSNORM_MATMUL_BF16 = 2
-MI_NUM_KERNELS = 3
+MI_KERNEL_MATMUL_LHS_RHS_BF16 = 3
+MI_NUM_KERNELS = 4
 
 # Legality codes (positive return values).
 MI_OK = 0
@@ -50,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "mi_get_config",
     "mi_default_config",
     "mi_matmul_lhsT_rhs_bf16",
+    "mi_matmul_lhs_rhs_bf16",
     "mi_matmul_lhsT_rhs_f32",
     "mi_rmsnorm_matmul_bf16",
     "mi_device_info",
@@ -94,6 +96,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "mi_get_config": (c_int, [c_int, c_int, cfgp]),
         "mi_default_config": (c_int, [c_int, c_int, c_int, c_int, cfgp]),
         "mi_matmul_lhsT_rhs_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, cfgp, c_void_p]),
+        "mi_matmul_lhs_rhs_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, cfgp, c_void_p]),
         "mi_matmul_lhsT_rhs_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, cfgp, c_void_p]),
         "mi_rmsnorm_matmul_bf16": (
             c_int,

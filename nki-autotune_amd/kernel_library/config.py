@@ -22,6 +22,7 @@ KERNEL_IDS = {
     "matmul_lhsT_rhs": _lib.MI_KERNEL_MATMUL_LHST_RHS_BF16,
     "matmul_lhsT_rhs_f32": _lib.MI_KERNEL_MATMUL_LHST_RHS_F32,
     "rmsnorm_matmul": _lib.MI_KERNEL_RMSNORM_MATMUL_BF16,
+    "matmul_lhs_rhs": _lib.MI_KERNEL_MATMUL_LHS_RHS_BF16,
 }
 
 # The 72-point search grid (72 points before legality pruning).

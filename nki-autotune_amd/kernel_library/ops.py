@@ -6,6 +6,9 @@ Drop-in for the reference kernel_library call signatures:
   (reference kernel_library/matmul/lhsT_rhs/kernel_hand_90.92mfu.py:101-131):
   ``out[M,N] = lhs_T[K,M].T @ rhs[K,N]``, output allocated by the kernel
   wrapper and returned, dtype of the first input.
+* ``matmul_lhs_rhs(lhs, rhs) -> out`` replaces ``matmul_lhs_rhs_nkigym``
+  (reference kernel_library/matmul/lhs_rhs/kernel_handtuned_89.26mfu.py:226-287):
+  ``out[M,N] = lhs[M,K] @ rhs[K,N]`` with lhs K-contiguous, bf16.
 * ``rmsnorm_matmul(lhs, rhs, gamma=None, eps=1e-6) -> out`` replaces
   ``rmsnorm_matmul_online`` (reference
   kernel_library/rmsnorm_matmul/kernel_hand_online.py:198-353):
@@ -80,6 +83,34 @@ def matmul_lhsT_rhs(
     return out
 
 
+def matmul_lhs_rhs(
+    lhs: torch.Tensor,
+    rhs: torch.Tensor,
+    cfg: TileConfig | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``out[M,N] = lhs[M,K] @ rhs[K,N]`` on the GPU (bf16, lhs K-contiguous)."""
+    _check_operand("lhs", lhs, (torch.bfloat16,))
+    _check_operand("rhs", rhs, (torch.bfloat16,))
+    if lhs.device != rhs.device:
+        raise ValueError("lhs and rhs on different devices")
+    M, K = lhs.shape
+    K2, N = rhs.shape
+    if K != K2:
+        raise ValueError(f"contraction mismatch: lhs has K={K}, rhs has K={K2}")
+    if out is None:
+        out = torch.empty((M, N), dtype=lhs.dtype, device=lhs.device)
+    elif out.shape != (M, N) or out.dtype != lhs.dtype or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous bf16 [{M},{N}] tensor")
+    cfg = cfg if cfg is not None else default_config("matmul_lhs_rhs", M, N, K)
+    c = cfg.to_c()
+    with torch.cuda.device(lhs.device):
+        rc = _lib.lib().mi_matmul_lhs_rhs_bf16(lhs.data_ptr(), rhs.data_ptr(), out.data_ptr(), M, N, K,
+                                               ctypes.byref(c), _stream_handle(lhs.device))
+    _lib.check_rc(rc, "matmul_lhs_rhs")
+    return out
+
+
 def rmsnorm_matmul(
     lhs: torch.Tensor,
     rhs: torch.Tensor,
@@ -115,6 +146,7 @@ def rmsnorm_matmul(
 
 # Reference names (drop-in aliases).
 matmul_lhsT_rhs_nkigym = matmul_lhsT_rhs
+matmul_lhs_rhs_nkigym = matmul_lhs_rhs
 
 
 def rmsnorm_matmul_online(lhs: torch.Tensor, rhs: torch.Tensor) -> torch.Tensor:

@@ -42,6 +42,16 @@ def closed_form(lhs_T: np.ndarray, rhs: np.ndarray) -> np.ndarray:
     return a.T @ b
 
 
+def closed_form_lhs(lhs: np.ndarray, rhs: np.ndarray) -> np.ndarray:
+    """float64 ``lhs @ rhs`` with lhs[M,K] K-contiguous: the product of
+    ``matmul_lhs_rhs_nkigym`` (kernel_library/matmul/lhs_rhs/kernel_handtuned_89.26mfu.py:226-287)."""
+    a = np.asarray(lhs, dtype=np.float64)
+    b = np.asarray(rhs, dtype=np.float64)
+    if a.ndim != 2 or b.ndim != 2 or a.shape[1] != b.shape[0]:
+        raise ValueError(f"shape mismatch: lhs {a.shape}, rhs {b.shape}")
+    return a @ b
+
+
 def brute_force(lhs_T: np.ndarray, rhs: np.ndarray) -> np.ndarray:
     """float64 triple loop (tiny shapes only): out[m][n] = sum_k lhs_T[k][m] * rhs[k][n]."""
     K, M = lhs_T.shape
@@ -90,3 +100,23 @@ def tiled(lhs_T: np.ndarray, rhs: np.ndarray, out_dtype: str = "bfloat16") -> np
                         acc = _cast(psum, out_dtype)          # tensor_copy PSUM -> acc_tile
                         out[m0:m1, t0:t1] = _cast(out[m0:m1, t0:t1] + acc, out_dtype)  # tensor_tensor add
     return out
+
+
+def tiled_lhs(lhs: np.ndarray, rhs: np.ndarray, out_dtype: str = "bfloat16") -> np.ndarray:
+    """The reference lhs.rhs kernel's reduction order
+    (kernel_library/matmul/lhs_rhs/kernel_handtuned_89.26mfu.py:226-287).
+
+    It transposes 1024x1024 blocks of lhs by DMA into the lhs_T layout
+    (dma_transpose_block, :54-92; :269-272) and runs the same
+    ``matmul_block`` (:120-166): per (128-row M tile, <=512-col N tile) an
+    fp32 PSUM over the 128-row K tiles of one 1024-row K block, drained to
+    the output dtype and added into the output accumulator in that dtype,
+    the accumulator zeroed once per M block (:255).  Its M/N blocking
+    (1024 / 512, :243-283) differs from the lhs_T kernel's, but blocking
+    along M or N changes no output element's reduction order, so the result
+    is :func:`tiled` of the transposed operand.
+    """
+    a = np.asarray(lhs)
+    if a.ndim != 2:
+        raise ValueError(f"lhs must be 2-D, got {a.shape}")
+    return tiled(np.ascontiguousarray(a.T), rhs, out_dtype)

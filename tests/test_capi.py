@@ -16,6 +16,7 @@ from kernel_library.config import TileConfig, check, compiled_configs, default_c
 
 ROOT = Path(__file__).resolve().parents[1]
 MM, F32, RMS = _lib.MI_KERNEL_MATMUL_LHST_RHS_BF16, _lib.MI_KERNEL_MATMUL_LHST_RHS_F32, _lib.MI_KERNEL_RMSNORM_MATMUL_BF16
+LHS = _lib.MI_KERNEL_MATMUL_LHS_RHS_BF16
 
 
 def header_symbols() -> set[str]:
@@ -38,7 +39,7 @@ def test_library_exports_every_header_symbol():
 
 def test_every_compiled_config_is_enumerable_and_legal():
     for fam, shape in (("matmul_lhsT_rhs", (2048, 2048, 2048)), ("rmsnorm_matmul", (2048, 2048, 2048)),
-                       ("matmul_lhsT_rhs_f32", (256, 512, 512))):
+                       ("matmul_lhs_rhs", (2048, 2048, 2048)), ("matmul_lhsT_rhs_f32", (256, 512, 512))):
         cfgs = compiled_configs(fam)
         assert len(cfgs) == len(set(cfgs)) > 0
         for c in cfgs:
@@ -69,6 +70,11 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (MM, TileConfig(128, 128, 48, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),
         (MM, TileConfig(512, 512, 32, 8, 1), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),  # legal, not prebuilt
         (MM, TileConfig(0, 128, 64, 4, 2), (1024, 1024, 1024), _lib.MI_E_ARGS),
+        (LHS, TileConfig(256, 256, 32, 4, 3), (8192, 8192, 8192), _lib.MI_OK),
+        (LHS, TileConfig(256, 256, 32, 4, 3), (1024, 1024, 1020), _lib.MI_E_ALIGN),      # K % 8 (K-contiguous lhs)
+        (LHS, TileConfig(128, 128, 16, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),       # pipelined core: bk >= 32
+        (LHS, TileConfig(256, 256, 32, 4, 3, variant=1), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),
+        (LHS, TileConfig(256, 256, 64, 4, 2), (65536, 65536, 65536), _lib.MI_E_RANGE),
     ],
 )
 def test_cfg_check_codes(kid, cfg, shape, code):
@@ -106,6 +112,9 @@ def test_entry_points_reject_bad_arguments_before_any_gpu_call():
     assert L.mi_matmul_lhsT_rhs_bf16(None, fake, fake, 8, 8, 8, ctypes.byref(c), None) == _lib.MI_E_ARGS
     assert L.mi_matmul_lhsT_rhs_bf16(fake, fake, fake, 0, 8, 8, ctypes.byref(c), None) == _lib.MI_OK
     assert L.mi_matmul_lhsT_rhs_f32(fake, fake, fake, 8, -8, 8, ctypes.byref(c), None) == _lib.MI_E_ARGS
+    assert L.mi_matmul_lhs_rhs_bf16(fake, fake, fake, 8, 8, -8, ctypes.byref(c), None) == _lib.MI_E_ARGS
+    assert L.mi_matmul_lhs_rhs_bf16(fake, None, fake, 8, 8, 8, ctypes.byref(c), None) == _lib.MI_E_ARGS
+    assert L.mi_matmul_lhs_rhs_bf16(fake, fake, fake, 8, 0, 8, ctypes.byref(c), None) == _lib.MI_OK
     assert L.mi_rmsnorm_matmul_bf16(fake, None, fake, fake, 8, 8, 0, 1e-6, ctypes.byref(c), None) == _lib.MI_E_ARGS
     assert L.mi_rmsnorm_matmul_bf16(fake, None, fake, fake, 8, 8, 8, float("nan"), ctypes.byref(c),
                                     None) == _lib.MI_E_ARGS
@@ -128,3 +137,5 @@ def test_python_wrappers_validate_on_the_host():
         kl.matmul_lhsT_rhs([[1.0]], a)
     with pytest.raises(ValueError):
         kl.rmsnorm_matmul(a, a, eps=1e-6)
+    with pytest.raises(ValueError, match="HIP device"):
+        kl.matmul_lhs_rhs(a, a.t().contiguous())

@@ -179,6 +179,42 @@ def test_matmul_tiled_bf16_two_stage_k():
     np.testing.assert_array_equal(two_equal, 2 * bf16.round_bf16(p))
 
 
+def test_matmul_lhs_hand_example():
+    """matmul_lhs_rhs: out[m, n] = sum_k lhs[m, k] rhs[k, n], worked by hand (lhs row-major, K contiguous)."""
+    lhs = np.array([[1.0, 4.0], [2.0, 5.0], [3.0, 6.0]])   # M=3, K=2
+    rhs = np.array([[1.0, -1.0], [0.5, 2.0]])              # K=2, N=2
+    expected = np.array([[1 + 2.0, -1 + 8.0], [2 + 2.5, -2 + 10.0], [3 + 3.0, -3 + 12.0]])
+    assert np.array_equal(matmul.closed_form_lhs(lhs, rhs), expected)
+    assert np.array_equal(matmul.tiled_lhs(lhs, rhs, "float32"), expected)
+    with pytest.raises(ValueError):
+        matmul.closed_form_lhs(lhs.T, rhs[:1])
+
+
+@pytest.mark.parametrize("M,K,N", [(5, 7, 3), (17, 33, 9)])
+def test_matmul_lhs_vs_brute_force(M, K, N):
+    """lhs . rhs against the BLAS-free triple loop of the transposed operand."""
+    d = inputs.generate({"lhs": ((M, K), "float32"), "rhs": ((K, N), "float32")}, M)
+    np.testing.assert_allclose(matmul.closed_form_lhs(d["lhs"], d["rhs"]),
+                               matmul.brute_force(np.ascontiguousarray(d["lhs"].T), d["rhs"]), rtol=1e-12, atol=1e-12)
+
+
+def test_matmul_lhs_tiled_two_stage_k():
+    """The lhs.rhs kernel drains each 1024-row K block to bf16 and adds in bf16
+    (kernel_handtuned_89.26mfu.py:120-166): integer operands make every fp32
+    partial exact, so only the drains round."""
+    rng = np.random.default_rng(3)
+    M, N = 128, 512
+    a1 = rng.integers(-2, 3, (M, 1024)).astype(np.float32)
+    b1 = rng.integers(-2, 3, (1024, N)).astype(np.float32)
+    p = (a1 @ b1).astype(np.float32)
+    assert np.any(bf16.round_bf16(p) != p)
+    two_equal = matmul.tiled_lhs(np.hstack([a1, a1]), np.vstack([b1, b1]), "bfloat16")
+    np.testing.assert_array_equal(two_equal, 2 * bf16.round_bf16(p))
+    d = inputs.generate({"lhs": ((640, 2304 + 100), "float32"), "rhs": ((2304 + 100, 300), "float32")}, 0)
+    np.testing.assert_allclose(matmul.tiled_lhs(d["lhs"], d["rhs"], "float32"),
+                               matmul.closed_form_lhs(d["lhs"], d["rhs"]), atol=5e-3, rtol=5e-3)
+
+
 # ------------------------------------------------------------------ rmsnorm
 
 

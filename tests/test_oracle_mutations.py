@@ -24,6 +24,16 @@ def test_transposed_operand_is_caught(monkeypatch):
     _fails(pins.test_matmul_hand_example)
 
 
+def test_lhs_used_as_lhs_T_is_caught(monkeypatch):
+    monkeypatch.setattr(matmul, "closed_form_lhs", lambda a, b: np.asarray(a, np.float64).T @ np.asarray(b, np.float64))
+    _fails(pins.test_matmul_lhs_hand_example)
+
+
+def test_lhs_tiled_without_transpose_is_caught(monkeypatch):
+    monkeypatch.setattr(matmul, "tiled_lhs", lambda a, b, out_dtype="bfloat16": matmul.tiled(a, b, out_dtype))
+    _fails(pins.test_matmul_lhs_hand_example)
+
+
 def test_dropped_k_tail_is_caught(monkeypatch):
     real = matmul.tiled
 

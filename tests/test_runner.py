@@ -8,6 +8,7 @@ The first three tests mirror the reference's only profiler-backend tests
 from __future__ import annotations
 
 import json
+from pathlib import Path
 
 import pytest
 
@@ -99,7 +100,8 @@ def test_work_and_utilisation_known_answers():
 
 
 def test_render_parse_roundtrip_and_aliases():
-    for fam in ("matmul_lhsT_rhs", "rmsnorm_matmul", "matmul_lhsT_rhs_nkigym", "rmsnorm_matmul_online"):
+    for fam in ("matmul_lhsT_rhs", "rmsnorm_matmul", "matmul_lhsT_rhs_nkigym", "rmsnorm_matmul_online",
+                "matmul_lhs_rhs", "matmul_lhs_rhs_nkigym"):
         cfg = TileConfig(128, 256, 64, 8, 2, variant=1 if "rms" in fam else 0)
         src = rcompile.render_source(fam, cfg)
         got_fam, got_cfg = rcompile.parse_source(src)
@@ -109,6 +111,38 @@ def test_render_parse_roundtrip_and_aliases():
         rcompile.parse_source("__global__ void k() {}")
     assert rcompile.problem_shape("matmul_lhsT_rhs", input_specs("matmul_lhsT_rhs", 64, 96, 128)) == (64, 96, 128)
     assert rcompile.problem_shape("rmsnorm_matmul", input_specs("rmsnorm_matmul", 64, 96, 128)) == (64, 96, 128)
+    assert rcompile.problem_shape("matmul_lhs_rhs", input_specs("matmul_lhs_rhs", 64, 96, 128)) == (64, 96, 128)
+
+
+@pytest.mark.parametrize("fam,variants", [("matmul_lhsT_rhs", (0, 1, 2)), ("matmul_lhs_rhs", (0,)),
+                                          ("rmsnorm_matmul", tuple(range(11)))])
+def test_jit_units_instantiate_every_variant(fam, variants, tmp_path):
+    """The generated single-config unit of every variant names a real template
+    and table row: hipcc parses and instantiates it (device side, no codegen),
+    and the row carries the config's variant."""
+    import shutil
+    import subprocess
+
+    import build_lib
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    from kernel_library.config import compiled_configs
+
+    prebuilt = compiled_configs(fam)
+    for v in variants:
+        cfg = next(c for c in prebuilt if c.variant == v)   # a config the template is known to take
+        src = rcompile.render_source(fam, cfg)
+        assert "prebuilt-only" not in src, (fam, v)
+        unit = tmp_path / f"{fam}_{v}.hip"
+        unit.write_text(src)
+        flags = [f for f in build_lib.HIPCC_FLAGS if f != "-fPIC"]
+        proc = subprocess.run([hipcc, *flags, f"-I{build_lib.CSRC}", f"-I{build_lib.INCLUDE}", "--cuda-device-only",
+                               "-fsyntax-only", str(unit)], capture_output=True, text=True)
+        assert proc.returncode == 0, (fam, v, proc.stderr[-2000:])
+    # a variant without a template is reported, not guessed
+    assert "prebuilt-only" in rcompile.render_source("matmul_lhs_rhs", TileConfig(128, 256, 32, 4, 2, variant=1))
 
 
 def test_compile_one_prebuilt_and_rejections(tmp_path):
