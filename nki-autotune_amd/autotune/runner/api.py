@@ -4,7 +4,10 @@
 builds and times a set of kernel instances on this MI355X and writes the
 standard cache layout (instance sources, results.json, per-kernel
 profile_summary.json) under ``cache_dir``; an empty ``cache_dir`` skips all
-disk output.  Per-kernel failures never raise: they are returned as
+disk output.  With ``collect_detailed_profile`` and a cache dir, each
+successful instance is also re-run under rocprofv3 in a child process and
+its kernel trace kept in its folder (``rocprof/``, ``replay.json``; the
+stats row goes into ``profile.json``).  Per-kernel failures never raise: they are returned as
 ``ProfileResult.hardware_output`` text.  Only environment faults raise (no
 GPU, wrong arch, a batch asking for more than one device).
 """
@@ -15,6 +18,7 @@ import logging
 import os
 import time
 
+from autotune.runner.compile import canonical_name, problem_shape
 from autotune.runner.driver import run_pipeline
 from autotune.runner.output import ProfileOutput, write_compiler_logs, write_kernel_sources, write_results_json
 from autotune.runner.types import KernelJob
@@ -43,7 +47,8 @@ def profile(
         platform_target: Offload arch the instances are built for
             (``neuron_platform_target`` in the reference); only "gfx950".
         collect_detailed_profile: Attach per-rep timings to each result
-            (``profile.json`` in the kernel's cache folder).
+            (``profile.json`` in the kernel's cache folder) and, with a
+            cache dir, a rocprofv3 kernel trace of each successful instance.
         warmup, reps: hipEvent timing schedule (median of ``reps``).
         flush_bytes: Size of a scratch buffer written before each timed
             launch, to evict L2 / MALL (0 = off).
@@ -65,6 +70,8 @@ def profile(
         flush_bytes=flush_bytes,
         allow_jit=allow_jit,
     )
+    if collect_detailed_profile and cache_dir:
+        _trace_successes(cache_dir, kernels, results, seed, warmup, reps, flush_bytes)
     elapsed_s = time.monotonic() - t0
     logger.info("Profile complete: %d results in %.1fs", len(results), elapsed_s)
     if cache_dir:
@@ -72,3 +79,24 @@ def profile(
         write_results_json(cache_dir, len(kernels), results, elapsed_s)
         logger.info("Cache saved to %s", cache_dir)
     return ProfileOutput(results=results, compiler_logs=compiler_logs, elapsed_s=elapsed_s, cache_dir=cache_dir)
+
+
+def _trace_successes(cache_dir: str, kernels: dict[str, KernelJob], results, seed: int, warmup: int, reps: int,
+                     flush_bytes: int) -> None:
+    """rocprofv3 kernel trace of every successful instance, into its cache folder."""
+    from pathlib import Path
+
+    from autotune.runner.trace import trace_kernel, write_replay_job
+
+    for i, r in enumerate(results):
+        summary = r.profiler_summary
+        job = kernels.get(r.kernel_name)
+        if summary is None or job is None:
+            continue
+        variant_dir = os.path.join(cache_dir, Path(r.kernel_name).stem)
+        replay = write_replay_job(variant_dir, r.kernel_name, canonical_name(job.func_name), summary["library"],
+                                  summary["config"], problem_shape(job.func_name, job.input_specs),
+                                  job.input_specs, job.input_dists, seed, warmup, reps, flush_bytes)
+        row = trace_kernel(variant_dir, replay)
+        results[i] = r._replace(profile_detailed={**(r.profile_detailed or {}), "rocprof": row})
+        logger.info("Traced %s: %s", r.kernel_name, row.get("avg_ns", row.get("error")))

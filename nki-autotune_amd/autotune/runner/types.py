@@ -99,7 +99,7 @@ class ProfileResult(NamedTuple):
     ``hardware_output`` is ``"[M, N] bfloat16"`` on success (so success is
     ``hardware_output.startswith("[")``, as in the reference) or the error
     text.  ``profiler_summary`` holds the hipEvent timing summary;
-    ``profile_detailed`` the optional rocprofv3 counter dict.
+    ``profile_detailed`` the optional per-rep timings and rocprofv3 kernel-trace row.
     """
 
     kernel_name: str

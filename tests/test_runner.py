@@ -231,3 +231,32 @@ def test_baseline_grid_and_tuned_table(tmp_path):
     assert doc["configs"]["matmul_lhsT_rhs:64x64x64"] == grid[5].asdict()
     assert doc["measurements"]["matmul_lhsT_rhs:64x64x64"] == {"tflops": 1.0}
     assert TileConfig(**doc["configs"]["rmsnorm_matmul:64x64x64"]) == grid[6]
+
+
+def test_detailed_profile_trace_helpers(tmp_path, monkeypatch):
+    """Replay job round trip, the profiler command shape, stats parsing, and
+    a missing profiler reported as data (never raised)."""
+    import autotune.runner.trace as tr
+    from autotune.runner.replay import main as replay_main
+
+    specs = input_specs("matmul_lhsT_rhs", 64, 96, 128)
+    path = tr.write_replay_job(str(tmp_path / "k0"), "k0.hip", "matmul_lhsT_rhs", "/x/lib.so",
+                               TileConfig(128, 128, 64, 4, 2).asdict(), (64, 96, 128), specs,
+                               {"lhs_T": ("normal", 0.02)}, 7, 3, 5)
+    job = json.loads(Path(path).read_text())
+    assert job["shape"] == [64, 96, 128] and job["input_specs"]["lhs_T"] == [[128, 64], "bfloat16"]
+    assert job["input_dists"] == {"lhs_T": ["normal", 0.02]} and job["seed"] == 7
+    cmd = tr.rocprof_command(str(tmp_path / "out"), path)
+    i = cmd.index("--")
+    assert "--kernel-trace" in cmd[:i] and "--pmc" not in cmd
+    assert cmd[i + 1:i + 4] == [cmd[i + 1], "-u", "-m"] and cmd[i + 4] == "autotune.runner.replay"
+    csv_path = tmp_path / "stats.csv"
+    csv_path.write_text('"Name","Calls","TotalDurationNs","AverageNs","Percentage","MinNs","MaxNs","StdDev"\n'
+                        '"void at::native::copy(int)",2,100,50.0,1.0,40,60,1.0\n'
+                        '"void mi::mm_lhsT_rhs_bf16_pipe_kernel<256, 256, 32, 4, 3>(int)",110,85577516,777977.4,'
+                        '99.8,742629,1029515,52412.2\n')
+    row = tr.parse_kernel_stats(str(csv_path))
+    assert row["calls"] == 110 and row["avg_ns"] == 777977.4 and "pipe_kernel" in row["kernel"]
+    monkeypatch.setattr(tr.shutil, "which", lambda name: None)
+    assert "not found" in tr.trace_kernel(str(tmp_path / "k0"), path)["error"]
+    assert replay_main([]) == 2
