@@ -92,20 +92,28 @@ def make_jobs(func_name: str, M: int, N: int, K: int, configs, dists: dict | Non
 
 
 def check_numerics(func_name: str, cfg, M: int, N: int, K: int, seed: int = 0, dists: dict | None = None,
-                   with_gamma: bool = True) -> dict:
-    """Run ``cfg`` once on seeded inputs and compare with a float64 torch product on the GPU."""
+                   with_gamma: bool = True, library_path: str | None = None) -> dict:
+    """Run ``cfg`` once on seeded inputs and compare with a float64 torch product on the GPU.
+
+    ``library_path`` selects the library holding the instance (default: the
+    prebuilt libmi_kernels.so; a just-in-time build for other configs).
+    """
     import torch
 
     import kernel_library as kl
-    from autotune.runner.benchmark import generate_tensors, upload
+    from autotune.runner.benchmark import Launcher, generate_tensors, upload
+    from kernel_library import _lib
 
     fam = canonical_name(func_name)
     specs = input_specs(fam, M, N, K, with_gamma=with_gamma)
     dev = upload(generate_tensors(specs, seed, default_dists(fam, K) if dists is None else dists), specs,
                  torch.device("cuda:0"))
+    out = torch.empty((M, N), dtype=torch.float32 if fam.endswith("f32") else torch.bfloat16, device="cuda:0")
+    library = _lib.load(library_path) if library_path else _lib.lib()
+    Launcher(library, fam, cfg, dev, out, M, N, K)()
+    torch.cuda.synchronize()
     if fam == "rmsnorm_matmul":
         x, w, g = dev["lhs"], dev["rhs"], dev.get("gamma")
-        out = kl.rmsnorm_matmul(x, w, g, cfg=cfg)
         xf = x.double()
         y = xf * torch.rsqrt((xf * xf).mean(dim=1, keepdim=True) + kl.EPS)
         if g is not None:
@@ -114,12 +122,10 @@ def check_numerics(func_name: str, cfg, M: int, N: int, K: int, seed: int = 0, d
         atol = RMS_ATOL_FRAC * float(exp.square().mean().sqrt())
     elif fam == "matmul_lhs_rhs":
         a, b = dev["lhs"], dev["rhs"]
-        out = kl.matmul_lhs_rhs(a, b, cfg=cfg)
         exp = a.double() @ b.double()
         atol = ATOL
     else:
         a, b = dev["lhs_T"], dev["rhs"]
-        out = kl.matmul_lhsT_rhs(a, b, cfg=cfg)
         exp = a.double().t() @ b.double()
         atol = ATOL
     diff = (out.double() - exp).abs()
@@ -137,8 +143,11 @@ def check_numerics(func_name: str, cfg, M: int, N: int, K: int, seed: int = 0, d
 
 def refine(func_name: str, M: int, N: int, K: int, configs, seed: int = 0, dists: dict | None = None,
            with_gamma: bool = True, warmup: int = 10, reps: int = 30, flush_bytes: int = 0,
-           rounds: int = 5) -> dict:
+           rounds: int = 5, libraries: dict | None = None) -> dict:
     """Re-time finalists in interleaved rounds; config name -> median of the per-round medians.
+
+    ``libraries`` maps a config name to the library that holds it (default:
+    the prebuilt libmi_kernels.so).
 
     A single sequential sweep drifts with the chip's clock and power state,
     so configs within a few percent of each other can swap places depending
@@ -157,7 +166,9 @@ def refine(func_name: str, M: int, N: int, K: int, configs, seed: int = 0, dists
     dev = torch.device("cuda:0")
     inputs = upload(generate_tensors(specs, seed, default_dists(fam, K) if dists is None else dists), specs, dev)
     out = torch.empty((M, N), dtype=torch.float32 if fam.endswith("f32") else torch.bfloat16, device=dev)
-    launchers = {c.name: Launcher(_lib.lib(), fam, c, inputs, out, M, N, K) for c in configs}
+    libraries = libraries or {}
+    launchers = {c.name: Launcher(_lib.load(libraries[c.name]) if c.name in libraries else _lib.lib(), fam, c,
+                                  inputs, out, M, N, K) for c in configs}
     flush = torch.empty(flush_bytes // 4, dtype=torch.float32, device=dev).zero_ if flush_bytes else None
     per_round: dict[str, list[float]] = {n: [] for n in launchers}
     for r in range(rounds):
@@ -174,8 +185,11 @@ def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, ca
 
     The sweep is ``profile`` (the reference's selection is the min of its
     single-run times, examples/tune_matmul_lhsT_rhs.py:238); the ``finalists``
-    fastest prebuilt configs are then re-timed in ``rounds`` interleaved
-    rounds (``refine``) and the winner is the fastest there.
+    fastest configs are then re-timed in ``rounds`` interleaved rounds
+    (``refine``), each from the library that holds it, and the winner is the
+    fastest there.  ``record`` stores the fastest config that the prebuilt
+    library holds (a just-in-time winner is noted beside it), since callers
+    of ``kernel_library`` only load that library.
     """
     import kernel_library as kl
     from kernel_library.config import TileConfig, record_tuned
@@ -191,20 +205,29 @@ def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, ca
         return TuneResult(None, None, output, None)
     cfg_of = {r.kernel_name: TileConfig(**r.profiler_summary["config"]) for r in output.results
               if r.profiler_summary and "config" in r.profiler_summary}
-    best = cfg_of[best_row.kernel_name]
-    best_time = best_row.total_time_s
-    if finalists > 1 and rounds > 0:
-        ranked = sorted((r for r in output.successes if r.kernel_name in cfg_of), key=lambda r: r.total_time_s)
-        cands = [cfg_of[r.kernel_name] for r in ranked if kl.check(fam, cfg_of[r.kernel_name], M, N, K)[0] == 0]
-        cands = cands[:finalists]
-        if len(cands) > 1:
-            med = refine(fam, M, N, K, cands, seed, dists, with_gamma, warmup, max(10, reps // 2), flush_bytes,
-                         rounds)
-            name = min(med, key=med.get)
-            best, best_time = next(c for c in cands if c.name == name), med[name]
-    rep = check_numerics(fam, best, M, N, K, seed, dists, with_gamma) if check else None
-    if record and (rep is None or rep["pass"]):
-        record_tuned(fam, M, N, K, best, extra={"total_time_s": best_time, "tflops": 2.0 * M * N * K / best_time / 1e12})
+    lib_of = {cfg_of[r.kernel_name].name: r.profiler_summary["library"] for r in output.results
+              if r.kernel_name in cfg_of}
+    prebuilt = {c.name for c in cfg_of.values() if kl.check(fam, c, M, N, K)[0] == 0}
+    ranked = sorted((r for r in output.successes if r.kernel_name in cfg_of), key=lambda r: r.total_time_s)
+    times = {cfg_of[r.kernel_name].name: r.total_time_s for r in ranked}
+    cands = [cfg_of[r.kernel_name] for r in ranked][:max(finalists, 1)]
+    if finalists > 1 and rounds > 0 and len(cands) > 1:
+        times.update(refine(fam, M, N, K, cands, seed, dists, with_gamma, warmup, max(10, reps // 2), flush_bytes,
+                            rounds, libraries=lib_of))
+    order = sorted(cands, key=lambda c: times[c.name])
+    best, best_time = order[0], times[order[0].name]
+    rep = check_numerics(fam, best, M, N, K, seed, dists, with_gamma, lib_of.get(best.name)) if check else None
+    if record:
+        keep = next((c for c in order if c.name in prebuilt), None)
+        if keep is None:
+            keep = next((cfg_of[r.kernel_name] for r in ranked if cfg_of[r.kernel_name].name in prebuilt), None)
+        keep_rep = rep if keep is best else (
+            check_numerics(fam, keep, M, N, K, seed, dists, with_gamma) if check and keep is not None else None)
+        if keep is not None and (keep_rep is None or keep_rep["pass"]):
+            extra = {"total_time_s": times[keep.name], "tflops": 2.0 * M * N * K / times[keep.name] / 1e12}
+            if keep is not best:
+                extra["jit_best"] = {"config": best.name, "total_time_s": best_time}
+            record_tuned(fam, M, N, K, keep, extra=extra)
     return TuneResult(best, best_time, output, rep)
 
 
@@ -215,8 +238,11 @@ def main(argv: list[str] | None = None) -> int:
                              "matmul_lhsT_rhs_nkigym", "rmsnorm_matmul_online", "matmul_lhs_rhs_nkigym"])
     ap.add_argument("--shape", nargs=3, type=int, metavar=("M", "N", "K"), default=[8192, 8192, 8192])
     ap.add_argument("--cache", default="", help="cache dir for sources / results.json (empty: none)")
-    ap.add_argument("--grid", choices=["compiled", "baseline"], default="compiled",
-                    help="compiled: every prebuilt config; baseline: the 72-point search grid (JIT-built if needed)")
+    ap.add_argument("--grid", choices=["compiled", "baseline", "frontier"], default="compiled",
+                    help="compiled: every prebuilt config; baseline: the 72-point search grid (JIT-built if needed); "
+                         "frontier: --num-kernels configs sampled by frontier expansion from the default config")
+    ap.add_argument("--num-kernels", type=int, default=24, help="configs drawn by --grid frontier")
+    ap.add_argument("--prebuilt-only", action="store_true", help="--grid frontier: never leave the prebuilt set")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--reps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
@@ -233,6 +259,10 @@ def main(argv: list[str] | None = None) -> int:
     if args.grid == "baseline":
         variants = (0, 1) if fam == "rmsnorm_matmul" else (0,)
         configs = [c for c in kl.baseline_grid(variants) if kl.check(fam, c, M, N, K)[0] in (0, 1)]
+    elif args.grid == "frontier":
+        from autotune.search import TileMDP, frontier_sample
+
+        configs = frontier_sample(TileMDP(fam, M, N, K, args.prebuilt_only), args.num_kernels, args.seed)
     if args.cache:
         shutil.rmtree(args.cache, ignore_errors=True)
         os.makedirs(args.cache, exist_ok=True)

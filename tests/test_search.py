@@ -1,0 +1,85 @@
+"""The tile-config MDP and the frontier-expansion sampler (CPU only).
+
+Pins the sampler's contract (reference docs/superpowers/specs/
+2026-05-05-unified-tune-stage-design.md:27-54): every pooled config is
+legal, same seed gives the same sample, each (config, atom) edge is tried
+once, and at exhaustion the pool is the whole reachable set whatever the
+seed -- checked against a plain breadth-first closure of the same moves.
+"""
+
+from __future__ import annotations
+
+from collections import deque
+
+import pytest
+
+import kernel_library as kl
+from autotune.search import Atom, IllegalMove, TileMDP, atoms_for, frontier_pool, frontier_sample
+from kernel_library.config import TileConfig
+
+
+def _closure(mdp: TileMDP) -> set[str]:
+    root = mdp.reset()
+    seen = {root.name: root}
+    q = deque([root])
+    while q:
+        s = q.popleft()
+        for a in mdp.atoms:
+            try:
+                n = mdp.step(s, a)
+            except IllegalMove:
+                continue
+            if n.name not in seen:
+                seen[n.name] = n
+                q.append(n)
+    return set(seen)
+
+
+def test_mdp_moves_and_legality():
+    mdp = TileMDP("matmul_lhsT_rhs", 4096, 4096, 4096, prebuilt_only=True)
+    s = mdp.reset()
+    assert mdp.is_legal(s)
+    acts = mdp.legal_actions(s)
+    assert acts and all(isinstance(a, Atom) for a in acts)
+    for a in acts:
+        n = mdp.step(s, a)
+        assert n != s and kl.check("matmul_lhsT_rhs", n, 4096, 4096, 4096)[0] == 0
+    with pytest.raises(IllegalMove):
+        mdp.step(TileConfig(512, 512, 32, 8, 2, variant=1), Atom("block_m", "x2"))   # 1024 out of range
+    with pytest.raises(IllegalMove):
+        mdp.step(s, Atom("variant", f"={s.variant}"))                                 # no-op move
+    assert Atom("variant", "=10") in atoms_for("rmsnorm_matmul")
+    assert not mdp.is_terminal(s)
+
+
+@pytest.mark.parametrize("fam", ["matmul_lhsT_rhs", "matmul_lhs_rhs", "rmsnorm_matmul"])
+def test_exhaustion_is_the_reachable_set_for_any_seed(fam):
+    mdp = TileMDP(fam, 2048, 2048, 2048, prebuilt_only=True)
+    want = _closure(mdp)
+    assert len(want) > 10
+    for seed in (0, 1, 7):
+        got = {c.name for c in frontier_pool(TileMDP(fam, 2048, 2048, 2048, prebuilt_only=True), 10**6, seed)}
+        assert got == want, seed
+
+
+def test_sample_is_deterministic_legal_and_capped():
+    mk = lambda: TileMDP("matmul_lhsT_rhs", 8192, 8192, 8192)   # noqa: E731
+    a = frontier_sample(mk(), 12, seed=3)
+    b = frontier_sample(mk(), 12, seed=3)
+    c = frontier_sample(mk(), 12, seed=4)
+    assert [x.name for x in a] == [x.name for x in b]
+    assert [x.name for x in a] != [x.name for x in c]
+    assert len({x.name for x in a}) == 12
+    mdp = mk()
+    assert all(mdp.is_legal(x) for x in a)
+    pool = frontier_pool(mk(), 30, seed=0)
+    assert len(pool) == 30          # capped before exhaustion: the JIT-reachable space is larger
+    with pytest.raises(ValueError):
+        frontier_sample(mk(), 0)
+
+
+def test_prebuilt_only_stays_in_the_library():
+    prebuilt = {c.name for c in kl.compiled_configs("matmul_lhsT_rhs")}
+    for c in frontier_pool(TileMDP("matmul_lhsT_rhs", 4096, 4096, 4096, prebuilt_only=True), 10**6, 0):
+        base = TileConfig(c.block_m, c.block_n, c.block_k, c.waves, c.lds_stages, c.split_k, 8, c.variant)
+        assert base.name in prebuilt, c
