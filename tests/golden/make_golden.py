@@ -30,6 +30,7 @@ FIXTURES = {
     "mm_f32_128cube_seed0": ("mm", (128, 128, 128), 0, None, "float32"),        # reference 128^3 procedure
     "mm_bf16_k160_m96_n128": ("mm", (160, 96, 128), 11, "uniform", "bfloat16"),  # ragged vs every block size
     "mm_bf16_k1040_m40_n136": ("mm", (1040, 40, 136), 12, ("normal", 0.02), "bfloat16"),
+    "lhs_bf16_m72_k296_n160": ("lhs", (72, 296, 160), 15, "uniform", "bfloat16"),   # K tail past a 32 tile
     "rms_bf16_m64_k256_n96": ("rms", (64, 256, 96), 13, None, "bfloat16"),
     "rms_bf16_m40_k520_n72_nogamma": ("rms", (40, 520, 72), 14, None, "bfloat16"),
 }
@@ -46,6 +47,11 @@ def make(name: str) -> dict[str, np.ndarray]:
             out.update(lhs_T_bits=bf16.to_bf16_bits(d["lhs_T"]), rhs_bits=bf16.to_bf16_bits(d["rhs"]))
         else:
             out.update(lhs_T=d["lhs_T"], rhs=d["rhs"])
+    elif kind == "lhs":
+        M, K, N = a, b, c
+        d = inputs.generate({"lhs": ((M, K), dtype), "rhs": ((K, N), dtype)}, seed, {"lhs": dist, "rhs": dist})
+        out = {"expected": matmul.closed_form_lhs(d["lhs"], d["rhs"]),
+               "lhs_bits": bf16.to_bf16_bits(d["lhs"]), "rhs_bits": bf16.to_bf16_bits(d["rhs"])}
     else:
         M, K, N = a, b, c
         gamma = not name.endswith("nogamma")

@@ -40,6 +40,21 @@ def test_matmul_golden(gpu, name):
             assert rep["ok"], (name, cfg, rep)
 
 
+@pytest.mark.parametrize("name", sorted(n for n in make_golden.FIXTURES if n.startswith("lhs_")))
+def test_matmul_lhs_golden(gpu, name):
+    import torch
+
+    import kernel_library as kl
+
+    d = make_golden.load(name)
+    a, b = _dev(d["lhs"], torch.bfloat16, gpu), _dev(d["rhs"], torch.bfloat16, gpu)
+    cfgs = kl.legal_configs("matmul_lhs_rhs", a.shape[0], b.shape[1], a.shape[1])
+    assert cfgs
+    for cfg in cfgs:
+        rep = mm_check(kl.matmul_lhs_rhs(a, b, cfg=cfg).float().cpu().numpy(), d["expected"])
+        assert rep["ok"], (name, cfg, rep)
+
+
 @pytest.mark.parametrize("name", sorted(n for n in make_golden.FIXTURES if n.startswith("rms_")))
 def test_rmsnorm_golden(gpu, name):
     import torch
