@@ -59,7 +59,8 @@ def _instance(fam: str, cfg) -> tuple[str, str, str] | None:
         macro = {0: "MI_MM", 1: "MI_MMP", 2: "MI_MMR"}.get(v)
         return (f"{macro}_INST", f"{macro}_ROW", f"{base}, {s}") if macro else None
     if fam == "matmul_lhs_rhs":
-        return ("MI_MMK_INST", "MI_MMK_ROW", f"{base}, {s}") if v == 0 else None
+        macro = {0: "MI_MMK", 1: "MI_MMKP"}.get(v)
+        return (f"{macro}_INST", f"{macro}_ROW", f"{base}, {s}") if macro else None
     if fam == "rmsnorm_matmul":
         if v in (0, 1):
             return "MI_RMS_INST", "MI_RMS_ROW", f"{base}, {s}, {v}"

@@ -1,0 +1,215 @@
+// mi_mm_lhs_pair.hpp -- matmul_lhs_rhs variant 1: the pipelined core with
+// the K-contiguous A panel fetched two K tiles at a time.
+//
+//   out[M,N] = lhs[M,K] . rhs[K,N]   (lhs row-major, K contiguous)
+//
+// One K tile of a K-contiguous panel is BK*2 bytes of each of BM rows.  With
+// BK = 32 that is half of a 128-byte line per row, and the vector L1 sends
+// one request per half line, so the A side of a tile costs twice the L2
+// requests of the same bytes in the lhsT layout (measured: +50 % L1->L2
+// read requests and +12..19 % time for the per-tile variant 0).  Here each
+// A load covers K tiles 2u and 2u+1 together -- whole lines, the same bytes
+// -- into a pair buffer whose rows hold both tiles (row stride 4*BK bytes,
+// 16-byte chunks XOR-swizzled by k_swz<2*BK>); B keeps its per-tile ring:
+//
+//   B(j)         -> stage j % STAGES, issued at the barrier that ends tile
+//                   j - STAGES (with A(j, j+1) when j is even)
+//   A(2u, 2u+1)  -> pair buffer u % NP
+//
+// Pair u's buffer is reused by pair u + NP, issued at the barrier ending
+// tile 2u + 2*NP - STAGES; tile 2u+1 has been consumed by then when
+// NP = (STAGES + 2) / 2.  At the barrier that ends tile t the wave waits for
+// tile t+1: its B loads, and its A loads, which are issued in the same group
+// (t+1 even, after the B loads) or one group earlier (t+1 odd).  The groups
+// of barriers t+2-STAGES .. t-1 may still fly: (STAGES-2) B groups plus one
+// A pair for every even tile among t+2 .. t+STAGES-1.  The loop is unrolled
+// over lcm(STAGES, 2*NP) tiles, so stage, pair buffer, tile half and wait
+// counts are compile-time constants in every tile body.
+#pragma once
+#include <numeric>
+
+#include "mi_gemm.hpp"
+
+namespace mi {
+
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+struct PairCfg {
+  using G = WaveGrid<BM, BN, WAVES>;
+  static constexpr int NP = (STAGES + 2) / 2;          // A pair buffers
+  static constexpr int A_PAIR_BYTES = BM * 2 * BK * 2;
+  static constexpr int B_BYTES = BK * BN * 2;
+  static constexpr int B_OFF = NP * A_PAIR_BYTES;
+  static constexpr int MAIN_BYTES = B_OFF + STAGES * B_BYTES;
+  static constexpr int EPI_BYTES = WAVES * 32 * (G::WTN * 2 + 16);
+  static constexpr int LDS_BYTES = MAIN_BYTES > EPI_BYTES ? MAIN_BYTES : EPI_BYTES;
+};
+
+// Number of even j in [lo, hi].
+constexpr int count_even(int lo, int hi) {
+  int n = 0;
+  for (int j = lo; j <= hi; ++j) n += (j % 2 == 0) ? 1 : 0;
+  return n;
+}
+
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+__global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pair_kernel(const uint16_t* __restrict__ lhs,
+                                                                         const uint16_t* __restrict__ rhs,
+                                                                         uint16_t* __restrict__ out, int M, int N,
+                                                                         int K, int group_m) {
+  using C = PairCfg<BM, BN, BK, WAVES, STAGES>;
+  using G = typename C::G;
+  static_assert(G::ok, "illegal wave grid");
+  static_assert(BK % 32 == 0 && BK <= 64, "BK of 32 or 64 (pairs of 64 or 128 columns)");
+  static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages for B");
+  constexpr int TM = G::TM, TN = G::TN, KS = BK / 16, KC = BK / 8, NP = C::NP;
+  using LA = KPanelLoader<2 * BK, BM, WAVES>;
+  using LB = PanelLoader<BK, BN, WAVES>;
+  constexpr int NLA = LA::LOADS_PER_TILE, NLB = LB::LOADS_PER_TILE;
+  // vm_wait<n> counts assume every wave issues the same number of loads.
+  static_assert(LA::EVEN && LB::EVEN, "every wave issues the same number of loads");
+  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  int tmi, tni;
+  tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
+  const int m0 = tmi * BM, n0 = tni * BN;
+  const int wm0 = (wave / G::WN) * G::WTM;
+  const int wn0 = (wave % G::WN) * G::WTN;
+
+  const uint32_t a_bytes = (uint32_t)K * (uint32_t)M * 2u;
+  const uint32_t b_bytes = (uint32_t)K * (uint32_t)N * 2u;
+  const int KT = (K + BK - 1) / BK;
+  const int UT = (KT + 1) / 2;  // A pairs
+  LA la;
+  LB lb;
+  la.init(wave, lane, m0, K, K - (UT - 1) * 2 * BK, a_bytes);
+  lb.init(wave, lane, n0, N);
+  const uint32_t kstep_pair = (uint32_t)(2 * BK) * 2u;
+  const uint32_t kstep_b = (uint32_t)BK * (uint32_t)N * 2u;
+  TrFrag<BN, TN> fb;
+  fb.init(lane, wn0);
+  // A operand: lane l reads row l%32 of a fragment, K chunk h*KC + 2*kk +
+  // l/32 of the pair row (h: which tile of the pair), at its k_swz slot.
+  const int arow = (wm0 + (lane & 31)) * (4 * BK);
+  const int aswz = k_swz<2 * BK>(wm0 + (lane & 31));
+  int akoff[2][KS];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) akoff[h][kk] = 16 * ((h * KC + 2 * kk + (lane >> 5)) ^ aswz);
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x16_t{};
+  bf16x8_t af[2][TM], bf[2][TN];
+  constexpr int NF = TM + TN;
+  // Operand f of sub-step kk of the tile in B stage `stage`, pair buffer
+  // `pb`, half `h`: A0, B0 .. B(TN-1), A1 .. A(TM-1).
+  auto read_frag = [&](int stage, int pb, int h, int kk, int buf, int f) {
+    if (f == 0 || f > TN) {
+      const int t = f == 0 ? 0 : f - TN;
+      af[buf][t] = __builtin_bit_cast(
+          bf16x8_t, *(MI_LDS u32x4_t*)((MI_LDS char*)smem + pb * C::A_PAIR_BYTES + arow + t * 32 * (4 * BK) +
+                                        akoff[h][kk]));
+    } else {
+      const int t = f - 1;
+      const int bbase = C::B_OFF + stage * C::B_BYTES;
+      bf[buf][t] = read_tr_frag(smem, bbase + (kk * 16) * (BN * 2) + fb.off[t],
+                                bbase + (kk * 16 + 4) * (BN * 2) + fb.off[t]);
+    }
+  };
+  auto read_frags = [&](int stage, int pb, int h, int kk, int buf) {
+#pragma unroll
+    for (int f = 0; f < NF; ++f) read_frag(stage, pb, h, kk, buf, f);
+  };
+  auto mfmas = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[buf][j], af[buf][i], acc[i][j], 0, 0, 0);
+  };
+  // Tiles and pairs past the end are clamped to the last one (re-read into
+  // a buffer that is never consumed), so every group has a static size.
+  auto clamp = [&](int kt) { return kt < KT ? kt : KT - 1; };
+  auto clamp_pair = [&](int u) { return u < UT ? u : UT - 1; };
+  // Load q of the group that brings tile j: the B loads of tile j, then
+  // (j even) the A loads of pair j/2.
+  auto issue_one = [&](int q, int j) {
+    if (q < NLB) {
+      lb.issue_at(q, make_rsrc_from(rhs, b_bytes, (uint32_t)clamp(j) * kstep_b), smem,
+                  C::B_OFF + (j % STAGES) * C::B_BYTES);
+    } else {
+      const int u = clamp_pair(j / 2);
+      la.issue_at(q - NLB, make_rsrc_from(lhs, a_bytes, (uint32_t)u * kstep_pair), smem,
+                  ((j / 2) % NP) * C::A_PAIR_BYTES, u == UT - 1);
+    }
+  };
+
+  // Prologue: the groups of tiles 0 .. STAGES-1, then wait for tile 0.
+#pragma unroll
+  for (int j = 0; j < STAGES; ++j) {
+#pragma unroll
+    for (int q = 0; q < NLB + (j % 2 == 0 ? NLA : 0); ++q) issue_one(q, j);
+  }
+  vm_wait<(STAGES - 1) * NLB + NLA * count_even(1, STAGES - 1)>();
+  __syncthreads();
+  read_frags(0, 0, 0, 0, 0);
+
+  // Tile t = t0 + I of a round (t0 a multiple of the round length, so even).
+  constexpr int UR = std::lcm(STAGES, 2 * NP);
+  auto tile = [&](int t, auto i_c) __attribute__((always_inline)) {
+    constexpr int I = decltype(i_c)::value;
+    constexpr int cur = I % STAGES, pb = (I / 2) % NP, h = I % 2;
+    constexpr int nxt = (I + 1) % STAGES, npb = ((I + 1) / 2) % NP, nh = (I + 1) % 2;
+    constexpr int WAIT = (STAGES - 2) * NLB + NLA * count_even(I + 2, I + STAGES - 1);
+    constexpr int NI = NLB + ((I + STAGES) % 2 == 0 ? NLA : 0);  // loads of the group issued here
+#pragma unroll
+    for (int kk = 0; kk + 1 < KS; ++kk) {
+      read_frags(cur, pb, h, kk + 1, (kk + 1) & 1);
+      mfmas(kk & 1);
+      interleave_mfma_ds<TM * TN, 2 * NF>();
+    }
+    vm_wait<WAIT>();
+    __syncthreads();
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      read_frag(nxt, npb, nh, 0, 0, f);
+#pragma unroll
+      for (int q = f * NI / NF; q < (f + 1) * NI / NF; ++q) issue_one(q, t + STAGES);
+    }
+    mfmas((KS - 1) & 1);
+    interleave_mfma_ds<TM * TN, 2 * NF>();
+  };
+  int t0 = 0;
+  for (; t0 + UR < KT; t0 += UR)
+    static_for<UR>([&](auto i_c) __attribute__((always_inline)) { tile(t0 + i_c(), i_c); });
+  static_while<UR>([&](auto i_c) __attribute__((always_inline)) {
+    if (t0 + i_c() + 1 >= KT) return false;
+    tile(t0 + i_c(), i_c);
+    return true;
+  });
+  // Last tile: no further loads.
+  const int tl = KT - 1;
+  const int cur = tl % STAGES, pb = (tl / 2) % NP, h = tl % 2;
+#pragma unroll
+  for (int kk = 0; kk < KS; ++kk) {
+    if (kk + 1 < KS) read_frags(cur, pb, h, kk + 1, (kk + 1) & 1);
+    mfmas(kk & 1);
+    interleave_mfma_ds<TM * TN, 2 * NF>();
+  }
+  wait_vmem();
+  __syncthreads();  // the epilogue reuses the panel buffers
+
+  float one[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) one[i] = 1.0f;
+  store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
+}
+
+}  // namespace mi
