@@ -27,7 +27,9 @@ library default), ``--only-kernel`` (skip the sweep, the fused pair and the
 CPU baseline: the command profiled under rocprofv3 PMC runs),
 ``--calibrate-copy-mib N`` (run one device copy of N MiB first, the PMC
 scale reference), ``--cpu-seconds`` (CPU baseline budget), ``--config NAME``
-(time this tile config instead of sweeping).
+(time this tile config instead of sweeping), ``--workload c3`` (time the
+fused rmsnorm_matmul at 4096^3 instead of the C2 matmul: the command the C3
+kernel profiles are taken with; the default line is always C2).
 """
 
 from __future__ import annotations
@@ -63,6 +65,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--sweep-reps", type=int, default=20)
     ap.add_argument("--config", default="", help="tile config name (e.g. bm256_bn256_bk32_w4_s3_v1) instead of the sweep")
+    ap.add_argument("--workload", choices=["c2", "c3"], default="c2",
+                    help="c2: lhsT.rhs matmul 8192^3 (the metric); c3: rmsnorm_matmul 4096^3 (profiling)")
     return ap.parse_args()
 
 
@@ -162,13 +166,13 @@ def cpu_baseline(budget_s: float) -> dict:
     }
 
 
-def recorded_traffic(cfg_name: str):
+def recorded_traffic(fam: str, s: int, cfg_name: str):
     try:
         with open(TRAFFIC_FILE) as f:
             rec = json.load(f)
     except (OSError, ValueError):
         return None
-    entry = rec.get(f"matmul_lhsT_rhs:{M}x{N}x{K}:{cfg_name}")
+    entry = rec.get(f"{fam}:{s}x{s}x{s}:{cfg_name}")
     return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
@@ -197,17 +201,21 @@ def main() -> int:
         log(f"calibration copy of {args.calibrate_copy_mib} MiB done")
         del src, dst
 
+    fam, s = ("matmul_lhsT_rhs", M) if args.workload == "c2" else ("rmsnorm_matmul", 4096)
     if args.config:
         cfg = kl.TileConfig.from_name(args.config)
     else:
-        cfg, _ = sweep("matmul_lhsT_rhs", M, N, K, args.sweep_reps, args.no_tune or args.only_kernel)
-    specs = input_specs("matmul_lhsT_rhs", M, N, K)
-    d = upload(generate_tensors(specs, 0, default_dists("matmul_lhsT_rhs", K)), specs, dev)
-    a, b = d["lhs_T"], d["rhs"]
-    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+        cfg, _ = sweep(fam, s, s, s, args.sweep_reps, args.no_tune or args.only_kernel)
+    specs = input_specs(fam, s, s, s)
+    d = upload(generate_tensors(specs, 0, default_dists(fam, s)), specs, dev)
+    out = torch.empty((s, s), dtype=torch.bfloat16, device=dev)
 
-    def step():
-        kl.matmul_lhsT_rhs(a, b, cfg=cfg, out=out)
+    if fam == "matmul_lhsT_rhs":
+        def step():
+            kl.matmul_lhsT_rhs(d["lhs_T"], d["rhs"], cfg=cfg, out=out)
+    else:
+        def step():
+            kl.rmsnorm_matmul(d["lhs"], d["rhs"], d["gamma"], cfg=cfg, out=out)
 
     for _ in range(args.warmup):
         step()
@@ -223,7 +231,7 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     kern_s = ev0.elapsed_time(ev1) * 1e-3 / args.steps
-    flop = 2.0 * M * N * K
+    flop = 2.0 * s * s * s
     value = flop * args.steps / wall / 1e12
     achieved = flop / kern_s / 1e12
     log(f"timed {args.steps} steps: wall {wall * 1e3:.1f} ms, {value:.1f} TFLOP/s; kernel avg {kern_s * 1e6:.1f} us")
@@ -240,10 +248,13 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic: lhsT, rhs ~ U(-1,1) seed 0 rounded to bf16, resident in HBM",
+        "data": "synthetic: lhsT, rhs ~ U(-1,1) seed 0 rounded to bf16, resident in HBM" if fam == "matmul_lhsT_rhs"
+        else "synthetic: x ~ N(0,1), gamma = 1 + 0.1 N(0,1), W ~ N(0, 1/64), seed 0, bf16, resident in HBM",
         "config": {
-            "workload": "lhsT[8192,8192]·rhs[8192,8192] bf16 matmul, fp32 accumulate, bf16 out (benchmark config C2)",
-            "kernel": "mm_lhsT_rhs_bf16",
+            "workload": "lhsT[8192,8192]·rhs[8192,8192] bf16 matmul, fp32 accumulate, bf16 out (benchmark config C2)"
+            if fam == "matmul_lhsT_rhs" else
+            "rmsnorm(x[4096,4096])*gamma[4096] . W[4096,4096] bf16, fp32 accumulate (benchmark config C3)",
+            "kernel": "mm_lhsT_rhs_bf16" if fam == "matmul_lhsT_rhs" else "rmsnorm_matmul_bf16",
             "tile_config": cfg.name,
             "autotuned": not (args.no_tune or args.only_kernel or args.config),
             "pct_mfma_peak": round(100.0 * value / PEAK_BF16_TFLOPS, 2),
@@ -254,10 +265,10 @@ def main() -> int:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": recorded_traffic(cfg.name),
+            "traffic": recorded_traffic(fam, s, cfg.name),
         },
     }
-    if not args.only_kernel:
+    if not args.only_kernel and fam == "matmul_lhsT_rhs":
         line["fused"] = fused_pair(args.sweep_reps, args.no_tune)
         log(f"fused pair: {line['fused']}")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
