@@ -96,7 +96,7 @@ def test_cfg_check_rejects_unknown_kernel_and_null():
                                    (1024, 4096, 14336), (16, 28672, 8192), (64, 28672, 8192), (128, 28672, 8192),
                                    (256, 512, 512)])
 def test_default_configs_are_legal_at_baseline_shapes(M, N, K):
-    for fam in ("matmul_lhsT_rhs", "rmsnorm_matmul"):
+    for fam in ("matmul_lhsT_rhs", "rmsnorm_matmul", "matmul_lhs_rhs"):
         cfg = default_config(fam, M, N, K)
         assert check(fam, cfg, M, N, K)[0] == 0, (fam, cfg)
     assert check("matmul_lhsT_rhs_f32", default_config("matmul_lhsT_rhs_f32", 256, 512, 512), 256, 512, 512)[0] == 0
