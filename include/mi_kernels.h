@@ -60,7 +60,8 @@ enum {
  *   variant                   : kernel-specific pipeline (every variant computes
  *                               the same function):
  *     matmul         0 plain double buffer; 1 software-pipelined LDS-direct
- *                    loads; 2 register prefetch ring (skinny shapes)
+ *                    loads; 2 register prefetch ring (skinny shapes); 3 as 1
+ *                    with rhs read non-temporally (streamed once: skinny M)
  *     matmul_lhs_rhs 0 the software-pipelined core (block_k >= 32, 2..4 stages);
  *                    1 the same with the K-contiguous A panel loaded two K
  *                    tiles per load (block_k 32 or 64)

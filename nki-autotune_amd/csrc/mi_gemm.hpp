@@ -94,9 +94,16 @@ __device__ __forceinline__ void vm_wait() {
 // Issued as inline assembly so that the compiler does not treat it as a
 // store that every later LDS read must wait for: the kernels order these
 // loads against LDS reads themselves (vm_wait / wait_vmem, then a barrier).
+// NT sets the non-temporal cache policy: data read once (a streamed
+// operand) then does not displace reused data in L2 and the MALL, which
+// nearly doubles the read bandwidth of a large streamed operand.
+template <bool NT = false>
 __device__ __forceinline__ void lds_dma16(__amdgpu_buffer_rsrc_t rs, char* lds, uint32_t voff) {
   const uint32_t m0 = (uint32_t)(uintptr_t)(MI_LDS char*)lds;
-  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
+  if constexpr (NT)
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen nt lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
+  else
+    asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(rs), "{m0}"(m0) : "memory");
 }
 
 // Wave grid: WM x WN waves, each owning a (BM/WM) x (BN/WN) block that is
@@ -210,8 +217,9 @@ struct PanelLoader {
   }
   // Load j of the K tile that the descriptor `rs_kt` starts at
   // (make_rsrc_from with the tile's byte offset).
+  template <bool NT = false>
   __device__ __forceinline__ void issue_at(int j, __amdgpu_buffer_rsrc_t rs_kt, char* smem, int base) const {
-    if (EVEN || active[j]) lds_dma16(rs_kt, smem + base + lds_off[j], voff[j]);
+    if (EVEN || active[j]) lds_dma16<NT>(rs_kt, smem + base + lds_off[j], voff[j]);
   }
   // Number of LDS-direct loads one wave issues per K tile.
   static constexpr int LOADS_PER_TILE = PER_WAVE;
@@ -522,7 +530,7 @@ struct PipeCfg {
 // lhsT[K,M] (M contiguous; MN-swizzled panel, transposing operand reads),
 // AK = true takes lhs[M,K] (K contiguous; K-swizzled panel, one
 // ds_read_b128 per operand fragment, no transpose).
-template <int BM, int BN, int BK, int WAVES, int STAGES, bool AK>
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool AK, bool NTB = false>
 __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, const uint16_t* __restrict__ rhs,
                                              uint16_t* __restrict__ out, int M, int N, int K, int group_m,
                                              char* smem) {
@@ -618,7 +626,7 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
       else
         la.issue_at(q, make_rsrc_from(a, a_bytes, (uint32_t)kt * kstep_a), smem, stage * C::STAGE_BYTES);
     } else
-      lb.issue_at(q - LA::LOADS_PER_TILE, make_rsrc_from(rhs, b_bytes, (uint32_t)kt * kstep_b), smem,
+      lb.template issue_at<NTB>(q - LA::LOADS_PER_TILE, make_rsrc_from(rhs, b_bytes, (uint32_t)kt * kstep_b), smem,
                   stage * C::STAGE_BYTES + C::A_BYTES);
   };
 
@@ -690,13 +698,15 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
 }
 
-template <int BM, int BN, int BK, int WAVES, int STAGES>
+// NTB: rhs loaded with the non-temporal cache policy (matmul variant 3, for
+// shapes where rhs is streamed once: skinny M).
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool NTB = false>
 __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const uint16_t* __restrict__ lhsT,
                                                                           const uint16_t* __restrict__ rhs,
                                                                           uint16_t* __restrict__ out, int M, int N,
                                                                           int K, int group_m) {
   __shared__ __attribute__((aligned(1024))) char smem[PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
-  mm_pipe_body<BM, BN, BK, WAVES, STAGES, false>(lhsT, rhs, out, M, N, K, group_m, smem);
+  mm_pipe_body<BM, BN, BK, WAVES, STAGES, false, NTB>(lhsT, rhs, out, M, N, K, group_m, smem);
 }
 
 // out[M,N] = lhs[M,K] . rhs[K,N] with lhs K-contiguous (matmul_lhs_rhs).

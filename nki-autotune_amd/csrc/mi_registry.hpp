@@ -48,9 +48,9 @@ hipError_t launch_mm_bf16(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int W, int S>
+template <int BM, int BN, int BK, int W, int S, bool NTB = false>
 hipError_t launch_mm_pipe(const MiArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+  hipLaunchKernelGGL((mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB>), dim3(grid_tiles(a.M, a.N, BM, BN)),
                      dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K,
                      a.group_m);
   return hipGetLastError();
@@ -151,6 +151,9 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
 #define MI_MMP_INST(BM, BN, BK, W, S)                                                                          \
   template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*,  \
                                                                            uint16_t*, int, int, int, int);
+#define MI_MMPN_INST(BM, BN, BK, W, S)                                                                            \
+  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true>(const uint16_t*, const uint16_t*, \
+                                                                                 uint16_t*, int, int, int, int);
 #define MI_MMK_INST(BM, BN, BK, W, S)                                                                         \
   template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*,    \
                                                                           uint16_t*, int, int, int, int);
@@ -198,6 +201,10 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
 #define MI_MMP_ROW(BM, BN, BK, W, S)                                                               \
   {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 1}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
    &launch_mm_pipe<BM, BN, BK, W, S>},
+// Pipelined matmul with rhs streamed non-temporally: variant 3.
+#define MI_MMPN_ROW(BM, BN, BK, W, S)                                                              \
+  {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 3}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_mm_pipe<BM, BN, BK, W, S, true>},
 // matmul_lhs_rhs (K-contiguous lhs) on the pipelined core: variant 0.
 #define MI_MMK_ROW(BM, BN, BK, W, S)                                                                \
   {MI_KERNEL_MATMUL_LHS_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 0}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \

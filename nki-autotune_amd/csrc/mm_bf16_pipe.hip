@@ -2,7 +2,8 @@
 // 4-wave blocks with 128x128 (or 128x64, 64x64) per wave at one wave per
 // SIMD, and 8-wave blocks at two waves per SIMD; 2 to 4 LDS stages.  The
 // small-block, deep-pipeline rows serve the skinny HBM-bound shapes, which
-// need many loads in flight per CU rather than MFMA throughput.
+// need many loads in flight per CU rather than MFMA throughput.  Every config
+// is also instantiated as variant 3, which loads rhs non-temporally.
 #include "mi_registry.hpp"
 
 #define MI_PIPE_CONFIGS(X)   \
@@ -33,9 +34,10 @@
 
 namespace mi {
 MI_PIPE_CONFIGS(MI_MMP_INST)
+MI_PIPE_CONFIGS(MI_MMPN_INST)
 
 const MiEntry* table_mm_pipe(int* n) {
-  static const MiEntry t[] = {MI_PIPE_CONFIGS(MI_MMP_ROW)};
+  static const MiEntry t[] = {MI_PIPE_CONFIGS(MI_MMP_ROW) MI_PIPE_CONFIGS(MI_MMPN_ROW)};
   *n = (int)(sizeof(t) / sizeof(t[0]));
   return t;
 }
