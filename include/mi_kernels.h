@@ -64,7 +64,8 @@ enum {
  *                    with rhs read non-temporally (streamed once: skinny M)
  *     matmul_lhs_rhs 0 the software-pipelined core (block_k >= 32, 2..4 stages);
  *                    1 the same with the K-contiguous A panel loaded two K
- *                    tiles per load (block_k 32 or 64)
+ *                    tiles per load (block_k 32 or 64); 2 as 0 with rhs read
+ *                    non-temporally (skinny M)
  *     rmsnorm_matmul 0 / 1 x scaled while staged (1/rms on the accumulators /
  *                    from a prologue pass); 2 / 3 LDS ring of raw x; 4 / 5 x
  *                    through a 2 / 3 tile register ring on the pipelined

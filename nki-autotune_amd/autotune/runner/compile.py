@@ -59,7 +59,7 @@ def _instance(fam: str, cfg) -> tuple[str, str, str] | None:
         macro = {0: "MI_MM", 1: "MI_MMP", 2: "MI_MMR", 3: "MI_MMPN"}.get(v)
         return (f"{macro}_INST", f"{macro}_ROW", f"{base}, {s}") if macro else None
     if fam == "matmul_lhs_rhs":
-        macro = {0: "MI_MMK", 1: "MI_MMKP"}.get(v)
+        macro = {0: "MI_MMK", 1: "MI_MMKP", 2: "MI_MMKN"}.get(v)
         return (f"{macro}_INST", f"{macro}_ROW", f"{base}, {s}") if macro else None
     if fam == "rmsnorm_matmul":
         if v in (0, 1):

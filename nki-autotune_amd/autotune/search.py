@@ -51,7 +51,7 @@ class Atom(NamedTuple):
 # Variants of each family that compute the same function (include/mi_kernels.h).
 FAMILY_VARIANTS = {
     "matmul_lhsT_rhs": (0, 1, 2, 3),
-    "matmul_lhs_rhs": (0, 1),
+    "matmul_lhs_rhs": (0, 1, 2),
     "rmsnorm_matmul": tuple(range(11)),
     "matmul_lhsT_rhs_f32": (0,),
 }

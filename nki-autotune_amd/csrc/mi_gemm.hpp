@@ -709,14 +709,15 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
   mm_pipe_body<BM, BN, BK, WAVES, STAGES, false, NTB>(lhsT, rhs, out, M, N, K, group_m, smem);
 }
 
-// out[M,N] = lhs[M,K] . rhs[K,N] with lhs K-contiguous (matmul_lhs_rhs).
-template <int BM, int BN, int BK, int WAVES, int STAGES>
+// out[M,N] = lhs[M,K] . rhs[K,N] with lhs K-contiguous (matmul_lhs_rhs);
+// NTB: rhs read non-temporally (variant 2, skinny M).
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool NTB = false>
 __global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pipe_kernel(const uint16_t* __restrict__ lhs,
                                                                          const uint16_t* __restrict__ rhs,
                                                                          uint16_t* __restrict__ out, int M, int N,
                                                                          int K, int group_m) {
   __shared__ __attribute__((aligned(1024))) char smem[PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
-  mm_pipe_body<BM, BN, BK, WAVES, STAGES, true>(lhs, rhs, out, M, N, K, group_m, smem);
+  mm_pipe_body<BM, BN, BK, WAVES, STAGES, true, NTB>(lhs, rhs, out, M, N, K, group_m, smem);
 }
 
 // ---------------------------------------------------------------------------

@@ -56,9 +56,9 @@ hipError_t launch_mm_pipe(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int W, int S>
+template <int BM, int BN, int BK, int W, int S, bool NTB = false>
 hipError_t launch_mm_lhs(const MiArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+  hipLaunchKernelGGL((mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB>), dim3(grid_tiles(a.M, a.N, BM, BN)),
                      dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K,
                      a.group_m);
   return hipGetLastError();
@@ -157,6 +157,9 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
 #define MI_MMK_INST(BM, BN, BK, W, S)                                                                         \
   template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*,    \
                                                                           uint16_t*, int, int, int, int);
+#define MI_MMKN_INST(BM, BN, BK, W, S)                                                                          \
+  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true>(const uint16_t*, const uint16_t*, \
+                                                                                uint16_t*, int, int, int, int);
 #define MI_MMKP_INST(BM, BN, BK, W, S)                                                                        \
   template __global__ void mm_lhs_rhs_bf16_pair_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*,    \
                                                                           uint16_t*, int, int, int, int);
@@ -209,6 +212,10 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
 #define MI_MMK_ROW(BM, BN, BK, W, S)                                                                \
   {MI_KERNEL_MATMUL_LHS_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 0}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
    &launch_mm_lhs<BM, BN, BK, W, S>},
+// matmul_lhs_rhs with rhs read non-temporally: variant 2.
+#define MI_MMKN_ROW(BM, BN, BK, W, S)                                                              \
+  {MI_KERNEL_MATMUL_LHS_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 2}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_mm_lhs<BM, BN, BK, W, S, true>},
 // matmul_lhs_rhs with A loaded two K tiles at a time: variant 1.
 #define MI_MMKP_ROW(BM, BN, BK, W, S)                                                               \
   {MI_KERNEL_MATMUL_LHS_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 1}, PairCfg<BM, BN, BK, W, S>::LDS_BYTES, \

@@ -73,7 +73,7 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (LHS, TileConfig(256, 256, 32, 4, 3), (8192, 8192, 8192), _lib.MI_OK),
         (LHS, TileConfig(256, 256, 32, 4, 3), (1024, 1024, 1020), _lib.MI_E_ALIGN),      # K % 8 (K-contiguous lhs)
         (LHS, TileConfig(128, 128, 16, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),       # pipelined core: bk >= 32
-        (LHS, TileConfig(256, 256, 32, 4, 3, variant=2), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),
+        (LHS, TileConfig(256, 256, 32, 4, 3, variant=3), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),
         (LHS, TileConfig(256, 256, 64, 4, 2), (65536, 65536, 65536), _lib.MI_E_RANGE),
     ],
 )

@@ -114,7 +114,7 @@ def test_render_parse_roundtrip_and_aliases():
     assert rcompile.problem_shape("matmul_lhs_rhs", input_specs("matmul_lhs_rhs", 64, 96, 128)) == (64, 96, 128)
 
 
-@pytest.mark.parametrize("fam,variants", [("matmul_lhsT_rhs", (0, 1, 2, 3)), ("matmul_lhs_rhs", (0, 1)),
+@pytest.mark.parametrize("fam,variants", [("matmul_lhsT_rhs", (0, 1, 2, 3)), ("matmul_lhs_rhs", (0, 1, 2)),
                                           ("rmsnorm_matmul", tuple(range(11)))])
 def test_jit_units_instantiate_every_variant(fam, variants, tmp_path):
     """The generated single-config unit of every variant names a real template
@@ -142,7 +142,7 @@ def test_jit_units_instantiate_every_variant(fam, variants, tmp_path):
                                "-fsyntax-only", str(unit)], capture_output=True, text=True)
         assert proc.returncode == 0, (fam, v, proc.stderr[-2000:])
     # a variant without a template is reported, not guessed
-    assert "prebuilt-only" in rcompile.render_source("matmul_lhs_rhs", TileConfig(128, 256, 32, 4, 2, variant=2))
+    assert "prebuilt-only" in rcompile.render_source("matmul_lhs_rhs", TileConfig(128, 256, 32, 4, 2, variant=3))
 
 
 def test_compile_one_prebuilt_and_rejections(tmp_path):
