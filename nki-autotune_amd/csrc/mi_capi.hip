@@ -87,15 +87,19 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
     // chunks: block_m / block_n must be powers of two in [32, 512] and
     // block_k a power of two in [16, 128] ([32, 128] for the fused kernel,
     // whose x rows are reduced over BK/8 lanes).
-    // The pipelined matmul (variant 1) double-buffers MFMA operands across
-    // K sub-steps of 16 and needs an even number of them.
-    const int kmin = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 || kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 ||
-                             (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && c.variant == 1)
-                         ? 32
-                         : 16;
-    if (!pow2_in(c.block_m, 32, 512) || !pow2_in(c.block_n, 32, 512) || !pow2_in(c.block_k, kmin, 128))
+    // The pipelined matmuls (lhsT variants 1 and 3, every matmul_lhs_rhs
+    // variant) double-buffer MFMA operands across K sub-steps of 16, need an
+    // even number of them, and keep a ring of 2..4 LDS stages; the paired
+    // K-contiguous loads (matmul_lhs_rhs variant 1) take block_k 32 or 64.
+    const bool pipelined = kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 ||
+                           (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (c.variant == 1 || c.variant == 3));
+    const int kmin = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 || pipelined ? 32 : 16;
+    const int kmax = kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 && c.variant == 1 ? 64 : 128;
+    if (!pow2_in(c.block_m, 32, 512) || !pow2_in(c.block_n, 32, 512) || !pow2_in(c.block_k, kmin, kmax))
       return fail(MI_E_TILE, "block sizes bm=%d bn=%d bk=%d outside the template range", c.block_m, c.block_n,
                   c.block_k);
+    if (pipelined && (c.lds_stages < 2 || c.lds_stages > 4))
+      return fail(MI_E_TILE, "the pipelined kernels take 2..4 LDS stages, not %d", c.lds_stages);
   }
   if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_F32 && !wave_grid_ok(c.block_m, c.block_n, c.waves))
     return fail(MI_E_WAVE_TILE, "%d waves cannot tile a %dx%d block in 32x32 MFMA tiles", c.waves, c.block_m,

@@ -75,6 +75,9 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (LHS, TileConfig(128, 128, 16, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),       # pipelined core: bk >= 32
         (LHS, TileConfig(256, 256, 32, 4, 3, variant=3), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),
         (LHS, TileConfig(256, 256, 64, 4, 2), (65536, 65536, 65536), _lib.MI_E_RANGE),
+        (LHS, TileConfig(64, 128, 128, 4, 3, variant=1), (1024, 1024, 1024), _lib.MI_E_TILE),    # pairs: bk <= 64
+        (MM, TileConfig(256, 256, 32, 8, 1, variant=1), (1024, 1024, 1024), _lib.MI_E_TILE),     # pipelined: >= 2 stages
+        (MM, TileConfig(256, 256, 16, 8, 2, variant=3), (1024, 1024, 1024), _lib.MI_E_TILE),     # pipelined: bk >= 32
     ],
 )
 def test_cfg_check_codes(kid, cfg, shape, code):
