@@ -158,3 +158,22 @@ def test_bf16_baseline_shapes(gpu, M, N, K, dist):
     del ref
     out2 = kl.matmul_lhsT_rhs(a, b * 2)
     assert torch.equal(out2, out * 2)
+
+
+def test_empty_contraction_writes_zeros(gpu):
+    """K = 0: every family writes an all-zero output (a fill kernel, also for odd M*N)."""
+    import torch
+
+    kl = _kl()
+    for M, N in ((3, 5), (64, 96)):
+        for dt in (torch.bfloat16, torch.float32):
+            out = torch.full((M, N), float("nan"), dtype=dt, device=gpu)
+            kl.matmul_lhsT_rhs(torch.empty((0, M), dtype=dt, device=gpu), torch.empty((0, N), dtype=dt, device=gpu),
+                               out=out)
+            torch.cuda.synchronize()
+            assert torch.count_nonzero(out).item() == 0, (M, N, dt)
+        out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+        kl.matmul_lhs_rhs(torch.empty((M, 0), dtype=torch.bfloat16, device=gpu),
+                          torch.empty((0, N), dtype=torch.bfloat16, device=gpu), out=out)
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(out).item() == 0, (M, N)
