@@ -71,7 +71,8 @@ enum {
  *                    through a 2 / 3 tile register ring on the pipelined
  *                    matmul core; 6..9 x loaded straight into MFMA operands
  *                    (need K <= 16384 - D*block_k); 10 x loaded two K tiles
- *                    per instruction (block_k 32, K <= 16384 - 4*block_k)
+ *                    per instruction (block_k 32, K <= 16384 - 4*block_k);
+ *                    11 / 12 as 4 / 5 with W read non-temporally (skinny M)
  */
 typedef struct {
   int block_m, block_n, block_k, waves, lds_stages, split_k, group_m, variant;

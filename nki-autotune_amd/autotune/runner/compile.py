@@ -68,6 +68,8 @@ def _instance(fam: str, cfg) -> tuple[str, str, str] | None:
             return ("MI_RMSR_INST", "MI_RMSR_ROW", f"{base}, {v - 2}") if s == 2 else None
         if v in (4, 5):
             return "MI_RMSX_INST", "MI_RMSX_ROW", f"{base}, {s}, {v - 2}"
+        if v in (11, 12):
+            return "MI_RMSXN_INST", "MI_RMSXN_ROW", f"{base}, {s}, {v - 9}"
         if 6 <= v <= 9:
             d, wmx = 2 + ((v - 6) & 1), (v - 6) >> 1
             return "MI_RMSD_INST", "MI_RMSD_ROW", f"{base}, {s}, {wmx}, {d}, {v}"

@@ -52,7 +52,7 @@ class Atom(NamedTuple):
 FAMILY_VARIANTS = {
     "matmul_lhsT_rhs": (0, 1, 2, 3),
     "matmul_lhs_rhs": (0, 1, 2),
-    "rmsnorm_matmul": tuple(range(11)),
+    "rmsnorm_matmul": tuple(range(13)),
     "matmul_lhsT_rhs_f32": (0,),
 }
 

@@ -136,12 +136,14 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
     b_span = kpad * (unsigned long long)N * 2ull;
     if (a_span > kMaxOffset || b_span > kMaxOffset)
       return fail(MI_E_RANGE, "operand spans exceed 32-bit buffer offsets (%llu, %llu bytes)", a_span, b_span);
-    // rmsnorm_matmul variants 4..10 stage gamma in LDS: K rounded up to the
-    // K step the kernel walks (variants 4/5: one tile; 6..9: D = 2 or 3
-    // tiles; 10: rounds of 4 tiles) must fit the instance's gamma entries.
+    // rmsnorm_matmul variants 4..12 stage gamma in LDS: K rounded up to the
+    // K step the kernel walks (variants 4/5/11/12: one tile; 6..9: D = 2 or
+    // 3 tiles; 10: rounds of 4 tiles) must fit the instance's gamma entries.
     // The limit holds with or without gamma (legality is gamma-agnostic).
     if (e->gamma_kmax > 0) {
-      const int d = c.variant == 10 ? 4 : c.variant >= 6 ? 2 + ((c.variant - 6) & 1) : 1;
+      const int d = c.variant == 10                      ? 4
+                    : c.variant >= 6 && c.variant <= 9 ? 2 + ((c.variant - 6) & 1)
+                                                       : 1;
       const long long span = (long long)d * c.block_k;
       if (((long long)K + span - 1) / span * span > e->gamma_kmax)
         return fail(MI_E_RANGE, "K=%d exceeds the %d gamma entries variant %d stages in LDS", K, e->gamma_kmax,
@@ -172,22 +174,33 @@ int zero_output(void* out, size_t n, void* stream) {
 }
 
 int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
-  (void)K;
+  // The autotune winners at the benchmark shapes, generalised by size:
+  // skinny M (decode) streams the weight once and takes the non-temporal
+  // variants; mid-size products take 128 x 128 tiles for enough workgroups;
+  // large ones the 256 x 256 pipelined core.
+  const bool mid = (long long)M * N <= 2048LL * 2048LL;
   mi_tile_cfg c = {256, 256, 64, 8, 2, 1, 8, 0};
   if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_F32) {
     c = {64, 64, 16, 4, 1, 1, 0, 0};
   } else if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16) {
-    if (M <= 32) c = {32, 256, 128, 4, 2, 1, 8, 0};
-    else if (M <= 64) c = {64, 256, 64, 4, 2, 1, 8, 0};
-    else if (M <= 128) c = {128, 128, 64, 4, 2, 1, 8, 0};
-    else if ((long long)M * N <= 4096LL * 4096LL) c = {128, 256, 64, 8, 2, 1, 8, 0};
+    if (M <= 32) c = {32, 128, 128, 4, 3, 1, 8, 3};
+    else if (M <= 64) c = {64, 128, 64, 4, 4, 1, 8, 3};
+    else if (M <= 128) c = {128, 128, 64, 4, 3, 1, 8, 3};
+    else if (mid) c = {128, 128, 64, 4, 3, 1, 8, 1};
+    else c = {256, 256, 32, 4, 3, 1, 8, 1};
   } else if (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16) {
-    c = {256, 256, 32, 4, 3, 1, 8, 0};
-    if (M <= 64) c = {64, 128, 64, 4, 4, 1, 8, 0};
-    else if (M <= 128) c = {128, 128, 64, 4, 3, 1, 8, 0};
+    if (M <= 128) c = {128, 128, 64, 4, 3, 1, 8, 2};
+    else if (mid) c = {128, 128, 64, 4, 3, 1, 8, 0};
+    else c = {256, 256, 32, 8, 3, 1, 8, 1};
   } else if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16) {
-    if (M <= 128) c = {64, 128, 64, 4, 2, 1, 8, 0};
-    else if ((long long)M * N <= 4096LL * 4096LL) c = {128, 256, 64, 8, 2, 1, 8, 0};
+    // The register-staged kernels keep gamma in LDS (K <= 8192 here); past
+    // that the LDS-staged kernel (variant 0) takes any K.
+    if (K > 8192) c = M <= 128 ? mi_tile_cfg{64, 128, 64, 4, 2, 1, 8, 0} : mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0};
+    else if (M <= 32) c = {32, 128, 64, 4, 3, 1, 8, 11};
+    else if (M <= 64) c = {64, 128, 64, 4, 3, 1, 8, 11};
+    else if (M <= 128) c = {128, 128, 64, 4, 3, 1, 8, 11};
+    else if (mid) c = {128, 128, 64, 4, 2, 1, 8, 4};
+    else c = {128, 512, 32, 8, 3, 1, 8, 4};
   }
   *cfg = c;
   return MI_OK;

@@ -101,16 +101,18 @@ hipError_t launch_rms_ring(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int W, int S, int XS>
+template <int BM, int BN, int BK, int W, int S, int XS, bool NTW = false>
 hipError_t launch_rms_xreg(const MiArgs& a, hipStream_t s) {
   if (a.g)
-    hipLaunchKernelGGL((rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, true>), dim3(grid_tiles(a.M, a.N, BM, BN)),
-                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
-                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, true, NTW>),
+                       dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
+                       (const uint16_t*)a.g, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps,
+                       a.group_m);
   else
-    hipLaunchKernelGGL((rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, false>), dim3(grid_tiles(a.M, a.N, BM, BN)),
-                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
-                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, false, NTW>),
+                       dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
+                       (const uint16_t*)a.g, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps,
+                       a.group_m);
   return hipGetLastError();
 }
 
@@ -183,6 +185,13 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
   template __global__ void rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, false>(                 \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
 
+// Variants 11 / 12: 4 / 5 with W read non-temporally (skinny M).
+#define MI_RMSXN_INST(BM, BN, BK, W, S, XS)                                                           \
+  template __global__ void rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, true, true>(            \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int); \
+  template __global__ void rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, false, true>(           \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
+
 // x operand straight to registers: variant 6 + (D-2) + 2*(wave grid transposed).
 #define MI_RMSD_INST(BM, BN, BK, W, S, WMX, D, V)                                                     \
   template __global__ void rmsnorm_mm_bf16_direct_kernel<BM, BN, BK, W, S, WMX, D, true>(             \
@@ -238,6 +247,10 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
 #define MI_RMSX_ROW(BM, BN, BK, W, S, XS)                                                                   \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 2 + XS}, XregCfg<BM, BN, BK, W, S>::LDS_BYTES, \
    &launch_rms_xreg<BM, BN, BK, W, S, XS>, XregCfg<BM, BN, BK, W, S>::GK_MAX},
+
+#define MI_RMSXN_ROW(BM, BN, BK, W, S, XS)                                                                  \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 9 + XS}, XregCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_rms_xreg<BM, BN, BK, W, S, XS, true>, XregCfg<BM, BN, BK, W, S>::GK_MAX},
 
 #define MI_RMSD_ROW(BM, BN, BK, W, S, WMX, D, V)                                                         \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, V}, DirectCfg<BM, BN, BK, W, S, WMX>::LDS_BYTES, \

@@ -1,5 +1,6 @@
 // mi_rms_xreg.hpp -- fused rmsnorm_matmul on the pipelined matmul core, with
-// the x panel staged through registers (rmsnorm_matmul variants 4 and 5).
+// the x panel staged through registers (rmsnorm_matmul variants 4 and 5;
+// 11 and 12 are the same with W read non-temporally).
 //
 //   out[M,N] = (x[M,K] * rsqrt(mean_k x^2 + eps) * gamma[K]) . W[K,N]
 //
@@ -75,7 +76,9 @@ __device__ __forceinline__ u32x4_t vload16(__amdgpu_buffer_rsrc_t rs, uint32_t v
 // Orders every later use of r after the preceding vm_wait.
 __device__ __forceinline__ void reg_ready(u32x4_t& r) { asm volatile("" : "+v"(r)); }
 
-template <int BM, int BN, int BK, int WAVES, int STAGES, int XS, bool HG, int SSQ_PARTS = 4>
+// NTW: W read non-temporally (variants 11 / 12: skinny M, where W is
+// streamed once).
+template <int BM, int BN, int BK, int WAVES, int STAGES, int XS, bool HG, bool NTW = false, int SSQ_PARTS = 4>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ w,
     uint16_t* __restrict__ out, int M, int N, int K, float inv_k, float eps, int group_m) {
@@ -160,7 +163,8 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   lb.init(wave, lane, n0, N);
   const uint32_t kstep_b = (uint32_t)BK * (uint32_t)N * 2u;
   auto issue_w = [&](int q, int kt, int stage) {
-    lb.issue_at(q, make_rsrc_from(w, w_bytes, (uint32_t)kt * kstep_b), smem, stage * C::STAGE_BYTES + C::A_BYTES);
+    lb.template issue_at<NTW>(q, make_rsrc_from(w, w_bytes, (uint32_t)kt * kstep_b), smem,
+                              stage * C::STAGE_BYTES + C::A_BYTES);
   };
   TrFrag<BN, TN> fb;
   fb.init(lane, wn0);

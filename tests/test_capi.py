@@ -67,6 +67,10 @@ def test_every_compiled_config_is_enumerable_and_legal():
         # four 32 KiB stages leave room for 7936 fp32 gamma entries
         (RMS, TileConfig(256, 256, 32, 8, 4, variant=4), (1024, 1024, 7968), _lib.MI_E_RANGE),
         (RMS, TileConfig(256, 256, 32, 8, 4, variant=4), (1024, 1024, 7936), _lib.MI_OK),
+        # variants 11 / 12 walk K one tile at a time, like 4 / 5
+        (RMS, TileConfig(128, 128, 32, 4, 3, variant=12), (1024, 1024, 8200), _lib.MI_E_RANGE),
+        (RMS, TileConfig(128, 128, 32, 4, 3, variant=12), (1024, 1024, 8192), _lib.MI_OK),
+        (RMS, TileConfig(64, 128, 64, 4, 2, variant=11), (16, 28672, 8192), _lib.MI_OK),
         (MM, TileConfig(128, 128, 48, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),
         (MM, TileConfig(512, 512, 32, 8, 1), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),  # legal, not prebuilt
         (MM, TileConfig(0, 128, 64, 4, 2), (1024, 1024, 1024), _lib.MI_E_ARGS),
@@ -103,6 +107,23 @@ def test_default_configs_are_legal_at_baseline_shapes(M, N, K):
         cfg = default_config(fam, M, N, K)
         assert check(fam, cfg, M, N, K)[0] == 0, (fam, cfg)
     assert check("matmul_lhsT_rhs_f32", default_config("matmul_lhsT_rhs_f32", 256, 512, 512), 256, 512, 512)[0] == 0
+
+
+def test_library_default_is_legal_everywhere():
+    """The C default (used when no config is passed and no tuned entry exists)
+    is a prebuilt, legal config over skinny, ragged, mid and large shapes,
+    including K past the gamma capacity of the register-staged fused kernels."""
+    L = _lib.lib()
+    for kid in (MM, LHS, RMS, F32):
+        for M in (8, 16, 24, 40, 64, 72, 128, 136, 200, 2048, 8192):
+            for N in (8, 136, 4096, 28672):
+                for K in (8, 264, 8192, 8200, 16384):
+                    if kid == F32 and M * N * K > 2 ** 30:
+                        continue
+                    c = _lib.MiTileCfg()
+                    assert L.mi_default_config(kid, M, N, K, ctypes.byref(c)) == _lib.MI_OK
+                    rc = L.mi_cfg_check(kid, ctypes.byref(c), M, N, K)
+                    assert rc == _lib.MI_OK, (kid, M, N, K, TileConfig.from_c(c), _lib.last_error())
 
 
 def test_entry_points_reject_bad_arguments_before_any_gpu_call():

@@ -58,7 +58,7 @@ def test_no_gamma_is_reference_kernel(gpu):
     assert _ok(rep), rep
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("variant", list(range(13)))
 def test_no_gamma_every_variant(gpu, variant):
     """gamma=None takes each kernel's no-gamma instance; K = 576 is not a multiple of 64."""
     import kernel_library as kl
@@ -73,7 +73,7 @@ def test_no_gamma_every_variant(gpu, variant):
         assert _ok(rep), (cfg, rep)
 
 
-@pytest.mark.parametrize("variant", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10])
+@pytest.mark.parametrize("variant", list(range(13)))
 def test_ragged_and_special_rows(gpu, variant):
     """Edge tiles (M, N not multiples of the block), K not a multiple of block_k; a zero row gives 0."""
     import torch
@@ -135,3 +135,21 @@ def test_baseline_c3_full_size(gpu):
         rep = rms_check(out[rows], expected)
         print(variant, rep)
         assert _ok(rep), rep
+
+
+def test_skinny_decode_shape(gpu):
+    """Decode-sized M (16 rows) against an 8192 x 28672 W: the non-temporal-W
+    variants 11 / 12 and the default config, every row vs the closed form."""
+    import kernel_library as kl
+
+    M, K, N = 16, 8192, 28672
+    print("skinny rmsnorm_matmul", M, K, N, flush=True)
+    d = rms_inputs(M, K, N, seed=3)
+    x, g, w = _dev(d["lhs"], gpu), _dev(d["gamma"], gpu), _dev(d["rhs"], gpu)
+    expected = orms.closed_form(d["lhs"], d["rhs"], d["gamma"])
+    cfgs = [kl.default_config("rmsnorm_matmul", M, N, K), kl.TileConfig(128, 128, 32, 4, 3, variant=11),
+            kl.TileConfig(64, 128, 64, 4, 2, variant=11), kl.TileConfig(128, 128, 32, 4, 3, variant=12),
+            kl.TileConfig(32, 128, 128, 4, 3, variant=11), kl.TileConfig(32, 128, 64, 4, 3, variant=11)]
+    for cfg in cfgs:
+        rep = rms_check(_host(kl.rmsnorm_matmul(x, w, g, cfg=cfg)), expected)
+        assert _ok(rep), (cfg, rep)
