@@ -16,7 +16,11 @@ one launch of that kernel on inputs resident in HBM.
   calibration) when that measurement for the same config is recorded in
   ``profiles/traffic.json``; otherwise null.
 * ``fused``: the rmsnorm_matmul kernel at 4096^3 (benchmark config C3) beside
-  the plain matmul at the same shape, each with its autotuned config.
+  the plain matmul at the same shape, each with its autotuned config; the
+  matmul both on its own U(-1,1) inputs and on the fused kernel's operands
+  (normalised x, W).
+* ``data_sensitivity``: the C2 kernel on all-zero and all-one inputs
+  (diagnostic: the chip's clock under MFMA load depends on operand data).
 * ``cpu_baseline``: the CPU oracle's tile-faithful emulation of the
   reference kernel's loop nest (fp32, numpy/BLAS) on a bounded column slice
   of the same workload, rank 0 only.
@@ -122,7 +126,18 @@ def fused_pair(reps: int, no_tune: bool) -> dict:
                                                                                   out=out_r), 40))
         tm.append(time_pair(mm, None, cfg_m, lambda d, _b, c: kl.matmul_lhsT_rhs(d["lhs_T"], d["rhs"], cfg=c,
                                                                                   out=out_m), 40))
-    t_r, t_m = sorted(tr)[2], sorted(tm)[2]
+    # The same matmul on the fused kernel's own operands: lhsT = the
+    # normalised, gamma-scaled x (bf16), rhs = W.  MI355X's clock under MFMA
+    # load depends on the operand data, so this is the like-for-like pair.
+    xf = r["lhs"].float()
+    xhat = (xf * torch.rsqrt(xf.pow(2).mean(1, keepdim=True) + 1e-6) * r["gamma"].float()).bfloat16()
+    same = {"lhs_T": xhat.t().contiguous(), "rhs": r["rhs"]}
+    del xf, xhat
+    ts = []
+    for _ in range(5):
+        ts.append(time_pair(same, None, cfg_m, lambda d, _b, c: kl.matmul_lhsT_rhs(d["lhs_T"], d["rhs"], cfg=c,
+                                                                                    out=out_m), 40))
+    t_r, t_m, t_s = sorted(tr)[2], sorted(tm)[2], sorted(ts)[2]
     fl = 2.0 * s ** 3
     return {
         "shape": [s, s, s],
@@ -131,7 +146,36 @@ def fused_pair(reps: int, no_tune: bool) -> dict:
         "matmul_tflops": round(fl / t_m / 1e12, 1),
         "matmul_config": cfg_m.name,
         "fused_over_matmul_time": round(t_r / t_m, 4),
+        "matmul_same_operands_tflops": round(fl / t_s / 1e12, 1),
+        "fused_over_same_operand_matmul_time": round(t_r / t_s, 4),
     }
+
+
+def data_sensitivity(cfg, steps: int = 20) -> dict:
+    """The C2 kernel and config on constant inputs (zeros, ones) instead of U(-1,1).
+
+    Same launches, same work; only the operand values differ.  MI355X lowers
+    its clock under MFMA load as the power the operand data draws rises, so
+    the constant-input rate shows what the kernel's issue rate reaches when
+    power does not limit it.  Diagnostic only: the metric is the U(-1,1)
+    figure."""
+    import torch
+
+    import kernel_library as kl
+    from autotune.runner.benchmark import time_launches
+
+    dev = torch.device("cuda:0")
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    res = {}
+    for name, fill in (("zeros", 0.0), ("ones", 1.0)):
+        a = torch.full((K, M), fill, dtype=torch.bfloat16, device=dev)
+        b = torch.full((K, N), fill, dtype=torch.bfloat16, device=dev)
+        times = time_launches(lambda: kl.matmul_lhsT_rhs(a, b, cfg=cfg, out=out), 3, steps)
+        t = sorted(times)[len(times) // 2]
+        res[f"{name}_inputs_tflops"] = round(2.0 * M * N * K / t / 1e12, 1)
+        del a, b
+    torch.cuda.synchronize()
+    return res
 
 
 def cpu_baseline(budget_s: float) -> dict:
@@ -269,6 +313,8 @@ def main() -> int:
         },
     }
     if not args.only_kernel and fam == "matmul_lhsT_rhs":
+        line["data_sensitivity"] = data_sensitivity(cfg)
+        log(f"data sensitivity: {line['data_sensitivity']}")
         line["fused"] = fused_pair(args.sweep_reps, args.no_tune)
         log(f"fused pair: {line['fused']}")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
