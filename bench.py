@@ -21,6 +21,8 @@ one launch of that kernel on inputs resident in HBM.
   (normalised x, W).
 * ``data_sensitivity``: the C2 kernel on all-zero and all-one inputs
   (diagnostic: the chip's clock under MFMA load depends on operand data).
+* ``other_configs``: C4's three shapes (TFLOP/s) and C5's three, plus the
+  fused kernel at C5's shapes (HBM GB/s), each with its tuned config.
 * ``cpu_baseline``: the CPU oracle's tile-faithful emulation of the
   reference kernel's loop nest (fp32, numpy/BLAS) on a bounded column slice
   of the same workload, rank 0 only.
@@ -33,7 +35,10 @@ CPU baseline: the command profiled under rocprofv3 PMC runs),
 scale reference), ``--cpu-seconds`` (CPU baseline budget), ``--config NAME``
 (time this tile config instead of sweeping), ``--workload c3`` (time the
 fused rmsnorm_matmul at 4096^3 instead of the C2 matmul: the command the C3
-kernel profiles are taken with; the default line is always C2).
+kernel profiles are taken with; the default line is always C2),
+``--workload c5 --m M`` / ``--workload decode --m M`` (the skinny matmul or
+the fused kernel at (M, 28672, 8192), HBM-bound: the commands their profiles
+are taken with).
 """
 
 from __future__ import annotations
@@ -69,8 +74,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--sweep-reps", type=int, default=20)
     ap.add_argument("--config", default="", help="tile config name (e.g. bm256_bn256_bk32_w4_s3_v1) instead of the sweep")
-    ap.add_argument("--workload", choices=["c2", "c3"], default="c2",
-                    help="c2: lhsT.rhs matmul 8192^3 (the metric); c3: rmsnorm_matmul 4096^3 (profiling)")
+    ap.add_argument("--workload", choices=["c2", "c3", "c5", "decode"], default="c2",
+                    help="c2: lhsT.rhs matmul 8192^3 (the metric); c3: rmsnorm_matmul 4096^3; c5: skinny "
+                         "lhsT.rhs (--m) x 28672 x 8192; decode: rmsnorm_matmul at the c5 shape (profiling)")
+    ap.add_argument("--m", type=int, default=16, choices=[16, 64, 128], help="M of the c5 / decode workloads")
     return ap.parse_args()
 
 
@@ -178,6 +185,89 @@ def data_sensitivity(cfg, steps: int = 20) -> dict:
     return res
 
 
+SKINNY_N, SKINNY_K = 28672, 8192
+HBM_PEAK_GBS = 8000.0
+
+
+def skinny_bytes(fam: str, m: int) -> int:
+    """Compulsory HBM bytes of one launch at (m, 28672, 8192): both operands read once, out written once."""
+    b = (m * SKINNY_K + SKINNY_K * SKINNY_N + m * SKINNY_N) * 2
+    return b + (2 * SKINNY_K if fam == "rmsnorm_matmul" else 0)
+
+
+def skinny_inputs(fam: str, m: int, dev):
+    """C5 inputs (N(0, 0.02)) for the matmul; the C3 distributions for the fused kernel."""
+    from autotune.runner.benchmark import generate_tensors, upload
+    from autotune.tune import default_dists, input_specs
+
+    specs = input_specs(fam, m, SKINNY_N, SKINNY_K)
+    dists = ({"lhs_T": ("normal", 0.02), "rhs": ("normal", 0.02)} if fam == "matmul_lhsT_rhs"
+             else default_dists(fam, SKINNY_K))
+    return upload(generate_tensors(specs, 0, dists), specs, dev)
+
+
+def warm(launch, seconds: float = 0.5) -> None:
+    """Launch back to back for ``seconds``: the engine clock rises over the
+    first few hundred milliseconds of sustained load, and a short burst of
+    launches after an idle gap is timed at the lower clock (10-15 % slower
+    for the C4 shapes)."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            launch()
+        torch.cuda.synchronize()
+
+
+def other_configs(reps: int = 30) -> dict:
+    """C4 (TFLOP/s) and C5 plus the fused kernel at C5's shapes (HBM GB/s), each with its tuned config.
+
+    Each shape is timed after half a second of back-to-back launches of the
+    same kernel.  C5 and the fused decode shapes are timed with a 512 MiB
+    buffer overwritten before every launch, so W streams from HBM, not from
+    the 256 MB MALL."""
+    import torch
+
+    import kernel_library as kl
+    from autotune.runner.benchmark import generate_tensors, time_launches, upload
+    from autotune.tune import default_dists, input_specs
+
+    dev = torch.device("cuda:0")
+    res = {}
+    for m, k, n in ((2048, 8192, 1024), (4096, 1024, 14336), (1024, 14336, 4096)):
+        specs = input_specs("matmul_lhsT_rhs", m, n, k)
+        d = upload(generate_tensors(specs, 0, default_dists("matmul_lhsT_rhs", k)), specs, dev)
+        cfg = kl.default_config("matmul_lhsT_rhs", m, n, k)
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        launch = lambda: kl.matmul_lhsT_rhs(d["lhs_T"], d["rhs"], cfg=cfg, out=out)  # noqa: E731
+        warm(launch)
+        t = sorted(time_launches(launch, 5, reps))
+        tf = 2.0 * m * n * k / t[len(t) // 2] / 1e12
+        res[f"C4 (M,K,N)=({m},{k},{n})"] = {"config": cfg.name, "tflops": round(tf, 1),
+                                            "pct_mfma_peak": round(100 * tf / PEAK_BF16_TFLOPS, 1)}
+        del d, out
+    scratch = torch.empty((512 << 20) // 4, dtype=torch.float32, device=dev)
+    for fam, label in (("matmul_lhsT_rhs", "C5"), ("rmsnorm_matmul", "fused decode")):
+        for m in (16, 64, 128):
+            d = skinny_inputs(fam, m, dev)
+            cfg = kl.default_config(fam, m, SKINNY_N, SKINNY_K)
+            out = torch.empty((m, SKINNY_N), dtype=torch.bfloat16, device=dev)
+            if fam == "matmul_lhsT_rhs":
+                launch = lambda: kl.matmul_lhsT_rhs(d["lhs_T"], d["rhs"], cfg=cfg, out=out)  # noqa: E731
+            else:
+                launch = lambda: kl.rmsnorm_matmul(d["lhs"], d["rhs"], d["gamma"], cfg=cfg, out=out)  # noqa: E731
+            warm(launch)
+            t = sorted(time_launches(launch, 5, reps, flush=scratch.zero_))
+            gbs = skinny_bytes(fam, m) / t[len(t) // 2] / 1e9
+            res[f"{label} M={m}"] = {"config": cfg.name, "us": round(t[len(t) // 2] * 1e6, 1),
+                                     "hbm_gbs": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 1)}
+            del d, out
+    del scratch
+    torch.cuda.synchronize()
+    return res
+
+
 def cpu_baseline(budget_s: float) -> dict:
     """The oracle's tile-faithful emulation of the reference loop nest, timed on a bounded column slice."""
     import numpy as np
@@ -210,13 +300,15 @@ def cpu_baseline(budget_s: float) -> dict:
     }
 
 
-def recorded_traffic(fam: str, s: int, cfg_name: str):
+def recorded_traffic(fam: str, shape, cfg_name: str):
+    """HBM bytes per launch recorded for (family, shape, config), or None; ``shape`` is s (s^3) or "MxNxK"."""
     try:
         with open(TRAFFIC_FILE) as f:
             rec = json.load(f)
     except (OSError, ValueError):
         return None
-    entry = rec.get(f"{fam}:{s}x{s}x{s}:{cfg_name}")
+    key = shape if isinstance(shape, str) else f"{shape}x{shape}x{shape}"
+    entry = rec.get(f"{fam}:{key}:{cfg_name}")
     return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
@@ -245,6 +337,8 @@ def main() -> int:
         log(f"calibration copy of {args.calibrate_copy_mib} MiB done")
         del src, dst
 
+    if args.workload in ("c5", "decode"):
+        return skinny_main(args, dev)
     fam, s = ("matmul_lhsT_rhs", M) if args.workload == "c2" else ("rmsnorm_matmul", 4096)
     if args.config:
         cfg = kl.TileConfig.from_name(args.config)
@@ -317,8 +411,63 @@ def main() -> int:
         log(f"data sensitivity: {line['data_sensitivity']}")
         line["fused"] = fused_pair(args.sweep_reps, args.no_tune)
         log(f"fused pair: {line['fused']}")
+        line["other_configs"] = other_configs()
+        log(f"other configs: {line['other_configs']}")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line, ensure_ascii=False), flush=True)
+    return 0
+
+
+def skinny_main(args, dev) -> int:
+    """--workload c5 / decode: one HBM-bound kernel at (--m, 28672, 8192), back-to-back launches.
+
+    The command the skinny kernel profiles are taken with; the line's
+    roofline is HBM bytes (compulsory, algorithmic) over the launch time."""
+    import torch
+
+    import kernel_library as kl
+
+    fam = "matmul_lhsT_rhs" if args.workload == "c5" else "rmsnorm_matmul"
+    m = args.m
+    cfg = kl.TileConfig.from_name(args.config) if args.config else kl.default_config(fam, m, SKINNY_N, SKINNY_K)
+    d = skinny_inputs(fam, m, dev)
+    out = torch.empty((m, SKINNY_N), dtype=torch.bfloat16, device=dev)
+    if fam == "matmul_lhsT_rhs":
+        def step():
+            kl.matmul_lhsT_rhs(d["lhs_T"], d["rhs"], cfg=cfg, out=out)
+    else:
+        def step():
+            kl.rmsnorm_matmul(d["lhs"], d["rhs"], d["gamma"], cfg=cfg, out=out)
+    for _ in range(args.warmup):
+        step()
+    stream = torch.cuda.current_stream(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kern_s = ev0.elapsed_time(ev1) * 1e-3 / args.steps
+    nbytes = skinny_bytes(fam, m)
+    log(f"timed {args.steps} steps of {fam} {m}x{SKINNY_N}x{SKINNY_K} {cfg.name}: kernel avg {kern_s * 1e6:.1f} us")
+    print(json.dumps({
+        "metric": f"HBM GB/s, {fam} {m}x{SKINNY_N}x{SKINNY_K} (profiling workload, not the headline metric)",
+        "value": round(nbytes * args.steps / wall / 1e9, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 5),
+        "higher_is_better": True,
+        "dtype": "bf16",
+        "config": {"workload": f"{fam} M={m}, N={SKINNY_N}, K={SKINNY_K}", "tile_config": cfg.name},
+        "roofline": {"bound": "hbm", "achieved": round(nbytes / kern_s / 1e9, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(nbytes / kern_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "traffic": recorded_traffic(fam, f"{m}x{SKINNY_N}x{SKINNY_K}", cfg.name)},
+    }, ensure_ascii=False), flush=True)
     return 0
 
 

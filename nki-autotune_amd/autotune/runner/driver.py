@@ -18,6 +18,7 @@ import json
 import logging
 import os
 import shutil
+import time
 from concurrent.futures import ThreadPoolExecutor, as_completed
 from pathlib import Path
 from typing import Any
@@ -37,6 +38,23 @@ def _inputs_key(job: KernelJob, seed: int) -> str:
                        list(job.input_specs), repr(sorted((job.input_dists or {}).items())), seed])
 
 
+def warm_clock(device, seconds: float) -> None:
+    """Keep the GPU busy for ``seconds`` with bf16 GEMMs before timing.
+
+    Under sustained load MI355X's engine clock rises over a few hundred
+    milliseconds; a kernel timed right after an idle gap (start-up, a hipcc
+    build) runs at the lower clock, 10-15 % slower on compute-bound shapes,
+    which would bias the sweep towards whichever configs are timed later."""
+    import torch
+
+    a = torch.empty((4096, 4096), dtype=torch.bfloat16, device=device).uniform_(-1, 1)
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            torch.matmul(a, a)
+        torch.cuda.synchronize(device)
+
+
 def run_pipeline(
     kernels: dict[str, KernelJob],
     seed: int,
@@ -47,8 +65,13 @@ def run_pipeline(
     flush_bytes: int = 0,
     allow_jit: bool = True,
     work_dir: str | None = None,
+    clock_warmup_s: float = 0.5,
 ) -> tuple[list[ProfileResult], dict[str, str]]:
-    """Build + time every job on GPU 0; return (results, compiler_logs)."""
+    """Build + time every job on GPU 0; return (results, compiler_logs).
+
+    Before the first timing, and before any timing that follows more than
+    0.2 s without GPU work (a just-in-time build), the GPU is kept busy for
+    ``clock_warmup_s`` seconds (:func:`warm_clock`)."""
     import torch
 
     if not kernels:
@@ -82,6 +105,7 @@ def run_pipeline(
     compile_results: list[CompileResult] = []
     compile_errors: list[ProfileResult] = []
     hw_results: list[ProfileResult] = []
+    last_gpu = None
     with ThreadPoolExecutor(max_workers=workers) as pool:
         futures = [
             pool.submit(compile_one, kname, job.source, job.func_name, job.input_specs, str(work), job.hipcc_args,
@@ -103,8 +127,11 @@ def run_pipeline(
                 hw_results.append(ProfileResult(cr.kernel_name, f"output_shape {tuple(job.output_shape)} does not "
                                                 f"match the inputs' [M, N] = [{M}, {N}]"))
                 continue
+            if clock_warmup_s > 0 and (last_gpu is None or time.perf_counter() - last_gpu > 0.2):
+                warm_clock(device, clock_warmup_s)
             hw_results.append(benchmark_one(cr.kernel_name, cr.library_path, canonical_name(job.func_name), cfg,
                                             dev_inputs[key], out, M, N, K, warmup, reps, flush_bytes,
                                             collect_detailed_profile))
+            last_gpu = time.perf_counter()
     logs = {cr.kernel_name: cr.compile_log for cr in compile_results if collect_compiler_logs and cr.compile_log}
     return compile_errors + hw_results, logs

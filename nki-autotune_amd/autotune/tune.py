@@ -159,6 +159,7 @@ def refine(func_name: str, M: int, N: int, K: int, configs, seed: int = 0, dists
     import torch
 
     from autotune.runner.benchmark import Launcher, generate_tensors, time_launches, upload
+    from autotune.runner.driver import warm_clock
     from kernel_library import _lib
 
     fam = canonical_name(func_name)
@@ -171,6 +172,7 @@ def refine(func_name: str, M: int, N: int, K: int, configs, seed: int = 0, dists
                                   inputs, out, M, N, K) for c in configs}
     flush = torch.empty(flush_bytes // 4, dtype=torch.float32, device=dev).zero_ if flush_bytes else None
     per_round: dict[str, list[float]] = {n: [] for n in launchers}
+    warm_clock(dev, 0.5)
     for r in range(rounds):
         for name, launch in launchers.items():
             per_round[name].append(statistics.median(time_launches(launch, warmup if r == 0 else 2, reps, flush)))
