@@ -55,7 +55,16 @@ enum {
  *   waves                     : wavefronts (64 lanes) per workgroup
  *   lds_stages                : LDS ring depth for K panels (1..4); for matmul
  *                               variant 2 the depth of its register ring
- *   split_k                   : must be 1 (reserved)
+ *   split_k                   : K split over this many workgroups per output
+ *                               tile (1..16; > 1 only for the pipelined lhsT
+ *                               matmul, variants 1 and 3, and every part must
+ *                               get at least one K tile).  The parts write fp32
+ *                               partial products to a workspace that the
+ *                               library allocates once per (device, stream)
+ *                               and keeps (split_k * M * N * 4 bytes, at most
+ *                               2 GiB); a second kernel sums them in part order
+ *                               into out.  The first call on a stream must not
+ *                               be under graph capture (it allocates).
  *   group_m                   : L2 raster group height in tiles (0 = default 8)
  *   variant                   : kernel-specific pipeline (every variant computes
  *                               the same function):
@@ -93,7 +102,8 @@ int mi_get_config(int kernel_id, int idx, mi_tile_cfg* cfg);
 int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
 
 /* out[M,N] = lhsT[K,M]^T . rhs[K,N]; bf16 storage, fp32 accumulation over
- * the whole K, one round-to-nearest-even store.
+ * the whole K (over each K part, then across parts in part order, when
+ * cfg->split_k > 1), one round-to-nearest-even store.
  * Replaces matmul_lhsT_rhs_nkigym(lhs_T, rhs)
  * (reference kernel_library/matmul/lhsT_rhs/kernel_hand_90.92mfu.py:101-131).
  * cfg == NULL selects mi_default_config. */

@@ -11,7 +11,9 @@ a state is a :class:`~kernel_library.config.TileConfig` and an action (an
 * ``waves`` 4 <-> 8,
 * ``lds_stages`` +1 / -1,
 * ``group_m`` (the L2 raster height) doubled or halved,
-* ``variant`` set to another pipeline of the same kernel family.
+* ``variant`` set to another pipeline of the same kernel family,
+* ``split_k`` (K split over several workgroups per output tile) doubled or
+  halved, for the lhsT matmul.
 
 An atom is legal at a state when its result passes the library's static
 legality check at the problem shape (``mi_cfg_check``: LDS budget, wave
@@ -56,7 +58,8 @@ FAMILY_VARIANTS = {
     "matmul_lhsT_rhs_f32": (0,),
 }
 
-_POW2_KNOBS = {"block_m": (32, 512), "block_n": (32, 512), "block_k": (16, 128), "group_m": (1, 64)}
+_POW2_KNOBS = {"block_m": (32, 512), "block_n": (32, 512), "block_k": (16, 128), "group_m": (1, 64),
+               "split_k": (1, 16)}
 
 
 def atoms_for(func_name: str) -> list[Atom]:
@@ -65,6 +68,8 @@ def atoms_for(func_name: str) -> list[Atom]:
     out += [Atom("waves", "swap"), Atom("lds_stages", "+1"), Atom("lds_stages", "-1"),
             Atom("group_m", "x2"), Atom("group_m", "/2")]
     out += [Atom("variant", f"={v}") for v in FAMILY_VARIANTS.get(fam, (0,))]
+    if fam == "matmul_lhsT_rhs":
+        out += [Atom("split_k", "x2"), Atom("split_k", "/2")]
     return out
 
 

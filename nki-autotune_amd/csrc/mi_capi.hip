@@ -8,7 +8,9 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <map>
 #include <mutex>
+#include <utility>
 #include <vector>
 
 #include "mi_registry.hpp"
@@ -72,6 +74,8 @@ bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1))
 
 constexpr unsigned long long kMaxOffset = 0xFFFFFFFFull;  // 32-bit buffer offsets
 constexpr int kLdsLimit = 160 * 1024;
+constexpr int kMaxSplit = 16;                                  // split-K parts
+constexpr unsigned long long kMaxSplitWorkspace = 1ull << 31;  // bytes of fp32 partial products
 
 int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::MiEntry** out) {
   if (kernel_id < 0 || kernel_id >= MI_NUM_KERNELS) return fail(MI_E_KERNEL, "unknown kernel id %d", kernel_id);
@@ -80,7 +84,23 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
   const mi_tile_cfg& c = *cfg;
   if (c.block_m <= 0 || c.block_n <= 0 || c.block_k <= 0 || c.waves <= 0 || c.lds_stages <= 0)
     return fail(MI_E_ARGS, "non-positive tile parameter");
-  if (c.split_k != 1) return fail(MI_E_SPLIT, "split_k=%d unsupported (must be 1)", c.split_k);
+  if (c.split_k < 1 || c.split_k > kMaxSplit)
+    return fail(MI_E_SPLIT, "split_k=%d outside [1, %d]", c.split_k, kMaxSplit);
+  if (c.split_k > 1) {
+    // Split-K: the pipelined lhsT kernels only, and every part must get at
+    // least one K tile.
+    if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_BF16 || (c.variant != 1 && c.variant != 3))
+      return fail(MI_E_SPLIT, "split_k=%d needs the pipelined lhsT.rhs kernel (matmul variants 1 and 3)",
+                  c.split_k);
+    const long long kt = ((long long)K + c.block_k - 1) / c.block_k;
+    const long long kts = (kt + c.split_k - 1) / c.split_k;
+    if ((long long)(c.split_k - 1) * kts >= kt)
+      return fail(MI_E_SPLIT, "split_k=%d leaves a K part empty at K=%d, block_k=%d", c.split_k, K, c.block_k);
+    const unsigned long long ws =
+        (unsigned long long)c.split_k * (unsigned long long)M * (unsigned long long)N * 4ull;
+    if (ws > kMaxSplitWorkspace)
+      return fail(MI_E_RANGE, "split-K workspace of %llu bytes exceeds %llu", ws, kMaxSplitWorkspace);
+  }
   if (c.group_m < 0) return fail(MI_E_ARGS, "group_m=%d negative", c.group_m);
   if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_F32) {
     // LDS panels are copied in 1 KiB wave loads and XOR-swizzled in 16-byte
@@ -206,6 +226,33 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
   return MI_OK;
 }
 
+// Split-K workspace, one per (device, stream): launches on one stream run in
+// order, so they can share it; launches on different streams get their own.
+// It grows to the largest request and lives until the process ends.
+struct SplitWorkspace {
+  float* ws = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, SplitWorkspace> g_ws;
+
+int split_workspace(size_t bytes, hipStream_t stream, float** ws) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  SplitWorkspace& w = g_ws[{dev, stream}];
+  if (w.bytes < bytes) {
+    if (w.ws && (e = hipFree(w.ws)) != hipSuccess) return hip_fail(e, "split-K workspace free");
+    w.ws = nullptr;
+    w.bytes = 0;
+    if ((e = hipMalloc((void**)&w.ws, bytes)) != hipSuccess) return hip_fail(e, "split-K workspace alloc");
+    w.bytes = bytes;
+  }
+  *ws = w.ws;
+  return MI_OK;
+}
+
 int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, void* stream) {
   mi_tile_cfg cfg;
   if (cfg_in) cfg = *cfg_in;
@@ -215,6 +262,12 @@ int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, voi
   if (rc != MI_OK) return rc;
   mi::MiArgs a = args_in;
   a.group_m = cfg.group_m > 0 ? cfg.group_m : 8;
+  if (cfg.split_k > 1) {
+    const size_t ws_bytes = (size_t)cfg.split_k * (size_t)a.M * (size_t)a.N * 4u;
+    const int wrc = split_workspace(ws_bytes, (hipStream_t)stream, &a.ws);
+    if (wrc != MI_OK) return wrc;
+    a.parts = cfg.split_k;
+  }
   const hipError_t err = e->launch(a, (hipStream_t)stream);
   if (err != hipSuccess) return hip_fail(err, "kernel launch");
   return MI_OK;

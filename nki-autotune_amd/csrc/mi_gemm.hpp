@@ -150,6 +150,33 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_
   tn = in_group / gm;
 }
 
+// Split-K: the grid holds `parts` copies of the tile grid, copy p computing
+// K tiles [p*KTS, (p+1)*KTS) of every output tile (KTS = ceil(KT/parts)).
+// Logical workgroup index = p * tiles + tile, so after the XCD renumbering
+// each XCD works on neighbouring tiles of one K range.
+struct SplitK {
+  int parts;          // 1: no split
+  float* ws;          // fp32 partial products, [parts][M][N]
+};
+
+__device__ __forceinline__ void tile_coords_split(int tiles_m, int tiles_n, int group_m, int parts, int& tm, int& tn,
+                                                  int& part) {
+  const int nwg = (int)gridDim.x;
+  int wg = (int)blockIdx.x;
+  const int per = nwg >> 3, rem = nwg & 7, xcd = wg & 7;
+  wg = xcd * per + (xcd < rem ? xcd : rem) + (wg >> 3);
+  const int tiles = tiles_m * tiles_n;
+  part = parts > 1 ? wg / tiles : 0;
+  wg -= part * tiles;
+  const int width = group_m * tiles_n;
+  const int group = wg / width;
+  const int first_m = group * group_m;
+  const int gm = (tiles_m - first_m) < group_m ? (tiles_m - first_m) : group_m;
+  const int in_group = wg - group * width;
+  tm = first_m + in_group % gm;
+  tn = in_group / gm;
+}
+
 // XOR swizzle of 16-byte chunks inside one K row of an MN-contiguous panel
 // (row = one K index, ROWB/16 chunks).  gfx950's LDS has 64 banks of 4 bytes
 // (a 256-byte bank window).  One ds_read_b64_tr_b16 reads, per 32 lanes,
@@ -530,10 +557,58 @@ struct PipeCfg {
 // lhsT[K,M] (M contiguous; MN-swizzled panel, transposing operand reads),
 // AK = true takes lhs[M,K] (K contiguous; K-swizzled panel, one
 // ds_read_b128 per operand fragment, no transpose).
-template <int BM, int BN, int BK, int WAVES, int STAGES, bool AK, bool NTB = false>
+// Split-K epilogue: part p stores its fp32 accumulators to ws[p][M][N]
+// straight from registers (lane l holds row l%32 of each 32x32 fragment,
+// four consecutive columns per dword quad; N % 8 == 0, so a quad is in
+// bounds whenever its first column is).  A second kernel sums the parts.
+template <int TM, int TN>
+__device__ __forceinline__ void store_partial(const f32x16_t (&acc)[TM][TN], float* __restrict__ ws, int lane,
+                                              int M, int N, int row0, int col0) {
+#pragma unroll
+  for (int mt = 0; mt < TM; ++mt) {
+    const int m = row0 + mt * 32 + (lane & 31);
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int n = col0 + nt * 32 + 8 * j + 4 * (lane >> 5);
+        if (m < M && n < N) {
+          const f32x4_t v = {acc[mt][nt][4 * j], acc[mt][nt][4 * j + 1], acc[mt][nt][4 * j + 2],
+                             acc[mt][nt][4 * j + 3]};
+          *(f32x4_t*)(ws + (size_t)m * N + n) = v;
+        }
+      }
+  }
+}
+
+// out[i] = bf16(sum over p = 0 .. parts-1 of ws[p][i]), summed in part order
+// (so the result does not depend on the order the parts ran in); 8
+// elements per thread (n = M*N, a multiple of 8).  A template so that every
+// translation unit may instantiate it.
+template <int UNUSED = 0>
+__global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict__ ws, uint16_t* __restrict__ out,
+                                                         size_t n, int parts) {
+  const size_t stride = (size_t)gridDim.x * 256 * 8;
+  for (size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += stride) {
+    f32x4_t lo = *(const f32x4_t*)(ws + i), hi = *(const f32x4_t*)(ws + i + 4);
+    for (int p = 1; p < parts; ++p) {
+      lo += *(const f32x4_t*)(ws + (size_t)p * n + i);
+      hi += *(const f32x4_t*)(ws + (size_t)p * n + i + 4);
+    }
+    u32x4_t o;
+    o.x = pack_bf16x2(lo[0], lo[1]);
+    o.y = pack_bf16x2(lo[2], lo[3]);
+    o.z = pack_bf16x2(hi[0], hi[1]);
+    o.w = pack_bf16x2(hi[2], hi[3]);
+    *(u32x4_t*)(out + i) = o;
+  }
+}
+
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool AK, bool NTB = false, bool SPLIT = false>
 __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, const uint16_t* __restrict__ rhs,
                                              uint16_t* __restrict__ out, int M, int N, int K, int group_m,
-                                             char* smem) {
+                                             char* smem, const SplitK sk = SplitK{1, nullptr}) {
+  static_assert(!(SPLIT && AK), "split-K is built for the lhsT layout only");
   using C = PipeCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
   static_assert(G::ok, "illegal wave grid");
@@ -551,11 +626,21 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  int tmi, tni;
-  tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
+  int tmi, tni, part = 0;
+  if constexpr (SPLIT) tile_coords_split(tiles_m, tiles_n, group_m, sk.parts, tmi, tni, part);
+  else tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
   const int m0 = tmi * BM, n0 = tni * BN;
   const int wm0 = (wave / G::WN) * G::WTM;
   const int wn0 = (wave % G::WN) * G::WTN;
+  if constexpr (SPLIT) {
+    // Split-K part `part`: K rows [k0, k0 + K) of lhsT and rhs (the host
+    // guarantees every part a non-empty range).
+    const int kts = ((K + BK - 1) / BK + sk.parts - 1) / sk.parts;
+    const int k0 = part * kts * BK;
+    a += (size_t)k0 * (size_t)M;
+    rhs += (size_t)k0 * (size_t)N;
+    K = K - k0 < kts * BK ? K - k0 : kts * BK;
+  }
 
   const uint32_t a_bytes = (uint32_t)K * (uint32_t)M * 2u;
   const uint32_t b_bytes = (uint32_t)K * (uint32_t)N * 2u;
@@ -692,6 +777,10 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   wait_vmem();
   __syncthreads();  // the epilogue reuses the panel buffers
 
+  if constexpr (SPLIT) {
+    store_partial<TM, TN>(acc, sk.ws + (size_t)part * (size_t)M * (size_t)N, lane, M, N, m0 + wm0, n0 + wn0);
+    return;
+  }
   float one[TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i) one[i] = 1.0f;
@@ -699,14 +788,19 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
 }
 
 // NTB: rhs loaded with the non-temporal cache policy (matmul variant 3, for
-// shapes where rhs is streamed once: skinny M).
-template <int BM, int BN, int BK, int WAVES, int STAGES, bool NTB = false>
+// shapes where rhs is streamed once: skinny M).  SPLIT: K split over
+// `parts` workgroups per output tile, each writing fp32 partial products to
+// ws (splitk_sum_kernel then forms out); a separate instance, so that the
+// unsplit kernel is unchanged.
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool NTB = false, bool SPLIT = false>
 __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const uint16_t* __restrict__ lhsT,
                                                                           const uint16_t* __restrict__ rhs,
                                                                           uint16_t* __restrict__ out, int M, int N,
-                                                                          int K, int group_m) {
+                                                                          int K, int group_m, int parts,
+                                                                          float* __restrict__ ws) {
   __shared__ __attribute__((aligned(1024))) char smem[PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
-  mm_pipe_body<BM, BN, BK, WAVES, STAGES, false, NTB>(lhsT, rhs, out, M, N, K, group_m, smem);
+  mm_pipe_body<BM, BN, BK, WAVES, STAGES, false, NTB, SPLIT>(lhsT, rhs, out, M, N, K, group_m, smem,
+                                                             SplitK{parts, ws});
 }
 
 // out[M,N] = lhs[M,K] . rhs[K,N] with lhs K-contiguous (matmul_lhs_rhs);

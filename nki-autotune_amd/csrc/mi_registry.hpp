@@ -27,6 +27,8 @@ struct MiArgs {
   int M, N, K;
   float eps, inv_k;
   int group_m;
+  int parts = 1;             // split-K parts (pipelined lhsT matmul only)
+  float* ws = nullptr;       // split-K workspace: fp32 partial products [parts][M][N]
 };
 
 typedef hipError_t (*LaunchFn)(const MiArgs&, hipStream_t);
@@ -50,9 +52,22 @@ hipError_t launch_mm_bf16(const MiArgs& a, hipStream_t s) {
 
 template <int BM, int BN, int BK, int W, int S, bool NTB = false>
 hipError_t launch_mm_pipe(const MiArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB>), dim3(grid_tiles(a.M, a.N, BM, BN)),
-                     dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K,
-                     a.group_m);
+  if (a.parts > 1) {
+    // Split-K: the parts' fp32 products into ws, then their sum into out.
+    hipLaunchKernelGGL((mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, true>),
+                       dim3(grid_tiles(a.M, a.N, BM, BN) * a.parts), dim3(W * 64), 0, s, (const uint16_t*)a.a,
+                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, a.ws);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t n = (size_t)a.M * (size_t)a.N;
+    const size_t blocks = (n / 8 + 255) / 256;
+    hipLaunchKernelGGL(splitk_sum_kernel<0>, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s,
+                       (const float*)a.ws, (uint16_t*)a.out, n, a.parts);
+  } else {
+    hipLaunchKernelGGL((mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, false>),
+                       dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
+                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, 1, nullptr);
+  }
   return hipGetLastError();
 }
 
@@ -150,12 +165,18 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
 #define MI_MM_INST(BM, BN, BK, W, S)                                                                      \
   template __global__ void mm_lhsT_rhs_bf16_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*, \
                                                                       uint16_t*, int, int, int, int);
+// Pipelined lhsT matmul (variant 1; MI_MMPN: variant 3, rhs non-temporal),
+// unsplit and split-K instances.
 #define MI_MMP_INST(BM, BN, BK, W, S)                                                                          \
-  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*,  \
-                                                                           uint16_t*, int, int, int, int);
-#define MI_MMPN_INST(BM, BN, BK, W, S)                                                                            \
-  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true>(const uint16_t*, const uint16_t*, \
-                                                                                 uint16_t*, int, int, int, int);
+  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, false>(                      \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);                \
+  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, true>(                       \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
+#define MI_MMPN_INST(BM, BN, BK, W, S)                                                                         \
+  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, false>(                       \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);                \
+  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, true>(                        \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
 #define MI_MMK_INST(BM, BN, BK, W, S)                                                                         \
   template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*,    \
                                                                           uint16_t*, int, int, int, int);

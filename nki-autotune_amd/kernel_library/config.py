@@ -13,7 +13,7 @@ from __future__ import annotations
 import ctypes
 import itertools
 import json
-from dataclasses import asdict, dataclass
+from dataclasses import asdict, dataclass, replace
 from pathlib import Path
 
 from kernel_library import _lib
@@ -72,13 +72,15 @@ class TileConfig:
             s += f"_g{self.group_m}"
         if self.variant:
             s += f"_v{self.variant}"
+        if self.split_k != 1:
+            s += f"_k{self.split_k}"
         return s
 
     @classmethod
     def from_name(cls, name: str) -> "TileConfig":
-        """Inverse of ``name`` (``bm256_bn256_bk32_w8_s3[_g4][_v1]``)."""
+        """Inverse of ``name`` (``bm256_bn256_bk32_w8_s3[_g4][_v1][_k2]``)."""
         fields = {"bm": "block_m", "bn": "block_n", "bk": "block_k", "w": "waves", "s": "lds_stages",
-                  "g": "group_m", "v": "variant"}
+                  "g": "group_m", "v": "variant", "k": "split_k"}
         kw = {}
         for part in name.split("_"):
             key = part.rstrip("0123456789")
@@ -140,8 +142,28 @@ def legal_configs(func_name: str, M: int, N: int, K: int, grid: list[TileConfig]
     nkigym/src/nkigym/environment/mdp.py:44-54): the action space of the
     search is the set of legal tile configs.
     """
-    grid = compiled_configs(func_name) if grid is None else grid
+    if grid is None:
+        grid = compiled_configs(func_name)
+        grid = grid + split_k_variants(func_name, grid, M, N)
     return [c for c in grid if check(func_name, c, M, N, K)[0] == 0]
+
+
+SPLIT_K_PARTS = (2, 4, 8, 16)
+
+
+def split_k_variants(func_name: str, grid: list[TileConfig], M: int, N: int) -> list[TileConfig]:
+    """Split-K copies of the pipelined lhsT configs whose output tiles fill
+    fewer than two waves of workgroups on the GPU (< 512 tiles): K is then
+    the only axis left to spread the work over more compute units.  Part
+    counts keep the grid within 1024 workgroups (four per compute unit)."""
+    if func_name not in ("matmul_lhsT_rhs", "matmul_lhsT_rhs_nkigym"):
+        return []
+    out = []
+    for c in grid:
+        tiles = -(-M // c.block_m) * -(-N // c.block_n)
+        if c.variant in (1, 3) and c.split_k == 1 and tiles < 512:
+            out += [replace(c, split_k=p) for p in SPLIT_K_PARTS if tiles * p <= 1024]
+    return out
 
 
 def default_config(func_name: str, M: int, N: int, K: int) -> TileConfig:

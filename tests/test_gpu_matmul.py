@@ -68,18 +68,24 @@ def test_bf16_every_config_small_fixture(gpu):
     d = mm_inputs(256, 256, 512, seed=0)
     a, b = _dev(d["lhs_T"], torch.bfloat16, gpu), _dev(d["rhs"], torch.bfloat16, gpu)
     expected = omm.closed_form(d["lhs_T"], d["rhs"])
-    first = None
-    for cfg in kl.legal_configs("matmul_lhsT_rhs", 256, 512, 256):
+    first = {}
+    K = 256
+    for cfg in kl.legal_configs("matmul_lhsT_rhs", 256, 512, K):
         out = kl.matmul_lhsT_rhs(a, b, cfg=cfg)
         torch.cuda.synchronize()
         rep = mm_check(_host(out), expected)
         assert rep["ok"], (cfg, rep)
         bits = out.view(torch.int16).cpu().numpy()
-        if first is None:
-            first = (cfg, bits)
+        # Same K order in every config (ascending, 16 per MFMA): bitwise equal.
+        # Split-K sums fp32 partials over K ranges, so configs are bitwise
+        # equal when they split K at the same boundaries.
+        kts = -(-(-(-K // cfg.block_k)) // cfg.split_k) * cfg.block_k
+        key = tuple(range(0, K, kts)) if cfg.split_k > 1 else ()
+        if key not in first:
+            first[key] = (cfg, bits)
         else:
-            # Same K order in every config (ascending, 16 per MFMA): bitwise equal.
-            assert np.array_equal(bits, first[1]), (cfg, first[0])
+            assert np.array_equal(bits, first[key][1]), (cfg, first[key][0])
+    assert () in first and len(first) > 1
 
 
 @pytest.mark.parametrize("M,N,K", [(264, 520, 100), (8, 8, 7), (40, 136, 33), (16, 1024, 512), (128, 96, 1000)])

@@ -1,0 +1,174 @@
+"""GPU parity of split-K (tile config ``split_k`` > 1) for the pipelined lhsT
+matmul, against the CPU oracle.
+
+With split_k = P each output tile is computed by P workgroups over disjoint
+K ranges; they write fp32 partial products to a per-stream workspace and a
+second kernel sums them in part order into the bf16 output.  The tests
+cover ragged M, N and K, part counts up to 8, both pipelined variants,
+repeated and interleaved launches of different shapes (the workspace is
+reused and grown), a second stream (its own workspace), run to run
+determinism and HIP-graph replay.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import mm_check, mm_inputs
+from oracle import matmul as omm
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a: np.ndarray, device):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).to(torch.bfloat16).to(device)
+
+
+def _host(t) -> np.ndarray:
+    import torch
+
+    return t.to(torch.float32).cpu().numpy()
+
+
+def _nan_out(M, N, device):
+    import torch
+
+    return torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=device)
+
+
+CONFIGS = [
+    # (block_m, block_n, block_k, waves, stages, variant)
+    (64, 128, 64, 4, 4, 1),
+    (128, 128, 64, 4, 3, 1),
+    (256, 256, 32, 4, 3, 1),
+    (32, 128, 128, 4, 3, 3),
+    (128, 128, 64, 4, 3, 3),
+]
+
+
+@pytest.mark.parametrize("parts", [2, 3, 4, 8])
+@pytest.mark.parametrize("cfg", CONFIGS, ids=lambda c: "bm{}_bn{}_bk{}_w{}_s{}_v{}".format(*c))
+def test_ragged_shapes_match_oracle(gpu, cfg, parts):
+    """M, N not multiples of the block, K not a multiple of block_k (the last part is short)."""
+    import kernel_library as kl
+
+    bm, bn, bk, w, s, v = cfg
+    M, N, K = 200, 264, 1000
+    tc = kl.TileConfig(bm, bn, bk, w, s, split_k=parts, variant=v)
+    assert kl.check("matmul_lhsT_rhs", tc, M, N, K)[0] == 0, kl.check("matmul_lhsT_rhs", tc, M, N, K)
+    print("split-K", tc.name, M, N, K, flush=True)
+    d = mm_inputs(K, M, N, seed=parts)
+    a, b = _dev(d["lhs_T"], gpu), _dev(d["rhs"], gpu)
+    out = _nan_out(M, N, gpu)
+    kl.matmul_lhsT_rhs(a, b, cfg=tc, out=out)
+    rep = mm_check(_host(out), omm.closed_form(d["lhs_T"], d["rhs"]))
+    assert rep["ok"], (tc.name, rep)
+
+
+def test_interleaved_launches_and_streams(gpu):
+    """Interleaved launches with different part counts and shapes on one
+    stream, then on a second stream: every output is whole and correct (the
+    output starts as NaN, so a part that is not summed shows)."""
+    import torch
+
+    import kernel_library as kl
+
+    shapes = [(256, 512, 2048, 4), (136, 128, 512, 2), (256, 512, 2048, 2), (256, 512, 2048, 4),
+              (64, 1024, 4096, 8)]
+    data = {}
+    for M, N, K, _ in shapes:
+        if (M, N, K) not in data:
+            d = mm_inputs(K, M, N, seed=M + N + K)
+            data[(M, N, K)] = (d, _dev(d["lhs_T"], gpu), _dev(d["rhs"], gpu))
+    side = torch.cuda.Stream(device=gpu)
+    for stream in (torch.cuda.current_stream(gpu), side):
+        with torch.cuda.stream(stream):
+            for rep_i in range(2):
+                for M, N, K, parts in shapes:
+                    d, a, b = data[(M, N, K)]
+                    tc = kl.TileConfig(64, 128, 64, 4, 4, split_k=parts, variant=1)
+                    out = _nan_out(M, N, gpu)
+                    kl.matmul_lhsT_rhs(a, b, cfg=tc, out=out)
+                    stream.synchronize()
+                    rep = mm_check(_host(out), omm.closed_form(d["lhs_T"], d["rhs"]))
+                    assert rep["ok"], (M, N, K, parts, rep_i, rep)
+    torch.cuda.synchronize()
+
+
+def test_deterministic_and_close_to_unsplit(gpu):
+    """The same split call twice gives the same bits (parts are summed in a
+    fixed order); against the unsplit kernel the difference is fp32
+    summation order only."""
+    import torch
+
+    import kernel_library as kl
+
+    M, N, K = 512, 512, 8192
+    d = mm_inputs(K, M, N, seed=11)
+    a, b = _dev(d["lhs_T"], gpu), _dev(d["rhs"], gpu)
+    split = kl.TileConfig(128, 128, 64, 4, 3, split_k=4, variant=1)
+    whole = kl.TileConfig(128, 128, 64, 4, 3, variant=1)
+    outs = [kl.matmul_lhsT_rhs(a, b, cfg=split) for _ in range(3)]
+    ref = kl.matmul_lhsT_rhs(a, b, cfg=whole)
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
+    diff = (outs[0].float() - ref.float()).abs().max().item()
+    scale = ref.float().abs().max().item()
+    assert diff <= 2 ** -7 * scale, (diff, scale)
+    rep = mm_check(_host(outs[0]), omm.closed_form(d["lhs_T"], d["rhs"]))
+    assert rep["ok"], rep
+
+
+@pytest.mark.parametrize("M,N,K,cfg", [
+    (2048, 1024, 8192, (128, 128, 64, 4, 3, 1, 2)),   # benchmark config C4a, 128 tiles x 2 parts
+    (128, 28672, 8192, (128, 128, 64, 4, 2, 3, 2)),   # C5 at M = 128, 224 tiles x 2 parts
+    (256, 512, 32768, (128, 128, 64, 4, 3, 1, 16)),   # 8 output tiles, long K: 16 parts
+])
+def test_benchmark_shapes(gpu, M, N, K, cfg):
+    """Split-K configs at shapes with few output tiles, whole output vs the oracle."""
+    import kernel_library as kl
+
+    bm, bn, bk, w, s, v, p = cfg
+    tc = kl.TileConfig(bm, bn, bk, w, s, split_k=p, variant=v)
+    print("split-K", tc.name, M, N, K, flush=True)
+    d = mm_inputs(K, M, N, seed=0)
+    out = _nan_out(M, N, gpu)
+    kl.matmul_lhsT_rhs(_dev(d["lhs_T"], gpu), _dev(d["rhs"], gpu), cfg=tc, out=out)
+    rep = mm_check(_host(out), omm.closed_form(d["lhs_T"], d["rhs"]))
+    assert rep["ok"], (tc.name, rep)
+
+
+def test_graph_replay_matches_eager(gpu):
+    """A split-K call captured in a HIP graph (workspace allocated by an
+    eager call first) replays to the eager result, with eager work between
+    replays."""
+    import torch
+
+    import kernel_library as kl
+
+    M, N, K = 256, 384, 4096
+    d = mm_inputs(K, M, N, seed=5)
+    a, b = _dev(d["lhs_T"], gpu), _dev(d["rhs"], gpu)
+    tc = kl.TileConfig(64, 128, 64, 4, 4, split_k=4, variant=1)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+    side = torch.cuda.Stream(device=gpu)
+    side.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(side):
+        kl.matmul_lhsT_rhs(a, b, cfg=tc, out=out)
+    torch.cuda.current_stream(gpu).wait_stream(side)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        kl.matmul_lhsT_rhs(a, b, cfg=tc, out=out)
+    for rep_i in range(4):
+        out.fill_(float("nan"))
+        kl.matmul_lhsT_rhs(a, b, cfg=tc)          # eager split-K work on the current stream between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), rep_i

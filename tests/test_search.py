@@ -49,6 +49,8 @@ def test_mdp_moves_and_legality():
     with pytest.raises(IllegalMove):
         mdp.step(s, Atom("variant", f"={s.variant}"))                                 # no-op move
     assert Atom("variant", "=10") in atoms_for("rmsnorm_matmul")
+    assert Atom("split_k", "x2") in atoms_for("matmul_lhsT_rhs")
+    assert Atom("split_k", "x2") not in atoms_for("rmsnorm_matmul")
     assert not mdp.is_terminal(s)
 
 
@@ -81,5 +83,7 @@ def test_sample_is_deterministic_legal_and_capped():
 def test_prebuilt_only_stays_in_the_library():
     prebuilt = {c.name for c in kl.compiled_configs("matmul_lhsT_rhs")}
     for c in frontier_pool(TileMDP("matmul_lhsT_rhs", 4096, 4096, 4096, prebuilt_only=True), 10**6, 0):
-        base = TileConfig(c.block_m, c.block_n, c.block_k, c.waves, c.lds_stages, c.split_k, 8, c.variant)
+        # split_k is a launch parameter of a prebuilt instance, not an instance of its own
+        base = TileConfig(c.block_m, c.block_n, c.block_k, c.waves, c.lds_stages, 1, 8, c.variant)
         assert base.name in prebuilt, c
+        assert c.split_k == 1 or c.variant in (1, 3), c
