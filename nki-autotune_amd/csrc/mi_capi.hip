@@ -208,6 +208,21 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
     else if (M <= 128) c = {128, 128, 64, 4, 3, 1, 8, 3};
     else if (mid) c = {128, 128, 64, 4, 3, 1, 8, 1};
     else c = {256, 256, 32, 4, 3, 1, 8, 1};
+    // Few output tiles: 64 x 64 tiles, and K split (doubling the parts)
+    // while the grid stays within one workgroup per compute unit (the sweep's
+    // winners at 512x512x32768 and 256x1024x16384), every part keeps at
+    // least 4 K tiles and no part is empty.
+    const long long t64 = (long long)((M + 63) / 64) * ((N + 63) / 64);
+    if (M > 128 && t64 < 256) {
+      const long long kt = (K + 63) / 64;
+      int parts = 1;
+      for (int next = 2; next <= 16; next *= 2) {
+        const long long kts = (kt + next - 1) / next;
+        if (t64 * next > 256 || kt < 4LL * next || (long long)(next - 1) * kts >= kt) break;
+        parts = next;
+      }
+      if (parts > 1) c = {64, 64, 64, 4, 4, parts, 8, 1};
+    }
   } else if (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16) {
     if (M <= 128) c = {128, 128, 64, 4, 3, 1, 8, 2};
     else if (mid) c = {128, 128, 64, 4, 3, 1, 8, 0};

@@ -172,3 +172,16 @@ def test_graph_replay_matches_eager(gpu):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), rep_i
+
+
+def test_library_default_splits_few_tile_long_k(gpu):
+    """With no config and no tuned entry, a few-tile long-K shape takes a split-K default; output vs the oracle."""
+    import kernel_library as kl
+
+    M, N, K = 512, 256, 16384
+    cfg = kl.default_config("matmul_lhsT_rhs", M, N, K)
+    assert cfg.split_k > 1, cfg
+    d = mm_inputs(K, M, N, seed=9)
+    out = kl.matmul_lhsT_rhs(_dev(d["lhs_T"], gpu), _dev(d["rhs"], gpu))
+    rep = mm_check(_host(out), omm.closed_form(d["lhs_T"], d["rhs"]))
+    assert rep["ok"], (cfg.name, rep)
