@@ -56,15 +56,17 @@ enum {
  *   lds_stages                : LDS ring depth for K panels (1..4); for matmul
  *                               variant 2 the depth of its register ring
  *   split_k                   : K split over this many workgroups per output
- *                               tile (1..16; > 1 only for the pipelined lhsT
- *                               matmul, variants 1 and 3, and every part must
- *                               get at least one K tile).  The parts write fp32
- *                               partial products to a workspace that the
- *                               library allocates once per (device, stream)
- *                               and keeps (split_k * M * N * 4 bytes, at most
- *                               2 GiB); a second kernel sums them in part order
- *                               into out.  The first call on a stream must not
- *                               be under graph capture (it allocates).
+ *                               tile (1..16; > 1 only for the pipelined matmul
+ *                               body: lhsT variants 1 and 3, matmul_lhs_rhs
+ *                               variants 0 and 2; every part must get at least
+ *                               one K tile).  The parts write fp32 partial
+ *                               products to a workspace (split_k * M * N * 4
+ *                               bytes, at most 2 GiB) that the call allocates
+ *                               stream-ordered from a library-owned memory
+ *                               pool and frees after the launch; a second
+ *                               kernel sums them in part order into out.  Under
+ *                               HIP graph capture the workspace becomes
+ *                               allocation and free nodes of the graph.
  *   group_m                   : L2 raster group height in tiles (0 = default 8)
  *   variant                   : kernel-specific pipeline (every variant computes
  *                               the same function):

@@ -87,10 +87,14 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
   if (c.split_k < 1 || c.split_k > kMaxSplit)
     return fail(MI_E_SPLIT, "split_k=%d outside [1, %d]", c.split_k, kMaxSplit);
   if (c.split_k > 1) {
-    // Split-K: the pipelined lhsT kernels only, and every part must get at
-    // least one K tile.
-    if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_BF16 || (c.variant != 1 && c.variant != 3))
-      return fail(MI_E_SPLIT, "split_k=%d needs the pipelined lhsT.rhs kernel (matmul variants 1 and 3)",
+    // Split-K: the pipelined matmul body only (lhsT variants 1 and 3,
+    // matmul_lhs_rhs variants 0 and 2), and every part must get at least
+    // one K tile.
+    const bool ok = (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (c.variant == 1 || c.variant == 3)) ||
+                    (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 && (c.variant == 0 || c.variant == 2));
+    if (!ok)
+      return fail(MI_E_SPLIT,
+                  "split_k=%d needs the pipelined matmul (lhsT.rhs variants 1, 3; lhs.rhs variants 0, 2)",
                   c.split_k);
     const long long kt = ((long long)K + c.block_k - 1) / c.block_k;
     const long long kts = (kt + c.split_k - 1) / c.split_k;
@@ -241,30 +245,35 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
   return MI_OK;
 }
 
-// Split-K workspace, one per (device, stream): launches on one stream run in
-// order, so they can share it; launches on different streams get their own.
-// It grows to the largest request and lives until the process ends.
-struct SplitWorkspace {
-  float* ws = nullptr;
-  size_t bytes = 0;
-};
-std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, SplitWorkspace> g_ws;
+// Split-K workspace: allocated per call, stream-ordered
+// (hipMallocFromPoolAsync / hipFreeAsync), from a memory pool the library
+// keeps per device with no release threshold, so that after the first calls
+// the pool hands back cached memory.  Each call has its own buffer (calls on
+// different streams do not share one), and a call under HIP graph capture
+// becomes allocation and free nodes of the graph.
+std::mutex g_pool_mu;
+std::map<int, hipMemPool_t> g_pools;
 
-int split_workspace(size_t bytes, hipStream_t stream, float** ws) {
+int split_pool(hipMemPool_t* out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-  std::lock_guard<std::mutex> lock(g_ws_mu);
-  SplitWorkspace& w = g_ws[{dev, stream}];
-  if (w.bytes < bytes) {
-    if (w.ws && (e = hipFree(w.ws)) != hipSuccess) return hip_fail(e, "split-K workspace free");
-    w.ws = nullptr;
-    w.bytes = 0;
-    if ((e = hipMalloc((void**)&w.ws, bytes)) != hipSuccess) return hip_fail(e, "split-K workspace alloc");
-    w.bytes = bytes;
+  std::lock_guard<std::mutex> lock(g_pool_mu);
+  auto it = g_pools.find(dev);
+  if (it == g_pools.end()) {
+    hipMemPoolProps props = {};
+    props.allocType = hipMemAllocationTypePinned;
+    props.handleTypes = hipMemHandleTypeNone;
+    props.location.type = hipMemLocationTypeDevice;
+    props.location.id = dev;
+    hipMemPool_t pool = nullptr;
+    if ((e = hipMemPoolCreate(&pool, &props)) != hipSuccess) return hip_fail(e, "split-K memory pool");
+    uint64_t keep = ~0ull;
+    if ((e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep)) != hipSuccess)
+      return hip_fail(e, "split-K memory pool threshold");
+    it = g_pools.emplace(dev, pool).first;
   }
-  *ws = w.ws;
+  *out = it->second;
   return MI_OK;
 }
 
@@ -278,10 +287,18 @@ int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, voi
   mi::MiArgs a = args_in;
   a.group_m = cfg.group_m > 0 ? cfg.group_m : 8;
   if (cfg.split_k > 1) {
+    hipMemPool_t pool = nullptr;
+    const int prc = split_pool(&pool);
+    if (prc != MI_OK) return prc;
     const size_t ws_bytes = (size_t)cfg.split_k * (size_t)a.M * (size_t)a.N * 4u;
-    const int wrc = split_workspace(ws_bytes, (hipStream_t)stream, &a.ws);
-    if (wrc != MI_OK) return wrc;
+    hipError_t ae = hipMallocFromPoolAsync((void**)&a.ws, ws_bytes, pool, (hipStream_t)stream);
+    if (ae != hipSuccess) return hip_fail(ae, "split-K workspace alloc");
     a.parts = cfg.split_k;
+    const hipError_t le = e->launch(a, (hipStream_t)stream);
+    const hipError_t fe = hipFreeAsync(a.ws, (hipStream_t)stream);
+    if (le != hipSuccess) return hip_fail(le, "kernel launch");
+    if (fe != hipSuccess) return hip_fail(fe, "split-K workspace free");
+    return MI_OK;
   }
   const hipError_t err = e->launch(a, (hipStream_t)stream);
   if (err != hipSuccess) return hip_fail(err, "kernel launch");

@@ -608,7 +608,6 @@ template <int BM, int BN, int BK, int WAVES, int STAGES, bool AK, bool NTB = fal
 __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, const uint16_t* __restrict__ rhs,
                                              uint16_t* __restrict__ out, int M, int N, int K, int group_m,
                                              char* smem, const SplitK sk = SplitK{1, nullptr}) {
-  static_assert(!(SPLIT && AK), "split-K is built for the lhsT layout only");
   using C = PipeCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
   static_assert(G::ok, "illegal wave grid");
@@ -632,22 +631,26 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   const int m0 = tmi * BM, n0 = tni * BN;
   const int wm0 = (wave / G::WN) * G::WTM;
   const int wn0 = (wave % G::WN) * G::WTN;
+  const int lda = K;  // row stride of the K-contiguous lhs: the whole K
+  int k0 = 0;
   if constexpr (SPLIT) {
-    // Split-K part `part`: K rows [k0, k0 + K) of lhsT and rhs (the host
-    // guarantees every part a non-empty range).
+    // Split-K part `part`: K indices [k0, k0 + K) of both operands (the host
+    // guarantees every part a non-empty range): rows of lhsT and rhs,
+    // columns of a K-contiguous lhs (whose rows keep their stride).
     const int kts = ((K + BK - 1) / BK + sk.parts - 1) / sk.parts;
-    const int k0 = part * kts * BK;
-    a += (size_t)k0 * (size_t)M;
+    k0 = part * kts * BK;
+    a += AK ? (size_t)k0 : (size_t)k0 * (size_t)M;
     rhs += (size_t)k0 * (size_t)N;
     K = K - k0 < kts * BK ? K - k0 : kts * BK;
   }
 
-  const uint32_t a_bytes = (uint32_t)K * (uint32_t)M * 2u;
+  // Bytes from the (part's) base to the end of the A buffer.
+  const uint32_t a_bytes = AK ? ((uint32_t)M * (uint32_t)lda - (uint32_t)k0) * 2u : (uint32_t)K * (uint32_t)M * 2u;
   const uint32_t b_bytes = (uint32_t)K * (uint32_t)N * 2u;
   const int KT = (K + BK - 1) / BK;
   LA la;
   LB lb;
-  if constexpr (AK) la.init(wave, lane, m0, K, K - (KT - 1) * BK, a_bytes);
+  if constexpr (AK) la.init(wave, lane, m0, lda, K - (KT - 1) * BK, a_bytes);
   else la.init(wave, lane, m0, M);
   lb.init(wave, lane, n0, N);
   const uint32_t kstep_a = AK ? (uint32_t)BK * 2u : (uint32_t)BK * (uint32_t)M * 2u;
@@ -804,14 +807,17 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
 }
 
 // out[M,N] = lhs[M,K] . rhs[K,N] with lhs K-contiguous (matmul_lhs_rhs);
-// NTB: rhs read non-temporally (variant 2, skinny M).
-template <int BM, int BN, int BK, int WAVES, int STAGES, bool NTB = false>
+// NTB: rhs read non-temporally (variant 2, skinny M); SPLIT: split-K as for
+// the lhsT kernel.
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool NTB = false, bool SPLIT = false>
 __global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pipe_kernel(const uint16_t* __restrict__ lhs,
                                                                          const uint16_t* __restrict__ rhs,
                                                                          uint16_t* __restrict__ out, int M, int N,
-                                                                         int K, int group_m) {
+                                                                         int K, int group_m, int parts,
+                                                                         float* __restrict__ ws) {
   __shared__ __attribute__((aligned(1024))) char smem[PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
-  mm_pipe_body<BM, BN, BK, WAVES, STAGES, true, NTB>(lhs, rhs, out, M, N, K, group_m, smem);
+  mm_pipe_body<BM, BN, BK, WAVES, STAGES, true, NTB, SPLIT>(lhs, rhs, out, M, N, K, group_m, smem,
+                                                            SplitK{parts, ws});
 }
 
 // ---------------------------------------------------------------------------

@@ -50,6 +50,14 @@ hipError_t launch_mm_bf16(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Split-K second pass: out = bf16(sum over the parts of ws), in part order.
+inline void launch_splitk_sum(const MiArgs& a, hipStream_t s) {
+  const size_t n = (size_t)a.M * (size_t)a.N;
+  const size_t blocks = (n / 8 + 255) / 256;
+  hipLaunchKernelGGL(splitk_sum_kernel<0>, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s,
+                     (const float*)a.ws, (uint16_t*)a.out, n, a.parts);
+}
+
 template <int BM, int BN, int BK, int W, int S, bool NTB = false>
 hipError_t launch_mm_pipe(const MiArgs& a, hipStream_t s) {
   if (a.parts > 1) {
@@ -59,10 +67,7 @@ hipError_t launch_mm_pipe(const MiArgs& a, hipStream_t s) {
                        (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, a.ws);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const size_t n = (size_t)a.M * (size_t)a.N;
-    const size_t blocks = (n / 8 + 255) / 256;
-    hipLaunchKernelGGL(splitk_sum_kernel<0>, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s,
-                       (const float*)a.ws, (uint16_t*)a.out, n, a.parts);
+    launch_splitk_sum(a, s);
   } else {
     hipLaunchKernelGGL((mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, false>),
                        dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
@@ -73,9 +78,18 @@ hipError_t launch_mm_pipe(const MiArgs& a, hipStream_t s) {
 
 template <int BM, int BN, int BK, int W, int S, bool NTB = false>
 hipError_t launch_mm_lhs(const MiArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB>), dim3(grid_tiles(a.M, a.N, BM, BN)),
-                     dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K,
-                     a.group_m);
+  if (a.parts > 1) {
+    hipLaunchKernelGGL((mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, true>),
+                       dim3(grid_tiles(a.M, a.N, BM, BN) * a.parts), dim3(W * 64), 0, s, (const uint16_t*)a.a,
+                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, a.ws);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_splitk_sum(a, s);
+  } else {
+    hipLaunchKernelGGL((mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, false>),
+                       dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
+                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, 1, nullptr);
+  }
   return hipGetLastError();
 }
 
@@ -177,12 +191,16 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);                \
   template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, true>(                        \
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
-#define MI_MMK_INST(BM, BN, BK, W, S)                                                                         \
-  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*,    \
-                                                                          uint16_t*, int, int, int, int);
-#define MI_MMKN_INST(BM, BN, BK, W, S)                                                                          \
-  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true>(const uint16_t*, const uint16_t*, \
-                                                                                uint16_t*, int, int, int, int);
+#define MI_MMK_INST(BM, BN, BK, W, S)                                                                          \
+  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, false>(                       \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);                           \
+  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, true>(                        \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
+#define MI_MMKN_INST(BM, BN, BK, W, S)                                                                         \
+  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, false>(                        \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);                           \
+  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, true>(                         \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
 #define MI_MMKP_INST(BM, BN, BK, W, S)                                                                        \
   template __global__ void mm_lhs_rhs_bf16_pair_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*,    \
                                                                           uint16_t*, int, int, int, int);

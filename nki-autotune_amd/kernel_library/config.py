@@ -152,16 +152,16 @@ SPLIT_K_PARTS = (2, 4, 8, 16)
 
 
 def split_k_variants(func_name: str, grid: list[TileConfig], M: int, N: int) -> list[TileConfig]:
-    """Split-K copies of the pipelined lhsT configs whose output tiles fill
+    """Split-K copies of the pipelined matmul configs whose output tiles fill
     fewer than two waves of workgroups on the GPU (< 512 tiles): K is then
     the only axis left to spread the work over more compute units.  Part
     counts keep the grid within 1024 workgroups (four per compute unit)."""
-    if func_name not in ("matmul_lhsT_rhs", "matmul_lhsT_rhs_nkigym"):
-        return []
+    splittable = {"matmul_lhsT_rhs": (1, 3), "matmul_lhsT_rhs_nkigym": (1, 3), "matmul_lhs_rhs": (0, 2),
+                  "matmul_lhs_rhs_nkigym": (0, 2)}.get(func_name, ())
     out = []
     for c in grid:
         tiles = -(-M // c.block_m) * -(-N // c.block_n)
-        if c.variant in (1, 3) and c.split_k == 1 and tiles < 512:
+        if c.variant in splittable and c.split_k == 1 and tiles < 512:
             out += [replace(c, split_k=p) for p in SPLIT_K_PARTS if tiles * p <= 1024]
     return out
 

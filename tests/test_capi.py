@@ -71,7 +71,7 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (RMS, TileConfig(128, 128, 32, 4, 3, variant=12), (1024, 1024, 8200), _lib.MI_E_RANGE),
         (RMS, TileConfig(128, 128, 32, 4, 3, variant=12), (1024, 1024, 8192), _lib.MI_OK),
         (RMS, TileConfig(64, 128, 64, 4, 2, variant=11), (16, 28672, 8192), _lib.MI_OK),
-        # split-K: pipelined lhsT kernels only, every part non-empty, workspace <= 2 GiB
+        # split-K: the pipelined matmul body only, every part non-empty, workspace <= 2 GiB
         (MM, TileConfig(128, 128, 64, 4, 3, split_k=2, variant=1), (2048, 1024, 8192), _lib.MI_OK),
         (MM, TileConfig(32, 128, 128, 4, 3, split_k=16, variant=3), (128, 28672, 8192), _lib.MI_OK),
         (MM, TileConfig(128, 128, 64, 4, 3, split_k=17, variant=1), (2048, 1024, 8192), _lib.MI_E_SPLIT),
@@ -79,7 +79,9 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (MM, TileConfig(128, 128, 64, 4, 3, split_k=2, variant=1), (2048, 1024, 64), _lib.MI_E_SPLIT),   # 1 K tile
         (MM, TileConfig(128, 128, 64, 4, 3, split_k=3, variant=1), (2048, 1024, 256), _lib.MI_E_SPLIT),  # 2+2+0
         (MM, TileConfig(128, 128, 64, 4, 3, split_k=2, variant=2), (2048, 1024, 8192), _lib.MI_E_SPLIT),
-        (LHS, TileConfig(128, 128, 64, 4, 3, split_k=2), (2048, 1024, 8192), _lib.MI_E_SPLIT),
+        (LHS, TileConfig(128, 128, 64, 4, 3, split_k=2), (2048, 1024, 8192), _lib.MI_OK),
+        (LHS, TileConfig(128, 128, 64, 4, 3, split_k=4, variant=2), (128, 28672, 8192), _lib.MI_OK),
+        (LHS, TileConfig(256, 256, 32, 8, 3, split_k=2, variant=1), (2048, 1024, 8192), _lib.MI_E_SPLIT),
         (RMS, TileConfig(128, 128, 64, 4, 2, split_k=2, variant=4), (2048, 1024, 4096), _lib.MI_E_SPLIT),
         (MM, TileConfig(32, 128, 64, 4, 4, split_k=16, variant=1), (16384, 16384, 8192), _lib.MI_E_RANGE),
         (MM, TileConfig(128, 128, 48, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),
@@ -114,6 +116,8 @@ def test_split_k_variants_are_named_and_legal():
     assert not [x for x in legal_configs("matmul_lhsT_rhs", 8192, 8192, 8192) if x.split_k > 1 and x.block_m >= 128
                 and x.block_n >= 128]
     assert split_k_variants("rmsnorm_matmul", compiled_configs("rmsnorm_matmul"), 16, 16) == []
+    lhs = [x for x in legal_configs("matmul_lhs_rhs", 512, 512, 32768) if x.split_k > 1]
+    assert lhs and all(x.variant in (0, 2) for x in lhs)
 
 
 def test_cfg_check_rejects_unknown_kernel_and_null():

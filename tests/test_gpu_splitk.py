@@ -142,10 +142,36 @@ def test_benchmark_shapes(gpu, M, N, K, cfg):
     assert rep["ok"], (tc.name, rep)
 
 
+def test_concurrent_streams(gpu):
+    """Split-K calls on two streams with no synchronisation between them: each call has its own workspace."""
+    import torch
+
+    import kernel_library as kl
+
+    M, N, K = 256, 512, 8192
+    tc = kl.TileConfig(64, 128, 64, 4, 4, split_k=8, variant=1)
+    ds = [mm_inputs(K, M, N, seed=30 + i) for i in range(2)]
+    ins = [(_dev(d["lhs_T"], gpu), _dev(d["rhs"], gpu)) for d in ds]
+    streams = [torch.cuda.Stream(device=gpu) for _ in range(2)]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream(gpu))
+    outs = [[None] * 4 for _ in range(2)]
+    for rep_i in range(4):
+        for i, st in enumerate(streams):
+            with torch.cuda.stream(st):
+                outs[i][rep_i] = kl.matmul_lhsT_rhs(*ins[i], cfg=tc)
+    torch.cuda.synchronize()
+    for i, d in enumerate(ds):
+        expected = omm.closed_form(d["lhs_T"], d["rhs"])
+        for rep_i in range(4):
+            rep = mm_check(_host(outs[i][rep_i]), expected)
+            assert rep["ok"], (i, rep_i, rep)
+
+
 def test_graph_replay_matches_eager(gpu):
-    """A split-K call captured in a HIP graph (workspace allocated by an
-    eager call first) replays to the eager result, with eager work between
-    replays."""
+    """A split-K call captured in a HIP graph (its workspace becomes allocation
+    and free nodes of the graph) replays to the eager result, with eager
+    split-K work between replays."""
     import torch
 
     import kernel_library as kl
@@ -185,3 +211,30 @@ def test_library_default_splits_few_tile_long_k(gpu):
     out = kl.matmul_lhsT_rhs(_dev(d["lhs_T"], gpu), _dev(d["rhs"], gpu))
     rep = mm_check(_host(out), omm.closed_form(d["lhs_T"], d["rhs"]))
     assert rep["ok"], (cfg.name, rep)
+
+
+@pytest.mark.parametrize("parts", [2, 4])
+@pytest.mark.parametrize("cfg", [(128, 128, 64, 4, 3, 0), (256, 256, 32, 4, 3, 0), (64, 128, 64, 4, 4, 2)],
+                         ids=lambda c: "bm{}_bn{}_bk{}_w{}_s{}_v{}".format(*c))
+def test_lhs_rhs_split_matches_oracle_and_lhsT(gpu, cfg, parts):
+    """matmul_lhs_rhs (K-contiguous lhs) with split-K: ragged M, N and K vs the oracle, and bitwise equal to
+    the lhsT kernel's split-K on the transposed operand (same K parts, same MFMA order)."""
+    import torch
+
+    import kernel_library as kl
+
+    bm, bn, bk, w, s, v = cfg
+    M, N, K = 200, 264, 1000
+    tc = kl.TileConfig(bm, bn, bk, w, s, split_k=parts, variant=v)
+    print("split-K lhs", tc.name, M, N, K, flush=True)
+    d = mm_inputs(K, M, N, seed=20 + parts)
+    lhs = _dev(np.ascontiguousarray(d["lhs_T"].T), gpu)
+    rhs = _dev(d["rhs"], gpu)
+    out = _nan_out(M, N, gpu)
+    kl.matmul_lhs_rhs(lhs, rhs, cfg=tc, out=out)
+    rep = mm_check(_host(out), omm.closed_form_lhs(np.ascontiguousarray(d["lhs_T"].T), d["rhs"]))
+    assert rep["ok"], (tc.name, rep)
+    twin = kl.TileConfig(bm, bn, bk, w, s, split_k=parts, variant=1 if v == 0 else 3)
+    ref = kl.matmul_lhsT_rhs(_dev(d["lhs_T"], gpu), rhs, cfg=twin)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), (tc.name, twin.name)
