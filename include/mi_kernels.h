@@ -58,13 +58,18 @@ enum {
  *   split_k                   : K split over this many workgroups per output
  *                               tile (1..16; > 1 only for the pipelined matmul
  *                               body: lhsT variants 1 and 3, matmul_lhs_rhs
- *                               variants 0 and 2; every part must get at least
- *                               one K tile).  The parts write fp32 partial
- *                               products to a workspace (split_k * M * N * 4
- *                               bytes, at most 2 GiB) that the call allocates
+ *                               variants 0 and 2, and the register-staged
+ *                               fused kernel: rmsnorm_matmul variants 4, 5, 11,
+ *                               12, whose gamma limit then applies per part;
+ *                               every part must get at least one K tile).  The
+ *                               parts write fp32 partial products (and, fused,
+ *                               their rows' sums of squares) to a workspace
+ *                               (split_k * (M * N + M) * 4 bytes, at most
+ *                               2 GiB) that the call allocates
  *                               stream-ordered from a library-owned memory
  *                               pool and frees after the launch; a second
- *                               kernel sums them in part order into out.  Under
+ *                               kernel sums them in part order into out (and
+ *                               applies 1/rms, fused).  Under
  *                               HIP graph capture the workspace becomes
  *                               allocation and free nodes of the graph.
  *   group_m                   : L2 raster group height in tiles (0 = default 8)

@@ -13,7 +13,7 @@ a state is a :class:`~kernel_library.config.TileConfig` and an action (an
 * ``group_m`` (the L2 raster height) doubled or halved,
 * ``variant`` set to another pipeline of the same kernel family,
 * ``split_k`` (K split over several workgroups per output tile) doubled or
-  halved, for the two matmuls.
+  halved, for the two matmuls and the fused kernel.
 
 An atom is legal at a state when its result passes the library's static
 legality check at the problem shape (``mi_cfg_check``: LDS budget, wave
@@ -68,7 +68,7 @@ def atoms_for(func_name: str) -> list[Atom]:
     out += [Atom("waves", "swap"), Atom("lds_stages", "+1"), Atom("lds_stages", "-1"),
             Atom("group_m", "x2"), Atom("group_m", "/2")]
     out += [Atom("variant", f"={v}") for v in FAMILY_VARIANTS.get(fam, (0,))]
-    if fam in ("matmul_lhsT_rhs", "matmul_lhs_rhs"):
+    if fam in ("matmul_lhsT_rhs", "matmul_lhs_rhs", "rmsnorm_matmul"):
         out += [Atom("split_k", "x2"), Atom("split_k", "/2")]
     return out
 

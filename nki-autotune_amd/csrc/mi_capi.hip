@@ -91,17 +91,20 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
     // matmul_lhs_rhs variants 0 and 2), and every part must get at least
     // one K tile.
     const bool ok = (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (c.variant == 1 || c.variant == 3)) ||
-                    (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 && (c.variant == 0 || c.variant == 2));
+                    (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 && (c.variant == 0 || c.variant == 2)) ||
+                    (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 &&
+                     (c.variant == 4 || c.variant == 5 || c.variant == 11 || c.variant == 12));
     if (!ok)
       return fail(MI_E_SPLIT,
-                  "split_k=%d needs the pipelined matmul (lhsT.rhs variants 1, 3; lhs.rhs variants 0, 2)",
+                  "split_k=%d needs the pipelined matmul (lhsT.rhs variants 1, 3; lhs.rhs variants 0, 2) or "
+                  "the register-staged fused kernel (rmsnorm_matmul variants 4, 5, 11, 12)",
                   c.split_k);
     const long long kt = ((long long)K + c.block_k - 1) / c.block_k;
     const long long kts = (kt + c.split_k - 1) / c.split_k;
     if ((long long)(c.split_k - 1) * kts >= kt)
       return fail(MI_E_SPLIT, "split_k=%d leaves a K part empty at K=%d, block_k=%d", c.split_k, K, c.block_k);
-    const unsigned long long ws =
-        (unsigned long long)c.split_k * (unsigned long long)M * (unsigned long long)N * 4ull;
+    const unsigned long long ws = (unsigned long long)c.split_k *
+                                  ((unsigned long long)M * (unsigned long long)N + (unsigned long long)M) * 4ull;
     if (ws > kMaxSplitWorkspace)
       return fail(MI_E_RANGE, "split-K workspace of %llu bytes exceeds %llu", ws, kMaxSplitWorkspace);
   }
@@ -164,14 +167,21 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
     // K step the kernel walks (variants 4/5/11/12: one tile; 6..9: D = 2 or
     // 3 tiles; 10: rounds of 4 tiles) must fit the instance's gamma entries.
     // The limit holds with or without gamma (legality is gamma-agnostic).
+    // With split_k > 1 (one-tile variants only) each part stages the gamma of
+    // its own K range: ceil(ceil(K/block_k)/split_k) tiles.
     if (e->gamma_kmax > 0) {
       const int d = c.variant == 10                      ? 4
                     : c.variant >= 6 && c.variant <= 9 ? 2 + ((c.variant - 6) & 1)
                                                        : 1;
       const long long span = (long long)d * c.block_k;
-      if (((long long)K + span - 1) / span * span > e->gamma_kmax)
-        return fail(MI_E_RANGE, "K=%d exceeds the %d gamma entries variant %d stages in LDS", K, e->gamma_kmax,
-                    c.variant);
+      long long need = ((long long)K + span - 1) / span * span;
+      if (c.split_k > 1) {
+        const long long kt = ((long long)K + c.block_k - 1) / c.block_k;
+        need = (kt + c.split_k - 1) / c.split_k * c.block_k;
+      }
+      if (need > e->gamma_kmax)
+        return fail(MI_E_RANGE, "K=%d (%lld per part) exceeds the %d gamma entries variant %d stages in LDS", K,
+                    need, e->gamma_kmax, c.variant);
     }
   }
   if (out) *out = e;
@@ -290,7 +300,9 @@ int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, voi
     hipMemPool_t pool = nullptr;
     const int prc = split_pool(&pool);
     if (prc != MI_OK) return prc;
-    const size_t ws_bytes = (size_t)cfg.split_k * (size_t)a.M * (size_t)a.N * 4u;
+    // Products [parts][M][N]; the fused kernel adds its rows' sums of squares [parts][M].
+    const size_t rows = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 ? (size_t)a.M : 0;
+    const size_t ws_bytes = (size_t)cfg.split_k * ((size_t)a.M * (size_t)a.N + rows) * 4u;
     hipError_t ae = hipMallocFromPoolAsync((void**)&a.ws, ws_bytes, pool, (hipStream_t)stream);
     if (ae != hipSuccess) return hip_fail(ae, "split-K workspace alloc");
     a.parts = cfg.split_k;

@@ -130,18 +130,30 @@ hipError_t launch_rms_ring(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int BM, int BN, int BK, int W, int S, int XS, bool HG, bool NTW, bool SPLIT>
+void launch_rms_xreg_one(const MiArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, HG, NTW, SPLIT>),
+                     dim3(grid_tiles(a.M, a.N, BM, BN) * (SPLIT ? a.parts : 1)), dim3(W * 64), 0, s,
+                     (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N,
+                     a.K, a.inv_k, a.eps, a.group_m, SPLIT ? a.parts : 1, SPLIT ? a.ws : nullptr);
+}
+
 template <int BM, int BN, int BK, int W, int S, int XS, bool NTW = false>
 hipError_t launch_rms_xreg(const MiArgs& a, hipStream_t s) {
-  if (a.g)
-    hipLaunchKernelGGL((rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, true, NTW>),
-                       dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
-                       (const uint16_t*)a.g, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps,
-                       a.group_m);
-  else
-    hipLaunchKernelGGL((rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, false, NTW>),
-                       dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
-                       (const uint16_t*)a.g, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps,
-                       a.group_m);
+  if (a.parts > 1) {
+    // Split-K: the parts' products and sums of squares into ws, then out.
+    if (a.g) launch_rms_xreg_one<BM, BN, BK, W, S, XS, true, NTW, true>(a, s);
+    else launch_rms_xreg_one<BM, BN, BK, W, S, XS, false, NTW, true>(a, s);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const size_t blocks = ((size_t)a.M * (size_t)a.N / 8 + 255) / 256;
+    hipLaunchKernelGGL(splitk_rms_sum_kernel<0>, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s,
+                       (const float*)a.ws, (uint16_t*)a.out, a.M, a.N, a.parts, a.inv_k, a.eps);
+  } else if (a.g) {
+    launch_rms_xreg_one<BM, BN, BK, W, S, XS, true, NTW, false>(a, s);
+  } else {
+    launch_rms_xreg_one<BM, BN, BK, W, S, XS, false, NTW, false>(a, s);
+  }
   return hipGetLastError();
 }
 
@@ -218,18 +230,23 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
 
 // Variant 4 stages x through a 2-slot register ring, variant 5 a 3-slot one.
-#define MI_RMSX_INST(BM, BN, BK, W, S, XS)                                                            \
-  template __global__ void rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, true>(                  \
-      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int); \
-  template __global__ void rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, false>(                 \
-      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
+// Each with and without gamma, unsplit and split-K.
+#define MI_RMSX_ONE(BM, BN, BK, W, S, XS, HG, NTW, SPLIT)                                                  \
+  template __global__ void rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, HG, NTW, SPLIT>(              \
+      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int, int, \
+      float*);
+#define MI_RMSX_INST(BM, BN, BK, W, S, XS)              \
+  MI_RMSX_ONE(BM, BN, BK, W, S, XS, true, false, false)  \
+  MI_RMSX_ONE(BM, BN, BK, W, S, XS, false, false, false) \
+  MI_RMSX_ONE(BM, BN, BK, W, S, XS, true, false, true)   \
+  MI_RMSX_ONE(BM, BN, BK, W, S, XS, false, false, true)
 
 // Variants 11 / 12: 4 / 5 with W read non-temporally (skinny M).
-#define MI_RMSXN_INST(BM, BN, BK, W, S, XS)                                                           \
-  template __global__ void rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, true, true>(            \
-      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int); \
-  template __global__ void rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, false, true>(           \
-      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
+#define MI_RMSXN_INST(BM, BN, BK, W, S, XS)           \
+  MI_RMSX_ONE(BM, BN, BK, W, S, XS, true, true, false)  \
+  MI_RMSX_ONE(BM, BN, BK, W, S, XS, false, true, false) \
+  MI_RMSX_ONE(BM, BN, BK, W, S, XS, true, true, true)   \
+  MI_RMSX_ONE(BM, BN, BK, W, S, XS, false, true, true)
 
 // x operand straight to registers: variant 6 + (D-2) + 2*(wave grid transposed).
 #define MI_RMSD_INST(BM, BN, BK, W, S, WMX, D, V)                                                     \

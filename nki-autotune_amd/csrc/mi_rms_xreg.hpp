@@ -77,11 +77,17 @@ __device__ __forceinline__ u32x4_t vload16(__amdgpu_buffer_rsrc_t rs, uint32_t v
 __device__ __forceinline__ void reg_ready(u32x4_t& r) { asm volatile("" : "+v"(r)); }
 
 // NTW: W read non-temporally (variants 11 / 12: skinny M, where W is
-// streamed once).
-template <int BM, int BN, int BK, int WAVES, int STAGES, int XS, bool HG, bool NTW = false, int SSQ_PARTS = 4>
+// streamed once).  SPLIT: K split over `parts` workgroups per output tile;
+// part p writes its unscaled fp32 products to ws[p][M][N] and its rows'
+// sums of squares over its K range to ws[parts*M*N + p*M + m] (from the
+// workgroups of the first column of tiles), and splitk_rms_sum_kernel forms
+// out.  gamma then needs LDS room for one part's K range only.
+template <int BM, int BN, int BK, int WAVES, int STAGES, int XS, bool HG, bool NTW = false, bool SPLIT = false,
+          int SSQ_PARTS = 4>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ gamma, const uint16_t* __restrict__ w,
-    uint16_t* __restrict__ out, int M, int N, int K, float inv_k, float eps, int group_m) {
+    uint16_t* __restrict__ out, int M, int N, int K, float inv_k, float eps, int group_m, int parts,
+    float* __restrict__ ws) {
   using C = XregCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
   static_assert(G::ok, "illegal wave grid");
@@ -103,13 +109,27 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  int tmi, tni;
-  tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
+  int tmi, tni, part = 0;
+  if constexpr (SPLIT) tile_coords_split(tiles_m, tiles_n, group_m, parts, tmi, tni, part);
+  else tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
   const int m0 = tmi * BM, n0 = tni * BN;
   const int wm0 = (wave / G::WN) * G::WTM;
   const int wn0 = (wave % G::WN) * G::WTN;
 
-  const uint32_t x_bytes = (uint32_t)M * (uint32_t)K * 2u;
+  const int ldx = K;  // row stride of x: the whole K
+  int k0 = 0;
+  if constexpr (SPLIT) {
+    // Part `part`: K indices [k0, k0 + K) -- columns of x, entries of gamma,
+    // rows of W (the host guarantees every part a non-empty range).
+    const int kts = ((K + BK - 1) / BK + parts - 1) / parts;
+    k0 = part * kts * BK;
+    x += k0;
+    gamma += k0;
+    w += (size_t)k0 * (size_t)N;
+    K = K - k0 < kts * BK ? K - k0 : kts * BK;
+  }
+  // Bytes from the (part's) base to the end of x.
+  const uint32_t x_bytes = ((uint32_t)M * (uint32_t)ldx - (uint32_t)k0) * 2u;
   const uint32_t w_bytes = (uint32_t)K * (uint32_t)N * 2u;
   const int KT = (K + BK - 1) / BK;
   auto clamp = [&](int kt) { return kt < KT ? kt : KT - 1; };
@@ -140,7 +160,7 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   for (int i = 0; i < CPT; ++i) {
     const int c = i * NT + tid;
     xrow[i] = c / KC;
-    xoff[i] = ((uint32_t)(m0 + xrow[i]) * (uint32_t)K + (uint32_t)(8 * kc)) * 2u;
+    xoff[i] = ((uint32_t)(m0 + xrow[i]) * (uint32_t)ldx + (uint32_t)(8 * kc)) * 2u;
     xlds[i] = xrow[i] * (BK * 2) + 16 * (kc ^ k_swz<BK>(xrow[i]));
   }
   u32x4_t xr[XS][CPT];
@@ -346,6 +366,18 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
   if constexpr (XS == 3) x_ready(S2{});
   __syncthreads();  // the epilogue reuses the panel buffers
 
+  if constexpr (SPLIT) {
+    // This part's sums of squares (one column of tiles writes them) and its
+    // unscaled products; the second pass sums the parts and scales.
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const float r = row_allreduce<KC>(sum_parts<NSA>(ss[i]));
+      const int m = m0 + xrow[i];
+      if (tni == 0 && kc == 0 && m < M) ws[(size_t)parts * M * N + (size_t)part * M + m] = r;
+    }
+    store_partial<TM, TN>(acc, ws + (size_t)part * M * N, lane, M, N, m0 + wm0, n0 + wn0);
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const float r = row_allreduce<KC>(sum_parts<NSA>(ss[i]));
@@ -356,6 +388,35 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
 #pragma unroll
   for (int mt = 0; mt < TM; ++mt) scale[mt] = rms_lds[wm0 + mt * 32 + (lane & 31)];
   store_tile<TM, TN, WAVES>(acc, scale, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
+}
+
+// Split-K second pass of the fused kernel: for 8 consecutive elements of
+// row m, out = bf16(rsqrt(sum_p ssq[p][m] * inv_k + eps) * sum_p ws[p][...]),
+// both sums in part order (ws = [parts][M][N] products, then [parts][M]
+// sums of squares; N % 8 == 0, so 8 elements never straddle rows).
+template <int UNUSED = 0>
+__global__ __launch_bounds__(256) void splitk_rms_sum_kernel(const float* __restrict__ ws, uint16_t* __restrict__ out,
+                                                             int M, int N, int parts, float inv_k, float eps) {
+  const size_t n = (size_t)M * (size_t)N;
+  const float* ssq = ws + (size_t)parts * n;
+  const size_t stride = (size_t)gridDim.x * 256 * 8;
+  for (size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += stride) {
+    const size_t m = i / (size_t)N;
+    float r = ssq[m];
+    f32x4_t lo = *(const f32x4_t*)(ws + i), hi = *(const f32x4_t*)(ws + i + 4);
+    for (int p = 1; p < parts; ++p) {
+      r += ssq[(size_t)p * M + m];
+      lo += *(const f32x4_t*)(ws + (size_t)p * n + i);
+      hi += *(const f32x4_t*)(ws + (size_t)p * n + i + 4);
+    }
+    const float sc = 1.0f / __builtin_sqrtf(r * inv_k + eps);
+    u32x4_t o;
+    o.x = pack_bf16x2(lo[0] * sc, lo[1] * sc);
+    o.y = pack_bf16x2(lo[2] * sc, lo[3] * sc);
+    o.z = pack_bf16x2(hi[0] * sc, hi[1] * sc);
+    o.w = pack_bf16x2(hi[2] * sc, hi[3] * sc);
+    *(u32x4_t*)(out + i) = o;
+  }
 }
 
 }  // namespace mi

@@ -82,7 +82,12 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (LHS, TileConfig(128, 128, 64, 4, 3, split_k=2), (2048, 1024, 8192), _lib.MI_OK),
         (LHS, TileConfig(128, 128, 64, 4, 3, split_k=4, variant=2), (128, 28672, 8192), _lib.MI_OK),
         (LHS, TileConfig(256, 256, 32, 8, 3, split_k=2, variant=1), (2048, 1024, 8192), _lib.MI_E_SPLIT),
-        (RMS, TileConfig(128, 128, 64, 4, 2, split_k=2, variant=4), (2048, 1024, 4096), _lib.MI_E_SPLIT),
+        (RMS, TileConfig(128, 128, 64, 4, 2, split_k=2, variant=0), (2048, 1024, 4096), _lib.MI_E_SPLIT),
+        (RMS, TileConfig(128, 128, 64, 4, 2, split_k=2, variant=4), (2048, 1024, 4096), _lib.MI_OK),
+        # split parts stage the gamma of their own K range: 2 x 8192 fits, 2 x 8256 does not
+        (RMS, TileConfig(128, 128, 64, 4, 2, split_k=2, variant=4), (256, 1024, 16384), _lib.MI_OK),
+        (RMS, TileConfig(128, 128, 64, 4, 2, split_k=2, variant=4), (256, 1024, 16448), _lib.MI_E_RANGE),
+        (RMS, TileConfig(128, 128, 64, 4, 2, variant=4), (256, 1024, 16384), _lib.MI_E_RANGE),
         (MM, TileConfig(32, 128, 64, 4, 4, split_k=16, variant=1), (16384, 16384, 8192), _lib.MI_E_RANGE),
         (MM, TileConfig(128, 128, 48, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),
         (MM, TileConfig(512, 512, 32, 8, 1), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),  # legal, not prebuilt
@@ -115,7 +120,9 @@ def test_split_k_variants_are_named_and_legal():
     assert split and all(x.variant in (1, 3) for x in split)
     assert not [x for x in legal_configs("matmul_lhsT_rhs", 8192, 8192, 8192) if x.split_k > 1 and x.block_m >= 128
                 and x.block_n >= 128]
-    assert split_k_variants("rmsnorm_matmul", compiled_configs("rmsnorm_matmul"), 16, 16) == []
+    assert split_k_variants("matmul_lhsT_rhs_f32", compiled_configs("matmul_lhsT_rhs_f32"), 16, 16) == []
+    rms = [x for x in legal_configs("rmsnorm_matmul", 512, 512, 8192) if x.split_k > 1]
+    assert rms and all(x.variant in (4, 5, 11, 12) for x in rms)
     lhs = [x for x in legal_configs("matmul_lhs_rhs", 512, 512, 32768) if x.split_k > 1]
     assert lhs and all(x.variant in (0, 2) for x in lhs)
 

@@ -238,3 +238,50 @@ def test_lhs_rhs_split_matches_oracle_and_lhsT(gpu, cfg, parts):
     ref = kl.matmul_lhsT_rhs(_dev(d["lhs_T"], gpu), rhs, cfg=twin)
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), (tc.name, twin.name)
+
+
+@pytest.mark.parametrize("with_gamma", [True, False])
+@pytest.mark.parametrize("parts", [2, 4])
+@pytest.mark.parametrize("cfg", [(128, 128, 64, 4, 2, 4), (128, 512, 32, 8, 3, 4), (256, 256, 32, 8, 3, 5),
+                                 (128, 128, 32, 4, 3, 12), (64, 128, 64, 4, 2, 11)],
+                         ids=lambda c: "bm{}_bn{}_bk{}_w{}_s{}_v{}".format(*c))
+def test_rmsnorm_split_matches_oracle(gpu, cfg, parts, with_gamma):
+    """Fused rmsnorm_matmul with split-K: each part's products and row sums of
+    squares are summed by the second pass, which applies 1/rms.  Ragged M, N,
+    K (a multiple of 8, not of block_k); a zero row stays exactly zero."""
+    import kernel_library as kl
+    from helpers import rms_check, rms_inputs
+    from oracle import rmsnorm as orms
+
+    bm, bn, bk, w, s, v = cfg
+    M, K, N = 200, 1000, 264
+    tc = kl.TileConfig(bm, bn, bk, w, s, split_k=parts, variant=v)
+    print("split-K rms", tc.name, M, N, K, with_gamma, flush=True)
+    d = rms_inputs(M, K, N, seed=40 + parts, with_gamma=with_gamma)
+    x = d["lhs"].copy()
+    x[5] = 0.0
+    g = _dev(d["gamma"], gpu) if with_gamma else None
+    out = _nan_out(M, N, gpu)
+    kl.rmsnorm_matmul(_dev(x, gpu), _dev(d["rhs"], gpu), g, cfg=tc, out=out)
+    host = _host(out)
+    rep = rms_check(host, orms.closed_form(x, d["rhs"], d["gamma"] if with_gamma else None))
+    assert rep["ok"], (tc.name, rep)
+    assert np.all(host[5] == 0.0)
+
+
+def test_rmsnorm_split_lifts_the_gamma_limit(gpu):
+    """K = 16384 is past the 8192 fp32 gamma entries a register-staged kernel
+    holds in LDS; split in two, each part stages 8192."""
+    import kernel_library as kl
+    from helpers import rms_check, rms_inputs
+    from oracle import rmsnorm as orms
+
+    M, K, N = 256, 16384, 1024
+    whole = kl.TileConfig(128, 128, 64, 4, 2, variant=4)
+    split = kl.TileConfig(128, 128, 64, 4, 2, split_k=2, variant=4)
+    assert kl.check("rmsnorm_matmul", whole, M, N, K)[0] != 0
+    assert kl.check("rmsnorm_matmul", split, M, N, K)[0] == 0
+    d = rms_inputs(M, K, N, seed=44)
+    out = kl.rmsnorm_matmul(_dev(d["lhs"], gpu), _dev(d["rhs"], gpu), _dev(d["gamma"], gpu), cfg=split)
+    rep = rms_check(_host(out), orms.closed_form(d["lhs"], d["rhs"], d["gamma"]))
+    assert rep["ok"], rep

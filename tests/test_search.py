@@ -50,7 +50,8 @@ def test_mdp_moves_and_legality():
         mdp.step(s, Atom("variant", f"={s.variant}"))                                 # no-op move
     assert Atom("variant", "=10") in atoms_for("rmsnorm_matmul")
     assert Atom("split_k", "x2") in atoms_for("matmul_lhsT_rhs")
-    assert Atom("split_k", "x2") not in atoms_for("rmsnorm_matmul")
+    assert Atom("split_k", "x2") in atoms_for("rmsnorm_matmul")
+    assert Atom("split_k", "x2") not in atoms_for("matmul_lhsT_rhs_f32")
     assert not mdp.is_terminal(s)
 
 
