@@ -242,10 +242,22 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
     else if (mid) c = {128, 128, 64, 4, 3, 1, 8, 0};
     else c = {256, 256, 32, 8, 3, 1, 8, 1};
   } else if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16) {
-    // The register-staged kernels keep gamma in LDS (K <= 8192 here); past
-    // that the LDS-staged kernel (variant 0) takes any K.
-    if (K > 8192) c = M <= 128 ? mi_tile_cfg{64, 128, 64, 4, 2, 1, 8, 0} : mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0};
-    else if (M <= 32) c = {32, 128, 64, 4, 3, 1, 8, 11};
+    // The register-staged kernels keep gamma in LDS (8192 entries here):
+    // past K = 8192 they split K into the fewest parts whose gamma fits
+    // (1..16 parts, none empty); past that the LDS-staged kernel (variant 0)
+    // takes any K.
+    if (K > 8192) {
+      const long long kt = (K + 63) / 64;
+      int parts = 0;
+      for (int p = 2; p <= 16 && !parts; p *= 2) {
+        const long long kts = (kt + p - 1) / p;
+        const unsigned long long ws = (unsigned long long)p * ((unsigned long long)M * N + M) * 4ull;
+        if (kts * 64 <= 8192 && (long long)(p - 1) * kts < kt && ws <= kMaxSplitWorkspace) parts = p;
+      }
+      if (!parts) c = M <= 128 ? mi_tile_cfg{64, 128, 64, 4, 2, 1, 8, 0} : mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0};
+      else if (M <= 128) c = {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, parts, 8, 11};
+      else c = {128, 128, 64, 4, 2, parts, 8, 4};
+    } else if (M <= 32) c = {32, 128, 64, 4, 3, 1, 8, 11};
     else if (M <= 64) c = {64, 128, 64, 4, 3, 1, 8, 11};
     else if (M <= 128) c = {128, 128, 64, 4, 3, 1, 8, 11};
     else if (mid) c = {128, 128, 64, 4, 2, 1, 8, 4};

@@ -151,9 +151,9 @@ def test_library_default_is_legal_everywhere():
     including K past the gamma capacity of the register-staged fused kernels."""
     L = _lib.lib()
     for kid in (MM, LHS, RMS, F32):
-        for M in (8, 16, 24, 40, 64, 72, 128, 136, 200, 2048, 8192):
+        for M in (8, 16, 24, 40, 64, 72, 128, 136, 200, 2048, 8192, 16384):
             for N in (8, 136, 4096, 28672):
-                for K in (8, 264, 8192, 8200, 16384):
+                for K in (8, 264, 8192, 8200, 16384, 65536):
                     if kid == F32 and M * N * K > 2 ** 30:
                         continue
                     c = _lib.MiTileCfg()

@@ -285,3 +285,18 @@ def test_rmsnorm_split_lifts_the_gamma_limit(gpu):
     out = kl.rmsnorm_matmul(_dev(d["lhs"], gpu), _dev(d["rhs"], gpu), _dev(d["gamma"], gpu), cfg=split)
     rep = rms_check(_host(out), orms.closed_form(d["lhs"], d["rhs"], d["gamma"]))
     assert rep["ok"], rep
+
+
+@pytest.mark.parametrize("M,K,N", [(256, 16384, 1024), (16, 16384, 4096)])
+def test_rmsnorm_default_splits_past_the_gamma_limit(gpu, M, K, N):
+    """With no config, K > 8192 takes a split register-staged fused config; output vs the oracle."""
+    import kernel_library as kl
+    from helpers import rms_check, rms_inputs
+    from oracle import rmsnorm as orms
+
+    cfg = kl.default_config("rmsnorm_matmul", M, N, K)
+    assert cfg.split_k > 1 and cfg.variant in (4, 11), cfg
+    d = rms_inputs(M, K, N, seed=45)
+    out = kl.rmsnorm_matmul(_dev(d["lhs"], gpu), _dev(d["rhs"], gpu), _dev(d["gamma"], gpu))
+    rep = rms_check(_host(out), orms.closed_form(d["lhs"], d["rhs"], d["gamma"]))
+    assert rep["ok"], (cfg.name, rep)
