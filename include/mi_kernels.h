@@ -105,7 +105,10 @@ int mi_cfg_check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K);
 int mi_num_configs(int kernel_id);
 int mi_get_config(int kernel_id, int idx, mi_tile_cfg* cfg);
 
-/* The library's default (tuned) config for a kernel at a shape. */
+/* The library's default config for a kernel at a shape: always prebuilt and
+ * legal there.  Generalised from the autotune winners: non-temporal variants
+ * for skinny M, split-K for few output tiles with a long K (and for the fused
+ * kernel past the K its gamma staging holds). */
 int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
 
 /* out[M,N] = lhsT[K,M]^T . rhs[K,N]; bf16 storage, fp32 accumulation over

@@ -64,19 +64,28 @@ def rocprof_command(out_dir: str, replay_path: str) -> list[str]:
 
 
 def parse_kernel_stats(stats_csv: str, match: str = "mi::") -> dict:
-    """The row of rocprofv3's kernel_stats.csv whose kernel name contains ``match``."""
+    """The rows of rocprofv3's kernel_stats.csv whose kernel name contains ``match``.
+
+    The longest-running one gives the top-level fields; ``kernels`` lists
+    every match (a split-K config launches its main kernel and a summing
+    kernel per call)."""
+    rows = []
     with open(stats_csv) as f:
         for row in csv.DictReader(f):
             if match in row["Name"]:
-                return {
+                rows.append({
                     "kernel": row["Name"],
                     "calls": int(row["Calls"]),
                     "avg_ns": float(row["AverageNs"]),
                     "min_ns": float(row["MinNs"]),
                     "max_ns": float(row["MaxNs"]),
                     "total_ns": float(row["TotalDurationNs"]),
-                }
-    raise ValueError(f"no kernel matching {match!r} in {stats_csv}")
+                })
+    if not rows:
+        raise ValueError(f"no kernel matching {match!r} in {stats_csv}")
+    main = dict(max(rows, key=lambda r: r["total_ns"]))
+    main["kernels"] = rows
+    return main
 
 
 def trace_kernel(variant_dir: str, replay_path: str, timeout_s: int = TRACE_TIMEOUT_S) -> dict:

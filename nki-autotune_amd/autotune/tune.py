@@ -182,7 +182,7 @@ def refine(func_name: str, M: int, N: int, K: int, configs, seed: int = 0, dists
 def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, cache_dir: str = "",
          check: bool = True, record: bool = False, warmup: int = 10, reps: int = 50, flush_bytes: int = 0,
          dists: dict | None = None, with_gamma: bool = True, allow_jit: bool = True,
-         finalists: int = 6, rounds: int = 5) -> TuneResult:
+         finalists: int = 6, rounds: int = 5, detailed: bool = False) -> TuneResult:
     """Sweep ``configs`` (default: every legal prebuilt config) at (M, N, K) and pick the fastest.
 
     The sweep is ``profile`` (the reference's selection is the min of its
@@ -191,7 +191,9 @@ def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, ca
     (``refine``), each from the library that holds it, and the winner is the
     fastest there.  ``record`` stores the fastest config that the prebuilt
     library holds (a just-in-time winner is noted beside it), since callers
-    of ``kernel_library`` only load that library.
+    of ``kernel_library`` only load that library.  ``detailed`` (with a
+    ``cache_dir``) keeps a rocprofv3 kernel trace of every successful config
+    in its folder.
     """
     import kernel_library as kl
     from kernel_library.config import TileConfig, record_tuned
@@ -200,7 +202,7 @@ def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, ca
     if configs is None:
         configs = kl.legal_configs(fam, M, N, K)
     jobs = make_jobs(fam, M, N, K, configs, dists, with_gamma)
-    output = profile(jobs, cache_dir, seed, "gfx950", False, warmup=warmup, reps=reps, flush_bytes=flush_bytes,
+    output = profile(jobs, cache_dir, seed, "gfx950", detailed, warmup=warmup, reps=reps, flush_bytes=flush_bytes,
                      allow_jit=allow_jit)
     best_row = output.best
     if best_row is None:
@@ -251,6 +253,9 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--flush-mib", type=int, default=0, help="L2/MALL flush buffer before each timed launch")
     ap.add_argument("--record", action="store_true", help="store the winner in kernel_library/tuned_configs.json")
     ap.add_argument("--baseline", action="store_true", help="also time torch.matmul (hipBLASLt) at the shape")
+    ap.add_argument("--configs", default="", help="comma-separated tile config names to time instead of a grid")
+    ap.add_argument("--detailed", action="store_true",
+                    help="with --cache: keep a rocprofv3 kernel trace of every successful config in its folder")
     args = ap.parse_args(argv)
 
     import kernel_library as kl
@@ -265,11 +270,15 @@ def main(argv: list[str] | None = None) -> int:
         from autotune.search import TileMDP, frontier_sample
 
         configs = frontier_sample(TileMDP(fam, M, N, K, args.prebuilt_only), args.num_kernels, args.seed)
+    if args.configs:
+        configs = [kl.TileConfig.from_name(n) for n in args.configs.split(",") if n]
+    if args.detailed and not args.cache:
+        ap.error("--detailed needs --cache (the traces are kept in the config folders)")
     if args.cache:
         shutil.rmtree(args.cache, ignore_errors=True)
         os.makedirs(args.cache, exist_ok=True)
     res = tune(fam, M, N, K, configs, args.seed, args.cache, True, args.record, args.warmup, args.reps,
-               args.flush_mib << 20)
+               args.flush_mib << 20, detailed=args.detailed)
     print(res.output)
     if res.best is not None:
         print(f"\n[tune] best {fam} {M}x{N}x{K}: {res.best.name} {res.best_time_s * 1e6:.1f} us "

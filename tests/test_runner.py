@@ -257,6 +257,11 @@ def test_detailed_profile_trace_helpers(tmp_path, monkeypatch):
                         '99.8,742629,1029515,52412.2\n')
     row = tr.parse_kernel_stats(str(csv_path))
     assert row["calls"] == 110 and row["avg_ns"] == 777977.4 and "pipe_kernel" in row["kernel"]
+    assert len(row["kernels"]) == 1
+    with open(csv_path, "a") as f:   # a split-K config: the main kernel and its summing kernel
+        f.write('"void mi::splitk_sum_kernel<0>(float const*)",110,1100000,10000.0,0.2,9000,12000,100.0\n')
+    row = tr.parse_kernel_stats(str(csv_path))
+    assert "pipe_kernel" in row["kernel"] and [r["calls"] for r in row["kernels"]] == [110, 110]
     monkeypatch.setattr(tr.shutil, "which", lambda name: None)
     assert "not found" in tr.trace_kernel(str(tmp_path / "k0"), path)["error"]
     assert replay_main([]) == 2
