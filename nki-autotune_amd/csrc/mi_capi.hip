@@ -1,9 +1,11 @@
 // mi_capi.hip -- the C ABI declared in include/mi_kernels.h.
 //
-// Stateless launchers over the instance table: look the config up, check
-// its static legality for the shape, launch on the caller's stream.  No
-// entry point allocates memory or throws; failures are return codes plus a
-// thread-local message (mi_last_error).
+// Launchers over the instance table: look the config up, check its static
+// legality for the shape, launch on the caller's stream.  The only state is
+// the instance table and, for split-K calls, a memory pool per device from
+// which each such call takes its workspace stream-ordered.  No entry point
+// throws; failures are return codes plus a thread-local message
+// (mi_last_error).
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
