@@ -265,3 +265,22 @@ def test_detailed_profile_trace_helpers(tmp_path, monkeypatch):
     monkeypatch.setattr(tr.shutil, "which", lambda name: None)
     assert "not found" in tr.trace_kernel(str(tmp_path / "k0"), path)["error"]
     assert replay_main([]) == 2
+
+
+def test_tune_cli_named_configs_and_detailed_needs_cache(monkeypatch):
+    """--configs names the configs to time (split_k included); --detailed without --cache is a usage error."""
+    from autotune import tune as tmod
+
+    seen = {}
+
+    def fake_tune(fam, M, N, K, configs, *a, **kw):
+        seen.update(fam=fam, shape=(M, N, K), configs=configs, detailed=kw.get("detailed"))
+        return tmod.TuneResult(None, None, "", None)
+
+    monkeypatch.setattr(tmod, "tune", fake_tune)
+    rc = tmod.main(["--kernel", "matmul_lhsT_rhs", "--shape", "512", "512", "32768", "--configs",
+                    "bm64_bn64_bk64_w4_s4_v1,bm64_bn64_bk64_w4_s4_v1_k4"])
+    assert rc == 1 and seen["shape"] == (512, 512, 32768) and seen["detailed"] is False
+    assert [c.split_k for c in seen["configs"]] == [1, 4]
+    with pytest.raises(SystemExit):
+        tmod.main(["--configs", "bm64_bn64_bk64_w4_s4_v1", "--detailed"])
