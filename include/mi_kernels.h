@@ -8,8 +8,9 @@
  * interface; the citation names it.  All pointers are device pointers owned
  * by the caller; tensors are row-major and contiguous.  bf16 tensors are
  * passed as raw 16-bit storage.  Launches are asynchronous on `stream`
- * (a hipStream_t, NULL = default stream).  No entry point allocates device
- * memory and no entry point throws.
+ * (a hipStream_t, NULL = default stream).  No entry point throws, and only
+ * a split-K call (tile config split_k > 1) allocates device memory: its
+ * workspace, stream-ordered from a library-owned pool (see split_k below).
  *
  * Return value: 0 on success; a positive MI_E_* legality code when the
  * request is rejected before launch; a negative value (-hipError_t) when the
