@@ -274,7 +274,8 @@ def test_tune_cli_named_configs_and_detailed_needs_cache(monkeypatch):
     seen = {}
 
     def fake_tune(fam, M, N, K, configs, *a, **kw):
-        seen.update(fam=fam, shape=(M, N, K), configs=configs, detailed=kw.get("detailed"))
+        seen.update(fam=fam, shape=(M, N, K), configs=configs, detailed=kw.get("detailed"),
+                    with_gamma=kw.get("with_gamma"))
         return tmod.TuneResult(None, None, "", None)
 
     monkeypatch.setattr(tmod, "tune", fake_tune)
@@ -284,3 +285,8 @@ def test_tune_cli_named_configs_and_detailed_needs_cache(monkeypatch):
     assert [c.split_k for c in seen["configs"]] == [1, 4]
     with pytest.raises(SystemExit):
         tmod.main(["--configs", "bm64_bn64_bk64_w4_s4_v1", "--detailed"])
+    # rmsnorm_matmul_online is the reference's no-gamma contract
+    tmod.main(["--kernel", "rmsnorm_matmul_online", "--shape", "256", "256", "512"])
+    assert seen["fam"] == "rmsnorm_matmul" and seen["with_gamma"] is False
+    tmod.main(["--kernel", "rmsnorm_matmul", "--shape", "256", "256", "512"])
+    assert seen["with_gamma"] is True
