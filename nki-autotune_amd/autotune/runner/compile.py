@@ -64,17 +64,12 @@ def _instance(fam: str, cfg) -> tuple[str, str, str] | None:
     if fam == "rmsnorm_matmul":
         if v in (0, 1):
             return "MI_RMS_INST", "MI_RMS_ROW", f"{base}, {s}, {v}"
-        if v in (2, 3):  # two LDS stages are part of the template
-            return ("MI_RMSR_INST", "MI_RMSR_ROW", f"{base}, {v - 2}") if s == 2 else None
         if v in (4, 5):
             return "MI_RMSX_INST", "MI_RMSX_ROW", f"{base}, {s}, {v - 2}"
         if v in (11, 12):
             return "MI_RMSXN_INST", "MI_RMSXN_ROW", f"{base}, {s}, {v - 9}"
-        if 6 <= v <= 9:
-            d, wmx = 2 + ((v - 6) & 1), (v - 6) >> 1
-            return "MI_RMSD_INST", "MI_RMSD_ROW", f"{base}, {s}, {wmx}, {d}, {v}"
-        if v == 10:
-            return "MI_RMSP_INST", "MI_RMSP_ROW", f"{base}, {s}"
+        if v == 13:
+            return "MI_RMS2_INST", "MI_RMS2_ROW", f"{base}, {s}"
     return None
 
 

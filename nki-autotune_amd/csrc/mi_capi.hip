@@ -2,11 +2,12 @@
 //
 // Launchers over the instance table: look the config up, check its static
 // legality for the shape, launch on the caller's stream.  The only state is
-// the instance table and, for split-K calls, a memory pool per device from
-// which each such call takes its workspace stream-ordered.  No entry point
-// throws; failures are return codes plus a thread-local message
-// (mi_last_error).
+// the instance table and, for calls that need device workspace (split-K,
+// the two-pass fused kernel), a memory pool per device from which each such
+// call takes its workspace stream-ordered.  No entry point throws; failures
+// are return codes plus a thread-local message (mi_last_error).
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <string.h>
 
@@ -60,24 +61,50 @@ const mi::MiEntry* find(int kernel_id, const mi_tile_cfg& cfg) {
   return nullptr;
 }
 
-// Host restatement of mi::WaveGrid: can `waves` waves split a BM x BN block
-// into per-wave blocks that are whole 32x32 MFMA tiles?
-bool wave_grid_ok(int bm, int bn, int waves) {
-  for (int wm = 1; wm <= waves; wm *= 2) {
-    const int wn = waves / wm;
-    if (wm * wn != waves || bm % wm || bn % wn) continue;
-    const int tm = bm / wm, tn = bn / wn;
-    if (tm >= 32 && tn >= 32 && tm % 32 == 0 && tn % 32 == 0) return true;
+constexpr unsigned long long kMaxOffset = 0xFFFFFFFFull;        // 32-bit buffer offsets
+constexpr int kMaxSplit = 16;                                    // split-K parts
+constexpr unsigned long long kMaxWorkspace = 1ull << 31;         // bytes of device workspace per call
+
+// The template rules of the variant `c` names (mi_legal.hpp: the same
+// predicates the kernel templates assert when they are instantiated).
+mi::Legal template_legal(int kernel_id, const mi_tile_cfg& c) {
+  const int bm = c.block_m, bn = c.block_n, bk = c.block_k, w = c.waves, s = c.lds_stages;
+  switch (kernel_id) {
+    case MI_KERNEL_MATMUL_LHST_RHS_BF16:
+      if (c.variant == 0) return mi::legal_mm_plain(bm, bn, bk, w, s);
+      if (c.variant == 1 || c.variant == 3) return mi::legal_mm_pipe(bm, bn, bk, w, s, false);
+      if (c.variant == 2) return mi::legal_mm_reg(bm, bn, bk, w, s);
+      break;
+    case MI_KERNEL_MATMUL_LHS_RHS_BF16:
+      if (c.variant == 0 || c.variant == 2) return mi::legal_mm_pipe(bm, bn, bk, w, s, true);
+      if (c.variant == 1) return mi::legal_lhs_pair(bm, bn, bk, w, s);
+      break;
+    case MI_KERNEL_RMSNORM_MATMUL_BF16:
+      if (c.variant == 0 || c.variant == 1) return mi::legal_rms_plain(bm, bn, bk, w, s);
+      if (c.variant == 4 || c.variant == 5) return mi::legal_rms_xreg(bm, bn, bk, w, s, c.variant - 2);
+      if (c.variant == 11 || c.variant == 12) return mi::legal_rms_xreg(bm, bn, bk, w, s, c.variant - 9);
+      if (c.variant == 13) return mi::legal_mm_pipe(bm, bn, bk, w, s, false);
+      break;
+    case MI_KERNEL_MATMUL_LHST_RHS_F32:
+      // 16 x 16 threads with 4 x 4 outputs each, K slices of 16 or 32.
+      if (c.variant == 0) {
+        if (bm != 64 || bn != 64 || (bk != 16 && bk != 32) || w != 4 || s != 1)
+          return mi::bad(MI_E_TILE, "the fp32 kernel takes 64x64 blocks, block_k 16 or 32, 4 waves, 1 stage");
+        return mi::ok();
+      }
+      break;
+    default:
+      break;
   }
-  return false;
+  return mi::bad(MI_E_TILE, "no such variant of this kernel");
 }
 
-bool pow2_in(int v, int lo, int hi) { return v >= lo && v <= hi && (v & (v - 1)) == 0; }
-
-constexpr unsigned long long kMaxOffset = 0xFFFFFFFFull;  // 32-bit buffer offsets
-constexpr int kLdsLimit = 160 * 1024;
-constexpr int kMaxSplit = 16;                                  // split-K parts
-constexpr unsigned long long kMaxSplitWorkspace = 1ull << 31;  // bytes of fp32 partial products
+bool splittable(int kernel_id, int variant) {
+  return (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (variant == 1 || variant == 3)) ||
+         (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 && (variant == 0 || variant == 2)) ||
+         (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 &&
+          (variant == 4 || variant == 5 || variant == 11 || variant == 12 || variant == 13));
+}
 
 int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::MiEntry** out) {
   if (kernel_id < 0 || kernel_id >= MI_NUM_KERNELS) return fail(MI_E_KERNEL, "unknown kernel id %d", kernel_id);
@@ -89,98 +116,57 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
   if (c.split_k < 1 || c.split_k > kMaxSplit)
     return fail(MI_E_SPLIT, "split_k=%d outside [1, %d]", c.split_k, kMaxSplit);
   if (c.split_k > 1) {
-    // Split-K: the pipelined matmul body only (lhsT variants 1 and 3,
-    // matmul_lhs_rhs variants 0 and 2), and every part must get at least
-    // one K tile.
-    const bool ok = (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (c.variant == 1 || c.variant == 3)) ||
-                    (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 && (c.variant == 0 || c.variant == 2)) ||
-                    (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 &&
-                     (c.variant == 4 || c.variant == 5 || c.variant == 11 || c.variant == 12));
-    if (!ok)
+    if (!splittable(kernel_id, c.variant))
       return fail(MI_E_SPLIT,
-                  "split_k=%d needs the pipelined matmul (lhsT.rhs variants 1, 3; lhs.rhs variants 0, 2) or "
-                  "the register-staged fused kernel (rmsnorm_matmul variants 4, 5, 11, 12)",
+                  "split_k=%d needs the pipelined matmul (lhsT.rhs variants 1, 3; lhs.rhs variants 0, 2) or a "
+                  "register-staged or two-pass fused kernel (rmsnorm_matmul variants 4, 5, 11, 12, 13)",
                   c.split_k);
+    // Every part must get at least one K tile.
     const long long kt = ((long long)K + c.block_k - 1) / c.block_k;
     const long long kts = (kt + c.split_k - 1) / c.split_k;
     if ((long long)(c.split_k - 1) * kts >= kt)
       return fail(MI_E_SPLIT, "split_k=%d leaves a K part empty at K=%d, block_k=%d", c.split_k, K, c.block_k);
-    const unsigned long long ws = (unsigned long long)c.split_k *
-                                  ((unsigned long long)M * (unsigned long long)N + (unsigned long long)M) * 4ull;
-    if (ws > kMaxSplitWorkspace)
-      return fail(MI_E_RANGE, "split-K workspace of %llu bytes exceeds %llu", ws, kMaxSplitWorkspace);
   }
   if (c.group_m < 0) return fail(MI_E_ARGS, "group_m=%d negative", c.group_m);
-  if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_F32) {
-    // LDS panels are copied in 1 KiB wave loads and XOR-swizzled in 16-byte
-    // chunks: block_m / block_n must be powers of two in [32, 512] and
-    // block_k a power of two in [16, 128] ([32, 128] for the fused kernel,
-    // whose x rows are reduced over BK/8 lanes).
-    // The pipelined matmuls (lhsT variants 1 and 3, every matmul_lhs_rhs
-    // variant) double-buffer MFMA operands across K sub-steps of 16, need an
-    // even number of them, and keep a ring of 2..4 LDS stages; the paired
-    // K-contiguous loads (matmul_lhs_rhs variant 1) take block_k 32 or 64.
-    const bool pipelined = kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 ||
-                           (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (c.variant == 1 || c.variant == 3));
-    const int kmin = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 || pipelined ? 32 : 16;
-    const int kmax = kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 && c.variant == 1 ? 64 : 128;
-    if (!pow2_in(c.block_m, 32, 512) || !pow2_in(c.block_n, 32, 512) || !pow2_in(c.block_k, kmin, kmax))
-      return fail(MI_E_TILE, "block sizes bm=%d bn=%d bk=%d outside the template range", c.block_m, c.block_n,
-                  c.block_k);
-    if (pipelined && (c.lds_stages < 2 || c.lds_stages > 4))
-      return fail(MI_E_TILE, "the pipelined kernels take 2..4 LDS stages, not %d", c.lds_stages);
-  }
-  if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_F32 && !wave_grid_ok(c.block_m, c.block_n, c.waves))
-    return fail(MI_E_WAVE_TILE, "%d waves cannot tile a %dx%d block in 32x32 MFMA tiles", c.waves, c.block_m,
-                c.block_n);
-  // Matmul variant 2 keeps its K-tile ring in registers (lds_stages = ring
-  // depth, 1..8) and two LDS stages.
-  const bool reg_ring = kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && c.variant == 2;
-  if (reg_ring && c.lds_stages > 8) return fail(MI_E_ARGS, "register ring depth %d > 8", c.lds_stages);
-  const long long lds = (long long)(reg_ring ? 2 : c.lds_stages) * (c.block_m + c.block_n) * c.block_k *
-                        (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_F32 ? 4 : 2);
-  if (lds > kLdsLimit) return fail(MI_E_LDS, "LDS %lld bytes > %d", lds, kLdsLimit);
+  const mi::Legal lg = template_legal(kernel_id, c);
+  if (lg.code != MI_OK)
+    return fail(lg.code, "kernel %d variant %d bm=%d bn=%d bk=%d waves=%d stages=%d: %s", kernel_id, c.variant,
+                c.block_m, c.block_n, c.block_k, c.waves, c.lds_stages, lg.why);
+  const size_t ws = mi::workspace_bytes(kernel_id, c, M, N, K);
+  if (ws > kMaxWorkspace) return fail(MI_E_RANGE, "device workspace of %zu bytes exceeds %llu", ws, kMaxWorkspace);
   const mi::MiEntry* e = find(kernel_id, c);
   if (!e)
     return fail(MI_E_NO_INSTANCE, "no compiled instance for kernel %d bm=%d bn=%d bk=%d waves=%d stages=%d variant=%d",
                 kernel_id, c.block_m, c.block_n, c.block_k, c.waves, c.lds_stages, c.variant);
-  if (e->lds_bytes > kLdsLimit) return fail(MI_E_LDS, "instance LDS %d bytes > %d", e->lds_bytes, kLdsLimit);
+  if (e->lds_bytes > mi::kLdsBytesMax)
+    return fail(MI_E_LDS, "instance LDS %d bytes > %d", e->lds_bytes, mi::kLdsBytesMax);
   if (kernel_id != MI_KERNEL_MATMUL_LHST_RHS_F32) {
     if (M % 8 || N % 8) return fail(MI_E_ALIGN, "M=%d and N=%d must be multiples of 8", M, N);
     const bool k_rows = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 || kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16;
     if (k_rows && K % 8)
       return fail(MI_E_ALIGN, "K=%d must be a multiple of 8 (16-byte rows of the K-contiguous operand)", K);
-    // Loads run up to one tile (the ring depth, for variant 2) past K.
+    // Loads run up to one tile (the ring depth, for matmul variant 2) past K.
+    const bool reg_ring = kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && c.variant == 2;
     const unsigned long long kpad =
         (unsigned long long)K + (unsigned long long)c.block_k * (unsigned long long)(reg_ring ? c.lds_stages + 1 : 1);
     const unsigned long long mpad = (unsigned long long)M + (unsigned long long)c.block_m;
-    unsigned long long a_span, b_span;
-    if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16) {
-      a_span = kpad * (unsigned long long)M * 2ull;
-    } else {
-      // K-contiguous A (x of the fused kernels, lhs of matmul_lhs_rhs): loads
-      // run up to 8 tiles past K on the last rows.
-      a_span = (mpad * (unsigned long long)K + 8ull * (unsigned long long)c.block_k) * 2ull;
-    }
-    b_span = kpad * (unsigned long long)N * 2ull;
+    // The A operand is MN-contiguous for lhsT.rhs and for the main pass of
+    // the two-pass fused kernel (its packed xt[K][M]), K-contiguous
+    // otherwise (x, lhs: loads run up to 8 tiles past K on the last rows).
+    const bool a_mn = kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 ||
+                      (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 && c.variant == 13);
+    const unsigned long long a_span = a_mn ? kpad * (unsigned long long)M * 2ull
+                                           : (mpad * (unsigned long long)K + 8ull * (unsigned long long)c.block_k) * 2ull;
+    const unsigned long long b_span = kpad * (unsigned long long)N * 2ull;
     if (a_span > kMaxOffset || b_span > kMaxOffset)
       return fail(MI_E_RANGE, "operand spans exceed 32-bit buffer offsets (%llu, %llu bytes)", a_span, b_span);
-    // rmsnorm_matmul variants 4..12 stage gamma in LDS: K rounded up to the
-    // K step the kernel walks (variants 4/5/11/12: one tile; 6..9: D = 2 or
-    // 3 tiles; 10: rounds of 4 tiles) must fit the instance's gamma entries.
-    // The limit holds with or without gamma (legality is gamma-agnostic).
-    // With split_k > 1 (one-tile variants only) each part stages the gamma of
-    // its own K range: ceil(ceil(K/block_k)/split_k) tiles.
+    // The register-staged fused variants stage gamma in LDS (one K tile at a
+    // time, K rounded up to it); with split_k > 1 each part stages the gamma
+    // of its own K range: ceil(ceil(K/block_k)/split_k) tiles.  The limit
+    // holds with or without gamma (legality is gamma-agnostic).
     if (e->gamma_kmax > 0) {
-      const int d = c.variant == 10                      ? 4
-                    : c.variant >= 6 && c.variant <= 9 ? 2 + ((c.variant - 6) & 1)
-                                                       : 1;
-      const long long span = (long long)d * c.block_k;
-      long long need = ((long long)K + span - 1) / span * span;
-      if (c.split_k > 1) {
-        const long long kt = ((long long)K + c.block_k - 1) / c.block_k;
-        need = (kt + c.split_k - 1) / c.split_k * c.block_k;
-      }
+      const long long kt = ((long long)K + c.block_k - 1) / c.block_k;
+      const long long need = (kt + c.split_k - 1) / c.split_k * c.block_k;
       if (need > e->gamma_kmax)
         return fail(MI_E_RANGE, "K=%d (%lld per part) exceeds the %d gamma entries variant %d stages in LDS", K,
                     need, e->gamma_kmax, c.variant);
@@ -254,7 +240,7 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
       for (int p = 2; p <= 16 && !parts; p *= 2) {
         const long long kts = (kt + p - 1) / p;
         const unsigned long long ws = (unsigned long long)p * ((unsigned long long)M * N + M) * 4ull;
-        if (kts * 64 <= 8192 && (long long)(p - 1) * kts < kt && ws <= kMaxSplitWorkspace) parts = p;
+        if (kts * 64 <= 8192 && (long long)(p - 1) * kts < kt && ws <= kMaxWorkspace) parts = p;
       }
       if (!parts) c = M <= 128 ? mi_tile_cfg{64, 128, 64, 4, 2, 1, 8, 0} : mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0};
       else if (M <= 128) c = {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, parts, 8, 11};
@@ -269,16 +255,19 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
   return MI_OK;
 }
 
-// Split-K workspace: allocated per call, stream-ordered
-// (hipMallocFromPoolAsync / hipFreeAsync), from a memory pool the library
-// keeps per device with no release threshold, so that after the first calls
-// the pool hands back cached memory.  Each call has its own buffer (calls on
-// different streams do not share one), and a call under HIP graph capture
-// becomes allocation and free nodes of the graph.
+// Device workspace (split-K partial products, the two-pass fused kernel's
+// packed operand): allocated per call, stream-ordered (hipMallocFromPoolAsync
+// / hipFreeAsync), from a memory pool the library keeps per device.  The
+// pool keeps at most kPoolKeepBytes of freed memory cached for the next
+// calls and returns the rest to the device at the next synchronisation.
+// Each call has its own buffer (calls on different streams do not share
+// one), and a call under HIP graph capture becomes allocation and free
+// nodes of the graph.
+constexpr uint64_t kPoolKeepBytes = 256ull << 20;
 std::mutex g_pool_mu;
 std::map<int, hipMemPool_t> g_pools;
 
-int split_pool(hipMemPool_t* out) {
+int workspace_pool(hipMemPool_t* out) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
@@ -291,45 +280,56 @@ int split_pool(hipMemPool_t* out) {
     props.location.type = hipMemLocationTypeDevice;
     props.location.id = dev;
     hipMemPool_t pool = nullptr;
-    if ((e = hipMemPoolCreate(&pool, &props)) != hipSuccess) return hip_fail(e, "split-K memory pool");
-    uint64_t keep = ~0ull;
+    if ((e = hipMemPoolCreate(&pool, &props)) != hipSuccess) return hip_fail(e, "workspace memory pool");
+    uint64_t keep = kPoolKeepBytes;
     if ((e = hipMemPoolSetAttribute(pool, hipMemPoolAttrReleaseThreshold, &keep)) != hipSuccess)
-      return hip_fail(e, "split-K memory pool threshold");
+      return hip_fail(e, "workspace memory pool threshold");
     it = g_pools.emplace(dev, pool).first;
   }
   *out = it->second;
   return MI_OK;
 }
 
-int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, void* stream) {
-  mi_tile_cfg cfg;
-  if (cfg_in) cfg = *cfg_in;
-  else pick_default(kernel_id, args_in.M, args_in.N, args_in.K, &cfg);
-  const mi::MiEntry* e = nullptr;
-  const int rc = check(kernel_id, &cfg, args_in.M, args_in.N, args_in.K, &e);
-  if (rc != MI_OK) return rc;
+// Resolves the config (cfg == NULL: the library default) and checks it.
+int resolve(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& a, mi_tile_cfg* cfg,
+            const mi::MiEntry** e) {
+  if (cfg_in) *cfg = *cfg_in;
+  else pick_default(kernel_id, a.M, a.N, a.K, cfg);
+  return check(kernel_id, cfg, a.M, a.N, a.K, e);
+}
+
+int launch(const mi::MiEntry* e, const mi_tile_cfg& cfg, const mi::MiArgs& args_in, char* ws, void* stream) {
   mi::MiArgs a = args_in;
   a.group_m = cfg.group_m > 0 ? cfg.group_m : 8;
-  if (cfg.split_k > 1) {
-    hipMemPool_t pool = nullptr;
-    const int prc = split_pool(&pool);
-    if (prc != MI_OK) return prc;
-    // Products [parts][M][N]; the fused kernel adds its rows' sums of squares [parts][M].
-    const size_t rows = kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 ? (size_t)a.M : 0;
-    const size_t ws_bytes = (size_t)cfg.split_k * ((size_t)a.M * (size_t)a.N + rows) * 4u;
-    hipError_t ae = hipMallocFromPoolAsync((void**)&a.ws, ws_bytes, pool, (hipStream_t)stream);
-    if (ae != hipSuccess) return hip_fail(ae, "split-K workspace alloc");
-    a.parts = cfg.split_k;
-    const hipError_t le = e->launch(a, (hipStream_t)stream);
-    const hipError_t fe = hipFreeAsync(a.ws, (hipStream_t)stream);
-    if (le != hipSuccess) return hip_fail(le, "kernel launch");
-    if (fe != hipSuccess) return hip_fail(fe, "split-K workspace free");
-    return MI_OK;
-  }
+  a.parts = cfg.split_k;
+  a.ws = ws;
   const hipError_t err = e->launch(a, (hipStream_t)stream);
-  if (err != hipSuccess) return hip_fail(err, "kernel launch");
+  return err == hipSuccess ? MI_OK : hip_fail(err, "kernel launch");
+}
+
+int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, void* stream) {
+  mi_tile_cfg cfg;
+  const mi::MiEntry* e = nullptr;
+  const int rc = resolve(kernel_id, cfg_in, args_in, &cfg, &e);
+  if (rc != MI_OK) return rc;
+  const size_t ws_bytes = mi::workspace_bytes(kernel_id, cfg, args_in.M, args_in.N, args_in.K);
+  if (ws_bytes == 0) return launch(e, cfg, args_in, nullptr, stream);
+  hipMemPool_t pool = nullptr;
+  const int prc = workspace_pool(&pool);
+  if (prc != MI_OK) return prc;
+  char* ws = nullptr;
+  const hipError_t ae = hipMallocFromPoolAsync((void**)&ws, ws_bytes, pool, (hipStream_t)stream);
+  if (ae != hipSuccess) return hip_fail(ae, "workspace alloc");
+  const int lrc = launch(e, cfg, args_in, ws, stream);
+  const hipError_t fe = hipFreeAsync(ws, (hipStream_t)stream);
+  if (lrc != MI_OK) return lrc;
+  if (fe != hipSuccess) return hip_fail(fe, "workspace free");
   return MI_OK;
 }
+
+// Device pointers are read and written in 16-byte vectors (bf16 kernels)
+// or as fp32 elements (the fp32 kernel).
+bool misaligned(const void* p, uintptr_t align) { return p && ((uintptr_t)p & (align - 1)) != 0; }
 
 }  // namespace
 
@@ -374,6 +374,8 @@ int mi_matmul_lhsT_rhs_bf16(const void* lhsT, const void* rhs, void* out, int M,
     return zero_output<uint16_t>(out, (size_t)M * N, stream);
   }
   if (!lhsT || !rhs) return fail(MI_E_ARGS, "null input pointer");
+  if (misaligned(lhsT, 16) || misaligned(rhs, 16) || misaligned(out, 16))
+    return fail(MI_E_ALIGN, "lhsT, rhs and out must be 16-byte aligned");
   mi::MiArgs a = {lhsT, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
   return run(MI_KERNEL_MATMUL_LHST_RHS_BF16, cfg, a, stream);
 }
@@ -387,6 +389,8 @@ int mi_matmul_lhs_rhs_bf16(const void* lhs, const void* rhs, void* out, int M, i
     return zero_output<uint16_t>(out, (size_t)M * N, stream);
   }
   if (!lhs || !rhs) return fail(MI_E_ARGS, "null input pointer");
+  if (misaligned(lhs, 16) || misaligned(rhs, 16) || misaligned(out, 16))
+    return fail(MI_E_ALIGN, "lhs, rhs and out must be 16-byte aligned");
   mi::MiArgs a = {lhs, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
   return run(MI_KERNEL_MATMUL_LHS_RHS_BF16, cfg, a, stream);
 }
@@ -400,6 +404,8 @@ int mi_matmul_lhsT_rhs_f32(const float* lhsT, const float* rhs, float* out, int 
     return zero_output<float>(out, (size_t)M * N, stream);
   }
   if (!lhsT || !rhs) return fail(MI_E_ARGS, "null input pointer");
+  if (misaligned(lhsT, 4) || misaligned(rhs, 4) || misaligned(out, 4))
+    return fail(MI_E_ALIGN, "lhsT, rhs and out must be 4-byte aligned");
   mi::MiArgs a = {lhsT, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
   return run(MI_KERNEL_MATMUL_LHST_RHS_F32, cfg, a, stream);
 }
@@ -410,6 +416,8 @@ int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void
   if (!(eps >= 0.0f) || eps > 3.0e38f) return fail(MI_E_ARGS, "eps must be finite and >= 0");
   if (M == 0 || N == 0) return MI_OK;
   if (!x || !W || !out) return fail(MI_E_ARGS, "null pointer");
+  if (misaligned(x, 16) || misaligned(gamma, 16) || misaligned(W, 16) || misaligned(out, 16))
+    return fail(MI_E_ALIGN, "x, gamma, W and out must be 16-byte aligned");
   mi::MiArgs a = {x, W, gamma, out, M, N, K, eps, 1.0f / (float)K, 8};
   return run(MI_KERNEL_RMSNORM_MATMUL_BF16, cfg, a, stream);
 }

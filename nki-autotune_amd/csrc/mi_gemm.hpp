@@ -28,6 +28,8 @@
 #include <type_traits>
 #include <utility>
 
+#include "mi_legal.hpp"
+
 namespace mi {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -157,6 +159,15 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_
 struct SplitK {
   int parts;          // 1: no split
   float* ws;          // fp32 partial products, [parts][M][N]
+};
+
+// Epilogue row scale of the two-pass fused kernel: output row m is
+// multiplied by 1/sqrt(sum_p ssq[p][m] * inv_k + eps), the partial sums of
+// squares taken in part order.
+struct RowScale {
+  const float* ssq;   // [parts][M]
+  int parts;
+  float inv_k, eps;
 };
 
 __device__ __forceinline__ void tile_coords_split(int tiles_m, int tiles_n, int group_m, int parts, int& tm, int& tn,
@@ -404,6 +415,8 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_kernel(const uint
                                                                      int K, int group_m) {
   using C = MatmulCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
+  static_assert(legal_mm_plain(BM, BN, BK, WAVES, STAGES).code == MI_OK, "illegal tile config (mi_legal.hpp)");
+  static_assert(C::LDS_BYTES == lds_mm_plain(BM, BN, BK, WAVES, STAGES), "host LDS budget out of step");
   static_assert(G::ok, "illegal wave grid");
   static_assert(BK % 16 == 0, "BK must be a multiple of 16");
   constexpr int TM = G::TM, TN = G::TN;
@@ -604,12 +617,16 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict
   }
 }
 
-template <int BM, int BN, int BK, int WAVES, int STAGES, bool AK, bool NTB = false, bool SPLIT = false>
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool AK, bool NTB = false, bool SPLIT = false,
+          bool RS = false>
 __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, const uint16_t* __restrict__ rhs,
                                              uint16_t* __restrict__ out, int M, int N, int K, int group_m,
-                                             char* smem, const SplitK sk = SplitK{1, nullptr}) {
+                                             char* smem, const SplitK sk = SplitK{1, nullptr},
+                                             const RowScale rsc = RowScale{nullptr, 0, 0.0f, 0.0f}) {
   using C = PipeCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
+  static_assert(legal_mm_pipe(BM, BN, BK, WAVES, STAGES, AK).code == MI_OK, "illegal tile config (mi_legal.hpp)");
+  static_assert(C::LDS_BYTES == lds_mm_pipe(BM, BN, BK, WAVES, STAGES), "host LDS budget out of step");
   static_assert(G::ok, "illegal wave grid");
   static_assert(BK % 32 == 0, "BK must be a multiple of 32 (even number of MFMA K steps)");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
@@ -770,6 +787,25 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
     return true;
   });
   const int cur = (KT - 1) % STAGES;
+  // Row scale (two-pass fused kernel): lane l scales row l%32 of each of its
+  // 32-row fragments by 1/sqrt(sum_p ssq[p][m] * inv_k + eps), p in order.
+  // The first RSB partial sums of its rows are loaded here, so that they fly
+  // during the last tile's MFMAs (no load is issued after them, so the
+  // compiler's wait for them is the final vmcnt(0) below); further ones are
+  // loaded RSB at a time in the epilogue.
+  constexpr int RSB = 8;
+  float rsum[TM];
+  float rpart[RS ? TM : 1][RS ? RSB : 1];
+  auto load_parts = [&](int p0) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int m = m0 + wm0 + i * 32 + (lane & 31);
+#pragma unroll
+      for (int q = 0; q < RSB; ++q)
+        rpart[i][q] = (m < M && p0 + q < rsc.parts) ? rsc.ssq[(size_t)(p0 + q) * (size_t)M + m] : 0.0f;
+    }
+  };
+  if constexpr (RS && !SPLIT) load_parts(0);
   // Last tile: no further loads.
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {
@@ -784,10 +820,24 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
     store_partial<TM, TN>(acc, sk.ws + (size_t)part * (size_t)M * (size_t)N, lane, M, N, m0 + wm0, n0 + wn0);
     return;
   }
-  float one[TM];
+  float scale[TM];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) one[i] = 1.0f;
-  store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
+  for (int i = 0; i < TM; ++i) scale[i] = 1.0f;
+  if constexpr (RS) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) rsum[i] = 0.0f;
+    for (int p0 = 0;; p0 += RSB) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int q = 0; q < RSB; ++q) rsum[i] += rpart[i][q];
+      if (p0 + RSB >= rsc.parts) break;
+      load_parts(p0 + RSB);
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i) scale[i] = 1.0f / __builtin_sqrtf(rsum[i] * rsc.inv_k + rsc.eps);
+  }
+  store_tile<TM, TN, WAVES>(acc, scale, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
 }
 
 // NTB: rhs loaded with the non-temporal cache policy (matmul variant 3, for
@@ -917,6 +967,8 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_kernel(
     uint16_t* __restrict__ out, int M, int N, int K, float inv_k, float eps, int group_m) {
   using C = RmsCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
+  static_assert(legal_rms_plain(BM, BN, BK, WAVES, STAGES).code == MI_OK, "illegal tile config (mi_legal.hpp)");
+  static_assert(C::LDS_BYTES == lds_rms_plain(BM, BN, BK, WAVES, STAGES), "host LDS budget out of step");
   static_assert(G::ok, "illegal wave grid");
   static_assert(BK % 16 == 0, "BK must be a multiple of 16");
   constexpr int TM = G::TM, TN = G::TN, KC = C::KC, CPT = C::CPT, NT = C::NT;

@@ -58,6 +58,8 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pair_kernel(const 
                                                                          int K, int group_m) {
   using C = PairCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
+  static_assert(legal_lhs_pair(BM, BN, BK, WAVES, STAGES).code == MI_OK, "illegal tile config (mi_legal.hpp)");
+  static_assert(C::LDS_BYTES == lds_lhs_pair(BM, BN, BK, WAVES, STAGES), "host LDS budget out of step");
   static_assert(G::ok, "illegal wave grid");
   static_assert(BK % 32 == 0 && BK <= 64, "BK of 32 or 64 (pairs of 64 or 128 columns)");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages for B");

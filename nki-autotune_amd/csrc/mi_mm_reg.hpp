@@ -50,6 +50,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_reg_kernel(const 
                                                                          uint16_t* __restrict__ out, int M, int N,
                                                                          int K, int group_m) {
   using G = WaveGrid<BM, BN, WAVES>;
+  static_assert(legal_mm_reg(BM, BN, BK, WAVES, PF).code == MI_OK, "illegal tile config (mi_legal.hpp)");
   static_assert(G::ok, "illegal wave grid");
   static_assert(BK % 32 == 0, "BK must be a multiple of 32");
   static_assert(PF >= 1 && PF <= 8, "1..8 tiles in the register ring");
@@ -57,6 +58,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_reg_kernel(const 
   constexpr int A_BYTES = BK * BM * 2, B_BYTES = BK * BN * 2, STAGE = A_BYTES + B_BYTES;
   constexpr int EPI = WAVES * 32 * (G::WTN * 2 + 16);
   constexpr int LDS = 2 * STAGE > EPI ? 2 * STAGE : EPI;
+  static_assert(LDS == lds_mm_reg(BM, BN, BK, WAVES), "host LDS budget out of step");
   using PA = RegPanel<BK, BM, NT>;
   using PB = RegPanel<BK, BN, NT>;
   __shared__ __attribute__((aligned(1024))) char smem[LDS];

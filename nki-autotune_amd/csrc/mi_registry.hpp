@@ -10,25 +10,24 @@
 
 #include "../../include/mi_kernels.h"
 #include "mi_gemm.hpp"
-#include "mi_rms_ring.hpp"
-#include "mi_mm_reg.hpp"
-#include "mi_rms_xreg.hpp"
-#include "mi_rms_direct.hpp"
-#include "mi_rms_xpair.hpp"
+#include "mi_legal.hpp"
 #include "mi_mm_lhs_pair.hpp"
+#include "mi_mm_reg.hpp"
+#include "mi_rms_2pass.hpp"
+#include "mi_rms_xreg.hpp"
 
 namespace mi {
 
 struct MiArgs {
-  const void* a;      // lhsT / x
+  const void* a;      // lhsT / lhs / x
   const void* b;      // rhs / W
   const void* g;      // gamma (fused kernel, may be null)
   void* out;
   int M, N, K;
   float eps, inv_k;
   int group_m;
-  int parts = 1;             // split-K parts (pipelined lhsT matmul only)
-  float* ws = nullptr;       // split-K workspace: fp32 partial products [parts][M][N]
+  int parts = 1;          // split-K parts
+  char* ws = nullptr;     // workspace of workspace_bytes() bytes (256-byte aligned), or null if none is needed
 };
 
 typedef hipError_t (*LaunchFn)(const MiArgs&, hipStream_t);
@@ -43,6 +42,22 @@ struct MiEntry {
 
 inline int grid_tiles(int M, int N, int BM, int BN) { return ((M + BM - 1) / BM) * ((N + BN - 1) / BN); }
 
+inline size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+// Device workspace a launch needs, in bytes (0: none).
+//   split-K matmul:                 fp32 products [parts][M][N]
+//   split-K fused (variants 4..12): products, then row sums of squares [parts][M]
+//   two-pass fused (variant 13):    xt [K][M] bf16, ssq [ceil(K/512)][M] fp32,
+//                                   then (split) products [parts][M][N]
+inline size_t workspace_bytes(int kernel_id, const mi_tile_cfg& c, int M, int N, int K) {
+  const size_t m = (size_t)M, n = (size_t)N, k = (size_t)K, p = (size_t)(c.split_k > 1 ? c.split_k : 0);
+  if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 && c.variant == 13)
+    return align256(k * m * 2) + align256((size_t)rms2_parts(K) * m * 4) + p * m * n * 4;
+  if (p == 0) return 0;
+  if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16) return p * (m * n + m) * 4;
+  return p * m * n * 4;
+}
+
 template <int BM, int BN, int BK, int W, int S>
 hipError_t launch_mm_bf16(const MiArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((mm_lhsT_rhs_bf16_kernel<BM, BN, BK, W, S>), dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64),
@@ -51,11 +66,19 @@ hipError_t launch_mm_bf16(const MiArgs& a, hipStream_t s) {
 }
 
 // Split-K second pass: out = bf16(sum over the parts of ws), in part order.
-inline void launch_splitk_sum(const MiArgs& a, hipStream_t s) {
-  const size_t n = (size_t)a.M * (size_t)a.N;
+inline void launch_splitk_sum(const float* ws, uint16_t* out, size_t n, int parts, hipStream_t s) {
   const size_t blocks = (n / 8 + 255) / 256;
-  hipLaunchKernelGGL(splitk_sum_kernel<0>, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s,
-                     (const float*)a.ws, (uint16_t*)a.out, n, a.parts);
+  hipLaunchKernelGGL(splitk_sum_kernel<0>, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s, ws, out,
+                     n, parts);
+}
+
+// Split-K second pass of the fused kernels: products and sums of squares in
+// part order, then 1/rms and the bf16 rounding.
+inline void launch_splitk_rms_sum(const float* prod, int parts, const float* ssq, int ssq_parts, const MiArgs& a,
+                                  hipStream_t s) {
+  const size_t blocks = ((size_t)a.M * (size_t)a.N / 8 + 255) / 256;
+  hipLaunchKernelGGL(splitk_rms_sum_kernel<0>, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s,
+                     prod, (uint16_t*)a.out, a.M, a.N, parts, ssq, ssq_parts, a.inv_k, a.eps);
 }
 
 template <int BM, int BN, int BK, int W, int S, bool NTB = false>
@@ -64,10 +87,10 @@ hipError_t launch_mm_pipe(const MiArgs& a, hipStream_t s) {
     // Split-K: the parts' fp32 products into ws, then their sum into out.
     hipLaunchKernelGGL((mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, true>),
                        dim3(grid_tiles(a.M, a.N, BM, BN) * a.parts), dim3(W * 64), 0, s, (const uint16_t*)a.a,
-                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, a.ws);
+                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, (float*)a.ws);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_splitk_sum(a, s);
+    launch_splitk_sum((const float*)a.ws, (uint16_t*)a.out, (size_t)a.M * (size_t)a.N, a.parts, s);
   } else {
     hipLaunchKernelGGL((mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, false>),
                        dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
@@ -81,10 +104,10 @@ hipError_t launch_mm_lhs(const MiArgs& a, hipStream_t s) {
   if (a.parts > 1) {
     hipLaunchKernelGGL((mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, true>),
                        dim3(grid_tiles(a.M, a.N, BM, BN) * a.parts), dim3(W * 64), 0, s, (const uint16_t*)a.a,
-                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, a.ws);
+                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, (float*)a.ws);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_splitk_sum(a, s);
+    launch_splitk_sum((const float*)a.ws, (uint16_t*)a.out, (size_t)a.M * (size_t)a.N, a.parts, s);
   } else {
     hipLaunchKernelGGL((mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, false>),
                        dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
@@ -117,25 +140,12 @@ hipError_t launch_mm_reg(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int W, bool PRE>
-hipError_t launch_rms_ring(const MiArgs& a, hipStream_t s) {
-  if (a.g)
-    hipLaunchKernelGGL((rmsnorm_mm_bf16_ring_kernel<BM, BN, BK, W, PRE, true>), dim3(grid_tiles(a.M, a.N, BM, BN)),
-                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
-                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
-  else
-    hipLaunchKernelGGL((rmsnorm_mm_bf16_ring_kernel<BM, BN, BK, W, PRE, false>), dim3(grid_tiles(a.M, a.N, BM, BN)),
-                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
-                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
-  return hipGetLastError();
-}
-
 template <int BM, int BN, int BK, int W, int S, int XS, bool HG, bool NTW, bool SPLIT>
 void launch_rms_xreg_one(const MiArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, HG, NTW, SPLIT>),
                      dim3(grid_tiles(a.M, a.N, BM, BN) * (SPLIT ? a.parts : 1)), dim3(W * 64), 0, s,
                      (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N,
-                     a.K, a.inv_k, a.eps, a.group_m, SPLIT ? a.parts : 1, SPLIT ? a.ws : nullptr);
+                     a.K, a.inv_k, a.eps, a.group_m, SPLIT ? a.parts : 1, SPLIT ? (float*)a.ws : nullptr);
 }
 
 template <int BM, int BN, int BK, int W, int S, int XS, bool NTW = false>
@@ -146,9 +156,8 @@ hipError_t launch_rms_xreg(const MiArgs& a, hipStream_t s) {
     else launch_rms_xreg_one<BM, BN, BK, W, S, XS, false, NTW, true>(a, s);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const size_t blocks = ((size_t)a.M * (size_t)a.N / 8 + 255) / 256;
-    hipLaunchKernelGGL(splitk_rms_sum_kernel<0>, dim3((unsigned)(blocks < 4096 ? blocks : 4096)), dim3(256), 0, s,
-                       (const float*)a.ws, (uint16_t*)a.out, a.M, a.N, a.parts, a.inv_k, a.eps);
+    const float* prod = (const float*)a.ws;
+    launch_splitk_rms_sum(prod, a.parts, prod + (size_t)a.parts * (size_t)a.M * (size_t)a.N, a.parts, a, s);
   } else if (a.g) {
     launch_rms_xreg_one<BM, BN, BK, W, S, XS, true, NTW, false>(a, s);
   } else {
@@ -157,31 +166,32 @@ hipError_t launch_rms_xreg(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int BM, int BN, int BK, int W, int S, int WMX, int D>
-hipError_t launch_rms_direct(const MiArgs& a, hipStream_t s) {
-  if (a.g)
-    hipLaunchKernelGGL((rmsnorm_mm_bf16_direct_kernel<BM, BN, BK, W, S, WMX, D, true>),
-                       dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
-                       (const uint16_t*)a.g, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps,
-                       a.group_m);
-  else
-    hipLaunchKernelGGL((rmsnorm_mm_bf16_direct_kernel<BM, BN, BK, W, S, WMX, D, false>),
-                       dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
-                       (const uint16_t*)a.g, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps,
-                       a.group_m);
-  return hipGetLastError();
-}
-
+// Two-pass fused kernel (variant 13): pass 1 packs x*gamma into the lhsT
+// layout and the row sums of squares into the workspace, pass 2 is the
+// pipelined lhsT.rhs core with the rms row scale (split: into the
+// products, then the fused second pass of split-K).
 template <int BM, int BN, int BK, int W, int S>
-hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
-  if (a.g)
-    hipLaunchKernelGGL((rmsnorm_mm_bf16_xpair_kernel<BM, BN, BK, W, S, true>), dim3(grid_tiles(a.M, a.N, BM, BN)),
-                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
-                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
-  else
-    hipLaunchKernelGGL((rmsnorm_mm_bf16_xpair_kernel<BM, BN, BK, W, S, false>), dim3(grid_tiles(a.M, a.N, BM, BN)),
-                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b,
-                       (uint16_t*)a.out, a.M, a.N, a.K, a.inv_k, a.eps, a.group_m);
+hipError_t launch_rms_2pass(const MiArgs& a, hipStream_t s) {
+  const size_t m = (size_t)a.M, k = (size_t)a.K;
+  const int sparts = rms2_parts(a.K);
+  uint16_t* xt = (uint16_t*)a.ws;
+  float* ssq = (float*)(a.ws + align256(k * m * 2));
+  float* prod = (float*)(a.ws + align256(k * m * 2) + align256((size_t)sparts * m * 4));
+  hipLaunchKernelGGL(rms_pack_kernel<0>, dim3((unsigned)((a.M + RP_ROWS - 1) / RP_ROWS), (unsigned)sparts),
+                     dim3(RP_WAVES * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, xt, ssq, a.M, a.K);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (a.parts > 1) {
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_2pass_kernel<BM, BN, BK, W, S, true>),
+                       dim3(grid_tiles(a.M, a.N, BM, BN) * a.parts), dim3(W * 64), 0, s, xt, (const uint16_t*)a.b,
+                       (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, prod, ssq, sparts, a.inv_k, a.eps);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    launch_splitk_rms_sum(prod, a.parts, ssq, sparts, a, s);
+  } else {
+    hipLaunchKernelGGL((rmsnorm_mm_bf16_2pass_kernel<BM, BN, BK, W, S, false>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                       dim3(W * 64), 0, s, xt, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, 1,
+                       nullptr, ssq, sparts, a.inv_k, a.eps);
+  }
   return hipGetLastError();
 }
 
@@ -193,41 +203,35 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
                                                                       uint16_t*, int, int, int, int);
 // Pipelined lhsT matmul (variant 1; MI_MMPN: variant 3, rhs non-temporal),
 // unsplit and split-K instances.
-#define MI_MMP_INST(BM, BN, BK, W, S)                                                                          \
-  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, false>(                      \
-      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);                \
-  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, true>(                       \
+#define MI_MMP_INST(BM, BN, BK, W, S)                                                     \
+  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, false>( \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);     \
+  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, true>(  \
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
-#define MI_MMPN_INST(BM, BN, BK, W, S)                                                                         \
-  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, false>(                       \
-      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);                \
-  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, true>(                        \
+#define MI_MMPN_INST(BM, BN, BK, W, S)                                                   \
+  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, false>( \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);    \
+  template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, true>(  \
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
-#define MI_MMK_INST(BM, BN, BK, W, S)                                                                          \
-  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, false>(                       \
-      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);                           \
-  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, true>(                        \
+#define MI_MMK_INST(BM, BN, BK, W, S)                                                    \
+  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, false>( \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);    \
+  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, true>(  \
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
-#define MI_MMKN_INST(BM, BN, BK, W, S)                                                                         \
-  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, false>(                        \
-      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);                           \
-  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, true>(                         \
+#define MI_MMKN_INST(BM, BN, BK, W, S)                                                  \
+  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, false>( \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);   \
+  template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, true>(  \
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
-#define MI_MMKP_INST(BM, BN, BK, W, S)                                                                        \
-  template __global__ void mm_lhs_rhs_bf16_pair_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*,    \
+#define MI_MMKP_INST(BM, BN, BK, W, S)                                                                     \
+  template __global__ void mm_lhs_rhs_bf16_pair_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*, \
                                                                           uint16_t*, int, int, int, int);
-#define MI_RMS_INST(BM, BN, BK, W, S, PRE)                                                                   \
-  template __global__ void rmsnorm_mm_bf16_kernel<BM, BN, BK, W, S, (PRE != 0)>(                            \
+#define MI_RMS_INST(BM, BN, BK, W, S, PRE)                                        \
+  template __global__ void rmsnorm_mm_bf16_kernel<BM, BN, BK, W, S, (PRE != 0)>( \
       const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
-
-#define MI_MMR_INST(BM, BN, BK, W, PF)                                                                          \
-  template __global__ void mm_lhsT_rhs_bf16_reg_kernel<BM, BN, BK, W, PF>(const uint16_t*, const uint16_t*,    \
+#define MI_MMR_INST(BM, BN, BK, W, PF)                                                                       \
+  template __global__ void mm_lhsT_rhs_bf16_reg_kernel<BM, BN, BK, W, PF>(const uint16_t*, const uint16_t*, \
                                                                            uint16_t*, int, int, int, int);
-#define MI_RMSR_INST(BM, BN, BK, W, PRE)                                                                  \
-  template __global__ void rmsnorm_mm_bf16_ring_kernel<BM, BN, BK, W, (PRE != 0), true>(                 \
-      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);       \
-  template __global__ void rmsnorm_mm_bf16_ring_kernel<BM, BN, BK, W, (PRE != 0), false>(                \
-      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
 
 // Variant 4 stages x through a 2-slot register ring, variant 5 a 3-slot one.
 // Each with and without gamma, unsplit and split-K.
@@ -248,21 +252,16 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
   MI_RMSX_ONE(BM, BN, BK, W, S, XS, true, true, true)   \
   MI_RMSX_ONE(BM, BN, BK, W, S, XS, false, true, true)
 
-// x operand straight to registers: variant 6 + (D-2) + 2*(wave grid transposed).
-#define MI_RMSD_INST(BM, BN, BK, W, S, WMX, D, V)                                                     \
-  template __global__ void rmsnorm_mm_bf16_direct_kernel<BM, BN, BK, W, S, WMX, D, true>(             \
-      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int); \
-  template __global__ void rmsnorm_mm_bf16_direct_kernel<BM, BN, BK, W, S, WMX, D, false>(            \
-      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
+// Variant 13: the main pass of the two-pass fused kernel, unsplit and split.
+#define MI_RMS2_INST(BM, BN, BK, W, S)                                                                       \
+  template __global__ void rmsnorm_mm_bf16_2pass_kernel<BM, BN, BK, W, S, false>(                           \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*, const float*, int, float, \
+      float);                                                                                                \
+  template __global__ void rmsnorm_mm_bf16_2pass_kernel<BM, BN, BK, W, S, true>(                            \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*, const float*, int, float, \
+      float);
 
-// x loaded two K tiles per instruction (variant 10).
-#define MI_RMSP_INST(BM, BN, BK, W, S)                                                                \
-  template __global__ void rmsnorm_mm_bf16_xpair_kernel<BM, BN, BK, W, S, true>(                      \
-      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int); \
-  template __global__ void rmsnorm_mm_bf16_xpair_kernel<BM, BN, BK, W, S, false>(                     \
-      const uint16_t*, const uint16_t*, const uint16_t*, uint16_t*, int, int, int, float, float, int);
-
-// Table rows; a config whose wave grid is illegal gets no instance.
+// Table rows.
 #define MI_MM_ROW(BM, BN, BK, W, S)                                                                  \
   {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 0}, MatmulCfg<BM, BN, BK, W, S>::LDS_BYTES, \
    &launch_mm_bf16<BM, BN, BK, W, S>},
@@ -292,13 +291,8 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
 // Register-ring matmul (variant 2): lds_stages carries the prefetch depth PF
 // (its LDS is always two stages).
 #define MI_MMR_ROW(BM, BN, BK, W, PF)                                                         \
-  {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, PF, 1, 0, 2}, 2 * (BM + BN) * BK * 2, \
+  {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, PF, 1, 0, 2}, lds_mm_reg(BM, BN, BK, W), \
    &launch_mm_reg<BM, BN, BK, W, PF>},
-// Ring-pipelined fused kernel: the tile config names 2 stages (its A/W
-// double buffer); variant 2 + PRE.
-#define MI_RMSR_ROW(BM, BN, BK, W, PRE)                                                                 \
-  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, 2, 1, 0, 2 + PRE}, RingCfg<BM, BN, BK, W>::LDS_BYTES, \
-   &launch_rms_ring<BM, BN, BK, W, (PRE != 0)>},
 
 #define MI_RMSX_ROW(BM, BN, BK, W, S, XS)                                                                   \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 2 + XS}, XregCfg<BM, BN, BK, W, S>::LDS_BYTES, \
@@ -308,13 +302,9 @@ hipError_t launch_rms_xpair(const MiArgs& a, hipStream_t s) {
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 9 + XS}, XregCfg<BM, BN, BK, W, S>::LDS_BYTES, \
    &launch_rms_xreg<BM, BN, BK, W, S, XS, true>, XregCfg<BM, BN, BK, W, S>::GK_MAX},
 
-#define MI_RMSD_ROW(BM, BN, BK, W, S, WMX, D, V)                                                         \
-  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, V}, DirectCfg<BM, BN, BK, W, S, WMX>::LDS_BYTES, \
-   &launch_rms_direct<BM, BN, BK, W, S, WMX, D>, DirectCfg<BM, BN, BK, W, S, WMX>::GK_MAX},
-
-#define MI_RMSP_ROW(BM, BN, BK, W, S)                                                                \
-  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 10}, XpairCfg<BM, BN, BK, W, S>::LDS_BYTES, \
-   &launch_rms_xpair<BM, BN, BK, W, S>, XpairCfg<BM, BN, BK, W, S>::GK_MAX},
+#define MI_RMS2_ROW(BM, BN, BK, W, S)                                                               \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 13}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_rms_2pass<BM, BN, BK, W, S>},
 
 // The 72-point search grid for one (BM, BN): BK in {32,64} x waves in {4,8} x
 // stages in {1,2}.  X is a row macro taking (BM, BN, BK, W, S, ...).
@@ -350,12 +340,10 @@ const MiEntry* table_mm_pipe(int* n);
 const MiEntry* table_mm_reg(int* n);
 const MiEntry* table_mm_lhs(int* n);
 const MiEntry* table_rms_xreg(int* n);
-const MiEntry* table_rms_direct(int* n);
-const MiEntry* table_rms_xpair(int* n);
+const MiEntry* table_rms_2pass(int* n);
 const MiEntry* table_rms_bm64(int* n);
 const MiEntry* table_rms_bm128(int* n);
 const MiEntry* table_rms_bm256(int* n);
-const MiEntry* table_rms_pipe(int* n);
 const MiEntry* table_f32(int* n);
 
 }  // namespace mi

@@ -90,6 +90,9 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
     float* __restrict__ ws) {
   using C = XregCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
+  static_assert(legal_rms_xreg(BM, BN, BK, WAVES, STAGES, XS).code == MI_OK, "illegal tile config (mi_legal.hpp)");
+  static_assert(C::LDS_BYTES == lds_rms_xreg(BM, BN, BK, WAVES, STAGES), "host LDS budget out of step");
+  static_assert(C::GK_MAX == xreg_gamma_kmax(BM, BN, BK, WAVES, STAGES), "host gamma capacity out of step");
   static_assert(G::ok, "illegal wave grid");
   static_assert(BK % 32 == 0, "BK must be a multiple of 32 (even number of MFMA K steps)");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
@@ -391,21 +394,21 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_xreg_kernel(
 }
 
 // Split-K second pass of the fused kernel: for 8 consecutive elements of
-// row m, out = bf16(rsqrt(sum_p ssq[p][m] * inv_k + eps) * sum_p ws[p][...]),
-// both sums in part order (ws = [parts][M][N] products, then [parts][M]
-// sums of squares; N % 8 == 0, so 8 elements never straddle rows).
+// row m, out = bf16(rsqrt(sum_q ssq[q][m] * inv_k + eps) * sum_p ws[p][...]),
+// both sums in part order (ws = [parts][M][N] products, ssq = [ssq_parts][M]
+// partial sums of squares; N % 8 == 0, so 8 elements never straddle rows).
 template <int UNUSED = 0>
 __global__ __launch_bounds__(256) void splitk_rms_sum_kernel(const float* __restrict__ ws, uint16_t* __restrict__ out,
-                                                             int M, int N, int parts, float inv_k, float eps) {
+                                                             int M, int N, int parts, const float* __restrict__ ssq,
+                                                             int ssq_parts, float inv_k, float eps) {
   const size_t n = (size_t)M * (size_t)N;
-  const float* ssq = ws + (size_t)parts * n;
   const size_t stride = (size_t)gridDim.x * 256 * 8;
   for (size_t i = ((size_t)blockIdx.x * 256 + threadIdx.x) * 8; i < n; i += stride) {
     const size_t m = i / (size_t)N;
     float r = ssq[m];
+    for (int q = 1; q < ssq_parts; ++q) r += ssq[(size_t)q * M + m];
     f32x4_t lo = *(const f32x4_t*)(ws + i), hi = *(const f32x4_t*)(ws + i + 4);
     for (int p = 1; p < parts; ++p) {
-      r += ssq[(size_t)p * M + m];
       lo += *(const f32x4_t*)(ws + (size_t)p * n + i);
       hi += *(const f32x4_t*)(ws + (size_t)p * n + i + 4);
     }

@@ -46,7 +46,7 @@ def asm_of(tmp_path_factory):
     return get
 
 
-@pytest.mark.parametrize("unit", ["rms_bf16_xreg.hip", "rms_bf16_direct.hip", "rms_bf16_xpair.hip"])
+@pytest.mark.parametrize("unit", ["rms_bf16_xreg.hip"])
 def test_async_register_loads_untouched_until_waited(unit, asm_of):
     ks = kernels(asm_of(unit))
     assert ks
@@ -59,7 +59,7 @@ def test_async_register_loads_untouched_until_waited(unit, asm_of):
 
 
 @pytest.mark.parametrize("unit", ["mm_bf16_pipe.hip", "mm_bf16_lhs.hip", "mm_bf16_reg.hip", "rms_bf16_xreg.hip",
-                                  "rms_bf16_direct.hip", "rms_bf16_xpair.hip"])
+                                  "rms_bf16_2pass.hip"])
 def test_kernels_straight_line(unit, asm_of):
     """The unrolled tile lambdas are inlined: a device-function call would
     pass buffer descriptors in VGPRs and read captures through flat loads."""

@@ -59,9 +59,17 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (MM, TileConfig(128, 128, 64, 4, 2), (1020, 1024, 1024), _lib.MI_E_ALIGN),       # M % 8
         (RMS, TileConfig(128, 128, 64, 8, 2), (1024, 1024, 1020), _lib.MI_E_ALIGN),      # K % 8 (fused)
         (MM, TileConfig(128, 128, 64, 4, 2), (65536, 65536, 65536), _lib.MI_E_RANGE),    # 8 GiB operand
-        (RMS, TileConfig(256, 256, 32, 8, 3, variant=6), (1024, 1024, 16392), _lib.MI_E_RANGE),   # gamma > LDS
-        (RMS, TileConfig(256, 256, 32, 8, 3, variant=10), (1024, 1024, 8200), _lib.MI_E_RANGE),   # 8192 fp32
-        (RMS, TileConfig(256, 256, 32, 8, 3, variant=10), (1024, 1024, 8192), _lib.MI_OK),
+        (RMS, TileConfig(256, 256, 32, 8, 3, variant=6), (1024, 1024, 1024), _lib.MI_E_TILE),     # no variant 6
+        (RMS, TileConfig(256, 256, 32, 8, 3, variant=10), (1024, 1024, 1024), _lib.MI_E_TILE),    # no variant 10
+        # the two-pass kernel (variant 13) has no gamma limit: its main pass is the lhsT core
+        (RMS, TileConfig(256, 256, 32, 4, 3, variant=13), (4096, 4096, 4096), _lib.MI_OK),
+        (RMS, TileConfig(256, 256, 32, 4, 3, variant=13), (1024, 1024, 32768), _lib.MI_OK),
+        (RMS, TileConfig(128, 128, 64, 4, 3, split_k=4, variant=13), (512, 512, 16384), _lib.MI_OK),
+        (RMS, TileConfig(256, 256, 32, 4, 3, variant=13), (1024, 1024, 1020), _lib.MI_E_ALIGN),   # K % 8
+        (RMS, TileConfig(256, 256, 32, 4, 1, variant=13), (1024, 1024, 1024), _lib.MI_E_TILE),    # pipelined core
+        (RMS, TileConfig(256, 256, 64, 4, 3, variant=13), (1024, 1024, 1024), _lib.MI_E_LDS),     # 3 x 64 KiB
+        (MM, TileConfig(256, 512, 32, 4, 3, variant=1), (1024, 1024, 1024), _lib.MI_E_WAVE_TILE),  # 512 acc regs
+        (MM, TileConfig(256, 512, 32, 8, 2, variant=1), (1024, 1024, 1024), _lib.MI_E_WAVE_TILE),  # 2 waves/SIMD
         (RMS, TileConfig(256, 256, 32, 8, 3, variant=5), (1024, 1024, 8200), _lib.MI_E_RANGE),
         (RMS, TileConfig(256, 256, 32, 8, 3, variant=5), (1024, 1024, 8192), _lib.MI_OK),
         # four 32 KiB stages leave room for 7936 fp32 gamma entries
@@ -90,12 +98,13 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (RMS, TileConfig(128, 128, 64, 4, 2, variant=4), (256, 1024, 16384), _lib.MI_E_RANGE),
         (MM, TileConfig(32, 128, 64, 4, 4, split_k=16, variant=1), (16384, 16384, 8192), _lib.MI_E_RANGE),
         (MM, TileConfig(128, 128, 48, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),
-        (MM, TileConfig(512, 512, 32, 8, 1), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),  # legal, not prebuilt
+        (MM, TileConfig(64, 512, 32, 8, 2), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),   # legal, not prebuilt
+        (MM, TileConfig(512, 512, 32, 8, 1), (1024, 1024, 1024), _lib.MI_E_WAVE_TILE),    # 256x128 per wave
         (MM, TileConfig(0, 128, 64, 4, 2), (1024, 1024, 1024), _lib.MI_E_ARGS),
         (LHS, TileConfig(256, 256, 32, 4, 3), (8192, 8192, 8192), _lib.MI_OK),
         (LHS, TileConfig(256, 256, 32, 4, 3), (1024, 1024, 1020), _lib.MI_E_ALIGN),      # K % 8 (K-contiguous lhs)
         (LHS, TileConfig(128, 128, 16, 4, 2), (1024, 1024, 1024), _lib.MI_E_TILE),       # pipelined core: bk >= 32
-        (LHS, TileConfig(256, 256, 32, 4, 3, variant=3), (1024, 1024, 1024), _lib.MI_E_NO_INSTANCE),
+        (LHS, TileConfig(256, 256, 32, 4, 3, variant=3), (1024, 1024, 1024), _lib.MI_E_TILE),     # no variant 3
         (LHS, TileConfig(256, 256, 64, 4, 2), (65536, 65536, 65536), _lib.MI_E_RANGE),
         (LHS, TileConfig(64, 128, 128, 4, 3, variant=1), (1024, 1024, 1024), _lib.MI_E_TILE),    # pairs: bk <= 64
         (MM, TileConfig(256, 256, 32, 8, 1, variant=1), (1024, 1024, 1024), _lib.MI_E_TILE),     # pipelined: >= 2 stages
@@ -122,7 +131,7 @@ def test_split_k_variants_are_named_and_legal():
                 and x.block_n >= 128]
     assert split_k_variants("matmul_lhsT_rhs_f32", compiled_configs("matmul_lhsT_rhs_f32"), 16, 16) == []
     rms = [x for x in legal_configs("rmsnorm_matmul", 512, 512, 8192) if x.split_k > 1]
-    assert rms and all(x.variant in (4, 5, 11, 12) for x in rms)
+    assert rms and all(x.variant in (4, 5, 11, 12, 13) for x in rms)
     lhs = [x for x in legal_configs("matmul_lhs_rhs", 512, 512, 32768) if x.split_k > 1]
     assert lhs and all(x.variant in (0, 2) for x in lhs)
 

@@ -138,7 +138,9 @@ def _sampled_check(out_host: np.ndarray, lhs_T: np.ndarray, rhs: np.ndarray, row
     ],
 )
 def test_bf16_baseline_shapes(gpu, M, N, K, dist):
-    """Benchmark shapes (C2, C4, C5) with the default (tuned) config.
+    """Benchmark shapes (C2, C4, C5) with the default (tuned) config and, at
+    C2, every config the benchmark's autotune sweep has shipped or can ship
+    (the 256x256 and 128x512 pipelined configs, 2..4 stages, 4 or 8 waves).
 
     Sampled rows against the oracle's float64 closed form; the whole output
     against a float64 torch product of the same bf16 inputs on the GPU; and
@@ -150,20 +152,30 @@ def test_bf16_baseline_shapes(gpu, M, N, K, dist):
     print(f"shape M={M} N={N} K={K}", flush=True)
     d = mm_inputs(K, M, N, seed=0, dist=dist)
     a, b = _dev(d["lhs_T"], torch.bfloat16, gpu), _dev(d["rhs"], torch.bfloat16, gpu)
-    out = kl.matmul_lhsT_rhs(a, b)
-    host = _host(out)
+    cfgs = [kl.default_config("matmul_lhsT_rhs", M, N, K)]
+    if (M, N, K) == (8192, 8192, 8192):
+        cfgs += [kl.TileConfig.from_name(n) for n in C2_SHIPPABLE]
     rng = np.random.default_rng(1)
     rows = np.unique(np.concatenate([[0, M - 1], rng.integers(0, M, size=min(M, 24))]))
-    rep = _sampled_check(host, d["lhs_T"], d["rhs"], rows)
-    print("sampled rows vs oracle", rep)
-    assert rep["ok"], rep
     ref = (a.double().t() @ b.double()).cpu().numpy()
-    full = mm_check(host, ref)
-    print("full output vs fp64 torch", full)
-    assert full["ok"], full
-    del ref
-    out2 = kl.matmul_lhsT_rhs(a, b * 2)
-    assert torch.equal(out2, out * 2)
+    for cfg in cfgs:
+        out = kl.matmul_lhsT_rhs(a, b, cfg=cfg)
+        host = _host(out)
+        rep = _sampled_check(host, d["lhs_T"], d["rhs"], rows)
+        print(cfg.name, "sampled rows vs oracle", rep, flush=True)
+        assert rep["ok"], (cfg, rep)
+        full = mm_check(host, ref)
+        print(cfg.name, "full output vs fp64 torch", full, flush=True)
+        assert full["ok"], (cfg, full)
+        out2 = kl.matmul_lhsT_rhs(a, b * 2, cfg=cfg)
+        assert torch.equal(out2, out * 2), cfg
+
+
+# Configs the C2 sweep has picked on some box (bench.py runs the sweep), and
+# their neighbours in the same family.
+C2_SHIPPABLE = ("bm256_bn256_bk32_w4_s3_v1", "bm256_bn256_bk32_w4_s4_v1", "bm256_bn256_bk32_w4_s2_v1",
+                "bm256_bn256_bk32_w8_s3_v1", "bm256_bn256_bk64_w4_s2_v1", "bm256_bn256_bk64_w8_s2_v1",
+                "bm128_bn512_bk32_w8_s3_v1")
 
 
 def test_empty_contraction_writes_zeros(gpu):

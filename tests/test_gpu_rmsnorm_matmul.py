@@ -16,6 +16,9 @@ from oracle import rmsnorm as orms
 
 pytestmark = pytest.mark.gpu
 
+# Every variant of the fused kernel (include/mi_kernels.h).
+VARIANTS = (0, 1, 4, 5, 11, 12, 13)
+
 
 def _dev(a, device):
     import torch
@@ -58,7 +61,7 @@ def test_no_gamma_is_reference_kernel(gpu):
     assert _ok(rep), rep
 
 
-@pytest.mark.parametrize("variant", list(range(13)))
+@pytest.mark.parametrize("variant", VARIANTS)
 def test_no_gamma_every_variant(gpu, variant):
     """gamma=None takes each kernel's no-gamma instance; K = 576 is not a multiple of 64."""
     import kernel_library as kl
@@ -73,7 +76,7 @@ def test_no_gamma_every_variant(gpu, variant):
         assert _ok(rep), (cfg, rep)
 
 
-@pytest.mark.parametrize("variant", list(range(13)))
+@pytest.mark.parametrize("variant", VARIANTS)
 def test_ragged_and_special_rows(gpu, variant):
     """Edge tiles (M, N not multiples of the block), K not a multiple of block_k; a zero row gives 0."""
     import torch
@@ -112,7 +115,8 @@ def test_scale_invariance_and_identity_weight(gpu):
 
 
 def test_baseline_c3_full_size(gpu):
-    """Benchmark config C3 (M=K=N=4096, gamma, eps=1e-6), every variant: sampled rows vs closed form."""
+    """Benchmark config C3 (M=K=N=4096, gamma, eps=1e-6), every variant family
+    and the configs the C3 sweep ships: sampled rows vs the closed form."""
     import kernel_library as kl
 
     print("C3 4096^3 rmsnorm_matmul", flush=True)
@@ -122,19 +126,55 @@ def test_baseline_c3_full_size(gpu):
     rows = np.unique(np.concatenate([[0, 4095], rng.integers(0, 4096, size=24)]))
     expected = orms.closed_form(d["lhs"][rows], d["rhs"], d["gamma"])
     cfgs = [kl.TileConfig(256, 256, 64, 8, 2, variant=0), kl.TileConfig(256, 256, 64, 8, 2, variant=1),
-            kl.TileConfig(256, 256, 32, 8, 2, variant=2), kl.TileConfig(256, 256, 32, 8, 2, variant=3),
-            kl.TileConfig(128, 256, 64, 4, 2, variant=2), kl.TileConfig(256, 256, 32, 4, 2, variant=3),
             kl.TileConfig(256, 256, 32, 8, 3, variant=4), kl.TileConfig(256, 256, 64, 4, 2, variant=4),
             kl.TileConfig(256, 256, 32, 8, 3, variant=5), kl.TileConfig(256, 256, 32, 8, 2, variant=5),
-            kl.TileConfig(256, 256, 32, 8, 3, variant=6), kl.TileConfig(256, 256, 32, 8, 3, variant=9),
-            kl.TileConfig(256, 256, 32, 4, 3, variant=7), kl.TileConfig(256, 256, 32, 8, 3, variant=10),
-            kl.TileConfig(128, 256, 32, 8, 3, variant=10)]
+            kl.TileConfig(128, 512, 32, 8, 3, variant=4), kl.TileConfig(128, 512, 32, 8, 3, variant=5),
+            kl.TileConfig(256, 256, 32, 4, 3, variant=13), kl.TileConfig(256, 256, 32, 4, 4, variant=13),
+            kl.TileConfig(128, 512, 32, 8, 3, variant=13), kl.TileConfig(256, 256, 32, 8, 3, variant=13),
+            kl.default_config("rmsnorm_matmul", 4096, 4096, 4096)]
     for cfg in cfgs:
-        variant = cfg.variant
         out = _host(kl.rmsnorm_matmul(x, w, g, cfg=cfg))
         rep = rms_check(out[rows], expected)
-        print(variant, rep)
-        assert _ok(rep), rep
+        print(cfg.name, rep, flush=True)
+        assert _ok(rep), (cfg, rep)
+
+
+@pytest.mark.parametrize("shape,with_gamma", [((4096, 4096, 4096), True), ((2048, 2048, 2048), False)])
+def test_error_within_reference_bf16_semantics(gpu, shape, with_gamma):
+    """The kernel's error is no larger than that of the reference kernel's own
+    bf16 arithmetic on the same rows: the online recurrence with the scaled
+    tile and O rounded to bf16 (kernel_hand_online.py:139-149, 165-192;
+    oracle.rmsnorm.online(tile_dtype="bfloat16")), both against the float64
+    closed form.  Checked for the configs the benchmark ships (C3 with gamma;
+    the reference's 2048^3 without), the library default and the two-pass
+    variant; the ratio of the two errors is printed."""
+    import kernel_library as kl
+
+    M, N, K = shape
+    print(f"reference-semantics bound M={M} N={N} K={K} gamma={with_gamma}", flush=True)
+    d = rms_inputs(M, K, N, seed=0, with_gamma=with_gamma)
+    gam = d.get("gamma")
+    x, w = _dev(d["lhs"], gpu), _dev(d["rhs"], gpu)
+    g = _dev(gam, gpu) if with_gamma else None
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(11).integers(0, M, size=30)]))
+    closed = orms.closed_form(d["lhs"][rows], d["rhs"], gam)
+    ref_bf16 = orms.online(d["lhs"][rows], d["rhs"], gam, tile_dtype="bfloat16")
+    ref_err = float(np.max(np.abs(ref_bf16.astype(np.float64) - closed)))
+    if with_gamma:
+        shipped = [kl.TileConfig.from_name("bm128_bn512_bk32_w8_s3_v4")]
+    else:
+        shipped = [kl.TileConfig.from_name("bm128_bn128_bk64_w4_s2_v4")]
+    cfgs = shipped + [kl.TileConfig(256, 256, 32, 4, 3, variant=13)]
+    if with_gamma:
+        cfgs.append(kl.default_config("rmsnorm_matmul", M, N, K))
+    for cfg in cfgs:
+        out = _host(kl.rmsnorm_matmul(x, w, g, cfg=cfg))[rows]
+        rep = rms_check(out, closed)
+        err = float(np.max(np.abs(out.astype(np.float64) - closed)))
+        print(cfg.name, f"max|hip-closed| {err:.4g}  max|reference bf16 - closed| {ref_err:.4g}  "
+              f"ratio {err / ref_err:.3f}", rep, flush=True)
+        assert _ok(rep), (cfg, rep)
+        assert err <= ref_err, (cfg, err, ref_err)
 
 
 def test_skinny_decode_shape(gpu):

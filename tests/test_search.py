@@ -48,7 +48,7 @@ def test_mdp_moves_and_legality():
         mdp.step(TileConfig(512, 512, 32, 8, 2, variant=1), Atom("block_m", "x2"))   # 1024 out of range
     with pytest.raises(IllegalMove):
         mdp.step(s, Atom("variant", f"={s.variant}"))                                 # no-op move
-    assert Atom("variant", "=10") in atoms_for("rmsnorm_matmul")
+    assert Atom("variant", "=13") in atoms_for("rmsnorm_matmul")
     assert Atom("split_k", "x2") in atoms_for("matmul_lhsT_rhs")
     assert Atom("split_k", "x2") in atoms_for("rmsnorm_matmul")
     assert Atom("split_k", "x2") not in atoms_for("matmul_lhsT_rhs_f32")
@@ -89,3 +89,46 @@ def test_prebuilt_only_stays_in_the_library():
         assert base.name in prebuilt, c
         assert c.split_k == 1 or c.variant in (1, 3), c
     assert Atom("split_k", "x2") in atoms_for("matmul_lhs_rhs")
+
+
+@pytest.mark.parametrize("fam,shape", [("matmul_lhsT_rhs", (4096, 4096, 4096)),
+                                       ("matmul_lhsT_rhs", (128, 28672, 8192)),
+                                       ("matmul_lhs_rhs", (2048, 2048, 2048)),
+                                       ("rmsnorm_matmul", (4096, 4096, 4096)),
+                                       ("rmsnorm_matmul", (64, 28672, 8192))])
+def test_sampled_jit_configs_instantiate(fam, shape, tmp_path):
+    """Every config the sampler takes as legal but not prebuilt is one its
+    template instantiates: a sample of them, instantiated together in one
+    unit, passes hipcc's device-side semantic checks (the templates'
+    static_asserts) -- the sampler never proposes a compile error."""
+    import random
+    import shutil
+    import subprocess
+    from pathlib import Path
+
+    import build_lib
+    from autotune.runner.compile import _instance
+    from kernel_library import _lib
+
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(hipcc).exists():
+        pytest.skip("hipcc not available")
+    mdp = TileMDP(fam, *shape, prebuilt_only=False)
+    pool = frontier_pool(mdp, 600, seed=0)
+    jit = [c for c in pool if kl.check(fam, c, *shape)[0] == _lib.MI_E_NO_INSTANCE]
+    assert jit, "the sampler reached no config outside the prebuilt set"
+    sample = random.Random(0).sample(jit, min(16, len(jit)))
+    lines = ['#include "mi_registry.hpp"', "namespace mi {"]
+    seen = set()
+    for c in sample:
+        inst, _row, args = _instance(fam, c)
+        if (inst, args) not in seen:
+            seen.add((inst, args))
+            lines.append(f"{inst}({args})")
+    lines.append("}  // namespace mi")
+    unit = tmp_path / "sampled.hip"
+    unit.write_text("\n".join(lines) + "\n")
+    flags = [f for f in build_lib.HIPCC_FLAGS if f != "-fPIC"]
+    proc = subprocess.run([hipcc, *flags, f"-I{build_lib.CSRC}", f"-I{build_lib.INCLUDE}", "--cuda-device-only",
+                           "-fsyntax-only", "-ferror-limit=0", str(unit)], capture_output=True, text=True)
+    assert proc.returncode == 0, ([c.name for c in sample], proc.stderr[-3000:])
