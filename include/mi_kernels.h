@@ -142,6 +142,20 @@ int mi_matmul_lhsT_rhs_f32(const float* lhsT, const float* rhs, float* out, int 
 int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void* out, int M, int N,
                            int K, float eps, const mi_tile_cfg* cfg, void* stream);
 
+/* mi_matmul_lhsT_rhs_bf16 without any device allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, result and errors as mi_matmul_lhsT_rhs_bf16;
+ * the workspace of a split-K config (split_k * M * N * 4 bytes of fp32
+ * partial products) is a static device array of MI_NOALLOC_SCRATCH_BYTES
+ * that each GPU holds from the first call there until the process ends, and
+ * a config needing more returns MI_E_RANGE.  Calls on one GPU share that
+ * array: calls ordered on one stream are safe, calls that overlap on one GPU
+ * race. */
+#define MI_NOALLOC_SCRATCH_BYTES (64ull * 1024ull * 1024ull)
+int mi_matmul_lhsT_rhs_bf16_noalloc(const void* lhsT, const void* rhs, void* out, int M, int N, int K,
+                                    const mi_tile_cfg* cfg, void* stream);
+
 /* Device discovery: number of visible HIP devices and the gfx arch name of
  * device 0 (written to arch, at most arch_len bytes).  Returns 0 or -error.
  * Replaces detect_neuron_cores()

@@ -16,9 +16,10 @@
 #include <utility>
 #include <vector>
 
-#include "mi_registry.hpp"
+#include "mi_capi_internal.hpp"
 
-namespace {
+namespace mi {
+namespace capi {
 
 thread_local char g_err[512] = "";
 
@@ -29,6 +30,14 @@ int fail(int code, const char* fmt, ...) {
   va_end(ap);
   return code;
 }
+
+}  // namespace capi
+}  // namespace mi
+
+namespace {
+
+using mi::capi::fail;
+using mi::capi::g_err;
 
 int hip_fail(hipError_t e, const char* what) {
   snprintf(g_err, sizeof(g_err), "%s: %s", what, hipGetErrorString(e));
@@ -307,13 +316,22 @@ int launch(const mi::MiEntry* e, const mi_tile_cfg& cfg, const mi::MiArgs& args_
   return err == hipSuccess ? MI_OK : hip_fail(err, "kernel launch");
 }
 
-int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, void* stream) {
+// fixed_ws != NULL: the caller's device buffer of fixed_cap bytes serves as
+// the workspace (nothing is allocated; a larger need is rejected).
+int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, void* stream, char* fixed_ws = nullptr,
+        size_t fixed_cap = 0) {
   mi_tile_cfg cfg;
   const mi::MiEntry* e = nullptr;
   const int rc = resolve(kernel_id, cfg_in, args_in, &cfg, &e);
   if (rc != MI_OK) return rc;
   const size_t ws_bytes = mi::workspace_bytes(kernel_id, cfg, args_in.M, args_in.N, args_in.K);
   if (ws_bytes == 0) return launch(e, cfg, args_in, nullptr, stream);
+  if (fixed_ws) {
+    if (ws_bytes > fixed_cap)
+      return fail(MI_E_RANGE, "the config needs %zu bytes of workspace, over the %zu-byte static scratch", ws_bytes,
+                  fixed_cap);
+    return launch(e, cfg, args_in, fixed_ws, stream);
+  }
   hipMemPool_t pool = nullptr;
   const int prc = workspace_pool(&pool);
   if (prc != MI_OK) return prc;
@@ -332,6 +350,27 @@ int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, voi
 bool misaligned(const void* p, uintptr_t align) { return p && ((uintptr_t)p & (align - 1)) != 0; }
 
 }  // namespace
+
+namespace mi {
+namespace capi {
+
+int matmul_lhsT_rhs_bf16(const void* lhsT, const void* rhs, void* out, int M, int N, int K, const mi_tile_cfg* cfg,
+                         void* stream, char* fixed_ws, size_t fixed_cap) {
+  if (M < 0 || N < 0 || K < 0) return fail(MI_E_ARGS, "negative size M=%d N=%d K=%d", M, N, K);
+  if (M == 0 || N == 0) return MI_OK;
+  if (!out) return fail(MI_E_ARGS, "null output pointer");
+  if (K == 0) {
+    return zero_output<uint16_t>(out, (size_t)M * N, stream);
+  }
+  if (!lhsT || !rhs) return fail(MI_E_ARGS, "null input pointer");
+  if (misaligned(lhsT, 16) || misaligned(rhs, 16) || misaligned(out, 16))
+    return fail(MI_E_ALIGN, "lhsT, rhs and out must be 16-byte aligned");
+  mi::MiArgs a = {lhsT, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
+  return run(MI_KERNEL_MATMUL_LHST_RHS_BF16, cfg, a, stream, fixed_ws, fixed_cap);
+}
+
+}  // namespace capi
+}  // namespace mi
 
 extern "C" {
 
@@ -367,17 +406,7 @@ int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
 
 int mi_matmul_lhsT_rhs_bf16(const void* lhsT, const void* rhs, void* out, int M, int N, int K,
                             const mi_tile_cfg* cfg, void* stream) {
-  if (M < 0 || N < 0 || K < 0) return fail(MI_E_ARGS, "negative size M=%d N=%d K=%d", M, N, K);
-  if (M == 0 || N == 0) return MI_OK;
-  if (!out) return fail(MI_E_ARGS, "null output pointer");
-  if (K == 0) {
-    return zero_output<uint16_t>(out, (size_t)M * N, stream);
-  }
-  if (!lhsT || !rhs) return fail(MI_E_ARGS, "null input pointer");
-  if (misaligned(lhsT, 16) || misaligned(rhs, 16) || misaligned(out, 16))
-    return fail(MI_E_ALIGN, "lhsT, rhs and out must be 16-byte aligned");
-  mi::MiArgs a = {lhsT, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
-  return run(MI_KERNEL_MATMUL_LHST_RHS_BF16, cfg, a, stream);
+  return mi::capi::matmul_lhsT_rhs_bf16(lhsT, rhs, out, M, N, K, cfg, stream, nullptr, 0);
 }
 
 int mi_matmul_lhs_rhs_bf16(const void* lhs, const void* rhs, void* out, int M, int N, int K,

@@ -51,6 +51,7 @@ EXPORTED_SYMBOLS = (
     "mi_get_config",
     "mi_default_config",
     "mi_matmul_lhsT_rhs_bf16",
+    "mi_matmul_lhsT_rhs_bf16_noalloc",
     "mi_matmul_lhs_rhs_bf16",
     "mi_matmul_lhsT_rhs_f32",
     "mi_rmsnorm_matmul_bf16",
@@ -58,6 +59,14 @@ EXPORTED_SYMBOLS = (
     "mi_last_error",
     "mi_version",
 )
+
+
+# Exported by libmi_kernels.so only (not by the single-config libraries the
+# autotuner builds just in time).
+PREBUILT_ONLY_SYMBOLS = frozenset({"mi_matmul_lhsT_rhs_bf16_noalloc"})
+# Bytes of the static device scratch of mi_matmul_lhsT_rhs_bf16_noalloc
+# (MI_NOALLOC_SCRATCH_BYTES).
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 
 class MiTileCfg(ctypes.Structure):
@@ -96,6 +105,10 @@ def _declare(lib: ctypes.CDLL) -> None:
         "mi_get_config": (c_int, [c_int, c_int, cfgp]),
         "mi_default_config": (c_int, [c_int, c_int, c_int, c_int, cfgp]),
         "mi_matmul_lhsT_rhs_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, cfgp, c_void_p]),
+        "mi_matmul_lhsT_rhs_bf16_noalloc": (
+            c_int,
+            [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, cfgp, c_void_p],
+        ),
         "mi_matmul_lhs_rhs_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, cfgp, c_void_p]),
         "mi_matmul_lhsT_rhs_f32": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, cfgp, c_void_p]),
         "mi_rmsnorm_matmul_bf16": (
@@ -107,6 +120,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         "mi_version": (c_char_p, []),
     }
     for name, (res, args) in sigs.items():
+        if name in PREBUILT_ONLY_SYMBOLS and not hasattr(lib, name):
+            continue
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
