@@ -156,8 +156,14 @@ def time_launches(launch, warmup: int, reps: int, flush=None) -> list[float]:
 
 def benchmark_one(kernel_name: str, library_path: str, func_name: str, cfg, inputs: dict[str, Any],
                   out_spec: OutputSpec, M: int, N: int, K: int, warmup: int = 10, reps: int = 50,
-                  flush_bytes: int = 0, collect_detailed_profile: bool = False) -> ProfileResult:
-    """Time one instance; errors become ``hardware_output`` text (reference benchmark.py:116-153)."""
+                  flush_bytes: int = 0, collect_detailed_profile: bool = False,
+                  golden: tuple | None = None) -> ProfileResult:
+    """Time one instance; errors become ``hardware_output`` text (reference benchmark.py:116-153).
+
+    ``golden`` = (expected float64 output, absolute floor) from
+    :mod:`autotune.runner.golden`: the output of the last timed launch must
+    pass that check, or the instance is reported as a numerics failure
+    instead of a success."""
     import torch
 
     from kernel_library import _lib
@@ -175,6 +181,14 @@ def benchmark_one(kernel_name: str, library_path: str, func_name: str, cfg, inpu
             scratch = torch.empty(flush_bytes // 4, dtype=torch.float32, device=dev)
             flush = scratch.zero_
         times = time_launches(launch, warmup, reps, flush)
+        numerics = None
+        if golden is not None:
+            from autotune.runner import golden as gold
+
+            numerics = gold.compare(out, golden[0], golden[1], gold.rtol_for(dtype))
+            if not numerics["pass"]:
+                return ProfileResult(kernel_name, gold.failure_text(numerics), None,
+                                     {"numerics": numerics, "times_s": times} if collect_detailed_profile else None)
         med = statistics.median(times)
         flops, nbytes = work_of(func_name, M, N, K, dtype, has_gamma="gamma" in inputs)
         summary = {
@@ -189,6 +203,8 @@ def benchmark_one(kernel_name: str, library_path: str, func_name: str, cfg, inpu
             "library": library_path,
             **utilisation(flops, nbytes, med, dtype),
         }
+        if numerics is not None:
+            summary["numerics"] = numerics
         if collect_detailed_profile:
             detailed = {"times_s": times, "l2_flush_bytes": flush_bytes}
     except Exception as exc:

@@ -26,6 +26,7 @@ from typing import Any
 from autotune.runner.benchmark import benchmark_one, generate_tensors, upload
 from autotune.runner.compile import canonical_name, compile_one, default_work_dir, parse_source, problem_shape
 from autotune.runner.detect import detect_gpus
+from autotune.runner.golden import expected_output
 from autotune.runner.types import CompileResult, KernelJob, OutputSpec, ProfileResult, compile_failure_result
 
 logger = logging.getLogger(__name__)
@@ -66,12 +67,16 @@ def run_pipeline(
     allow_jit: bool = True,
     work_dir: str | None = None,
     clock_warmup_s: float = 0.5,
+    check_numerics: bool = True,
 ) -> tuple[list[ProfileResult], dict[str, str]]:
     """Build + time every job on GPU 0; return (results, compiler_logs).
 
     Before the first timing, and before any timing that follows more than
     0.2 s without GPU work (a just-in-time build), the GPU is kept busy for
-    ``clock_warmup_s`` seconds (:func:`warm_clock`)."""
+    ``clock_warmup_s`` seconds (:func:`warm_clock`).  With
+    ``check_numerics`` every timed job's output is checked against a float64
+    evaluation of its inputs (:mod:`autotune.runner.golden`), computed once
+    per input set; a job that fails becomes a failure row."""
     import torch
 
     if not kernels:
@@ -89,17 +94,16 @@ def run_pipeline(
                 arch, cus)
     device = torch.device("cuda:0")
 
-    host_cache: dict[str, dict[str, Any]] = {}
     dev_inputs: dict[str, dict[str, Any]] = {}
+    goldens: dict[str, tuple] = {}
     meta: dict[str, tuple] = {}
     for kname, job in kernels.items():
         key = _inputs_key(job, seed)
         if key not in dev_inputs:
-            host = generate_tensors(job.input_specs, seed, job.input_dists)
-            dev_inputs[key] = upload(host, job.input_specs, device)
-            host_cache[key] = host
+            dev_inputs[key] = upload(generate_tensors(job.input_specs, seed, job.input_dists), job.input_specs, device)
+            if check_numerics:
+                goldens[key] = expected_output(job.func_name, dev_inputs[key])
         meta[kname] = (key, problem_shape(job.func_name, job.input_specs))
-    host_cache.clear()
 
     workers = min(max((os.cpu_count() or 2) - 1, 1), len(kernels), 16)
     compile_results: list[CompileResult] = []
@@ -131,7 +135,16 @@ def run_pipeline(
                 warm_clock(device, clock_warmup_s)
             hw_results.append(benchmark_one(cr.kernel_name, cr.library_path, canonical_name(job.func_name), cfg,
                                             dev_inputs[key], out, M, N, K, warmup, reps, flush_bytes,
-                                            collect_detailed_profile))
+                                            collect_detailed_profile, goldens.get(key)))
             last_gpu = time.perf_counter()
-    logs = {cr.kernel_name: cr.compile_log for cr in compile_results if collect_compiler_logs and cr.compile_log}
+    logs = {}
+    if collect_compiler_logs:
+        for cr in compile_results:
+            text = cr.compile_log
+            ignored = kernels[cr.kernel_name].ignored_args
+            if ignored:
+                note = "ignored (Neuron compiler options with no hipcc counterpart): " + " ".join(ignored)
+                text = f"{text}\n{note}" if text else note
+            if text:
+                logs[cr.kernel_name] = text
     return compile_errors + hw_results, logs

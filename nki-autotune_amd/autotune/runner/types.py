@@ -9,8 +9,9 @@ records and helpers, with the Neuron-specific fields re-read for HIP:
   instantiates the kernel template for one tile config.  The config is
   also carried in a machine-readable header line of that text, so a job is
   fully described by its source, as in the reference (types.py:32-58).
-* ``hipcc_args`` replaces ``neuronx_cc_args``; ``lnc`` (logical device
-  count) must be 1 -- every run uses one GPU.
+* ``neuronx_cc_args`` keeps its name; its command-line flags go to hipcc
+  (``KernelJob.hipcc_args``); ``lnc`` (logical device count) must be 1 --
+  every run uses one GPU.
 * ``ProfileResult.profiler_summary`` is the hipEvent timing summary written
   by ``benchmark.benchmark_one`` (``total_time`` in seconds plus the
   utilisation fractions), in place of the ``neuron-profile`` summary JSON.
@@ -56,12 +57,18 @@ class KernelJob(NamedTuple):
 
     Attributes:
         source: HIP source text of the kernel instance (one tile config).
-        func_name: Kernel family: ``matmul_lhsT_rhs``, ``matmul_lhsT_rhs_f32``
-            or ``rmsnorm_matmul`` (reference names ``matmul_lhsT_rhs_nkigym``
-            and ``rmsnorm_matmul_online`` are accepted as aliases).
+        func_name: Kernel family: ``matmul_lhsT_rhs``, ``matmul_lhsT_rhs_f32``,
+            ``matmul_lhs_rhs`` or ``rmsnorm_matmul`` (the reference names
+            ``matmul_lhsT_rhs_nkigym``, ``matmul_lhs_rhs_nkigym`` and
+            ``rmsnorm_matmul_online`` are accepted as aliases).
         output_shape: Shape of the kernel's output tensor.
         input_specs: Map of param name to (shape, dtype_str), in signature order.
-        hipcc_args: Extra hipcc flags for a just-in-time build of ``source``.
+        neuronx_cc_args: Extra compiler arguments, under the reference's field
+            name.  Entries that are command-line flags (they start with
+            ``-``) go to hipcc for a just-in-time build of ``source``; the
+            Neuron pipeline options the reference's hand kernels pass (such
+            as ``enable-instruction-scheduling=false``) have no hipcc
+            counterpart and are listed as ignored in the compile log.
         lnc: Logical device count; only 1 is supported (one GPU).
         input_dists: Optional per-input distribution ("normal", "uniform",
             ("normal", sigma), "gamma"); default standard normal, as in the
@@ -72,9 +79,19 @@ class KernelJob(NamedTuple):
     func_name: str
     output_shape: tuple[int, ...]
     input_specs: dict[str, tuple[tuple[int, ...], str]]
-    hipcc_args: tuple[str, ...] = ()
+    neuronx_cc_args: tuple[str, ...] = ()
     lnc: int = 1
     input_dists: dict[str, Any] | None = None
+
+    @property
+    def hipcc_args(self) -> tuple[str, ...]:
+        """The entries of ``neuronx_cc_args`` that hipcc takes (command-line flags)."""
+        return tuple(a for a in self.neuronx_cc_args if a.startswith("-"))
+
+    @property
+    def ignored_args(self) -> tuple[str, ...]:
+        """Neuron compiler pipeline options with no hipcc counterpart."""
+        return tuple(a for a in self.neuronx_cc_args if not a.startswith("-"))
 
 
 class CompileResult(NamedTuple):
@@ -117,31 +134,24 @@ class OutputSpec(NamedTuple):
 
 
 def capture_error(exc: BaseException) -> str:
-    """Full traceback of ``exc`` as a string (reference types.py:109-111)."""
-    return "".join(traceback.format_exception(type(exc), exc, exc.__traceback__))
-
-
-def make_failure(kernel_name: str, hardware_output: str) -> ProfileResult:
-    """A failed ProfileResult with no profiler summary."""
-    return ProfileResult(kernel_name=kernel_name, hardware_output=hardware_output)
+    """The formatted traceback of ``exc``: how a per-kernel failure is reported."""
+    return "".join(traceback.TracebackException.from_exception(exc).format())
 
 
 def compile_failure_result(cr: CompileResult) -> ProfileResult:
-    """Convert a failed CompileResult into a ProfileResult."""
-    return make_failure(cr.kernel_name, cr.error)
+    """The ProfileResult of a job that never reached the GPU: its build error, no summary."""
+    return ProfileResult(kernel_name=cr.kernel_name, hardware_output=cr.error)
 
 
 def profiler_percent(summary: dict | None, field: str) -> float | None:
-    """Fractional utilisation field of a summary, scaled to percent.
+    """A utilisation field of a profiler summary (a fraction) in percent.
 
-    Same contract as the reference (types.py:129-143): fields are fractions
-    in [0, 1]; a missing field or a negative sentinel gives ``None``.
+    None when there is no summary, no such field, or the field holds a
+    negative value (the "not measured" sentinel), as callers of the
+    reference's helper expect (types.py:129-143).
     """
-    result: float | None = None
-    if summary is not None:
-        value = summary.get(field)
-        if value is not None:
-            scaled = float(value) * 100.0
-            if scaled >= 0:
-                result = scaled
-    return result
+    value = (summary or {}).get(field)
+    if value is None:
+        return None
+    pct = 100.0 * float(value)
+    return pct if pct >= 0.0 else None

@@ -6,10 +6,12 @@ calls ``profile()``, picks ``min(total_time)`` (:238) and prints the
 compiler baseline beside it (:226-242).  Its candidate generator is an MDP
 over NKI loop transforms; here the action space is the CDNA4 tile grid
 (``kernel_library.legal_configs`` plays ``KernelMDP.legal_actions``,
-nkigym/src/nkigym/environment/mdp.py:44-54).  The winner's numerics are
-checked on the GPU against a float64 torch product of the same inputs with
-the reference's pass criterion (``np.allclose``, kernel_transforms.py:592-596)
-and its reported ``max(|a-e| / (|e| + atol))``.
+nkigym/src/nkigym/environment/mdp.py:44-54).  Every candidate's output is
+checked on the GPU against a float64 torch evaluation of the same inputs
+before selection (:mod:`autotune.runner.golden`: the reference's pass
+criterion ``np.allclose``, kernel_transforms.py:592-596, and its reported
+``max(|a-e| / (|e| + atol))``), and so is the winner again after the
+interleaved refinement.
 
 CLI::
 
@@ -37,14 +39,6 @@ DEFAULT_DISTS = {
     "matmul_lhsT_rhs_f32": {},
     "rmsnorm_matmul": {"lhs": "normal", "gamma": "gamma"},
 }
-# Pass criterion: the reference's np.allclose form (kernel_transforms.py:592-596)
-# with rtol = 1e-2 (the bound the benchmark sets for bf16 inputs).  matmul keeps the
-# reference's absolute floor 5e-3; rmsnorm_matmul scales it with the output
-# (1e-2 * RMS), since rounding the normalised rows to bf16 -- which the
-# reference kernel does as well -- leaves ~1e-3 * RMS of absolute error.
-RTOL = 1e-2
-ATOL = 5e-3
-RMS_ATOL_FRAC = 1e-2
 
 
 class TuneResult(NamedTuple):
@@ -93,14 +87,15 @@ def make_jobs(func_name: str, M: int, N: int, K: int, configs, dists: dict | Non
 
 def check_numerics(func_name: str, cfg, M: int, N: int, K: int, seed: int = 0, dists: dict | None = None,
                    with_gamma: bool = True, library_path: str | None = None) -> dict:
-    """Run ``cfg`` once on seeded inputs and compare with a float64 torch product on the GPU.
+    """Run ``cfg`` once on seeded inputs and compare with a float64 torch evaluation on the GPU
+    (:mod:`autotune.runner.golden`: allclose with rtol 1e-2, plus max_abs / max_rel).
 
     ``library_path`` selects the library holding the instance (default: the
     prebuilt libmi_kernels.so; a just-in-time build for other configs).
     """
     import torch
 
-    import kernel_library as kl
+    from autotune.runner import golden
     from autotune.runner.benchmark import Launcher, generate_tensors, upload
     from kernel_library import _lib
 
@@ -108,37 +103,13 @@ def check_numerics(func_name: str, cfg, M: int, N: int, K: int, seed: int = 0, d
     specs = input_specs(fam, M, N, K, with_gamma=with_gamma)
     dev = upload(generate_tensors(specs, seed, default_dists(fam, K) if dists is None else dists), specs,
                  torch.device("cuda:0"))
-    out = torch.empty((M, N), dtype=torch.float32 if fam.endswith("f32") else torch.bfloat16, device="cuda:0")
+    fp32 = fam.endswith("f32")
+    out = torch.empty((M, N), dtype=torch.float32 if fp32 else torch.bfloat16, device="cuda:0")
     library = _lib.load(library_path) if library_path else _lib.lib()
     Launcher(library, fam, cfg, dev, out, M, N, K)()
     torch.cuda.synchronize()
-    if fam == "rmsnorm_matmul":
-        x, w, g = dev["lhs"], dev["rhs"], dev.get("gamma")
-        xf = x.double()
-        y = xf * torch.rsqrt((xf * xf).mean(dim=1, keepdim=True) + kl.EPS)
-        if g is not None:
-            y = y * g.double()[None, :]
-        exp = y @ w.double()
-        atol = RMS_ATOL_FRAC * float(exp.square().mean().sqrt())
-    elif fam == "matmul_lhs_rhs":
-        a, b = dev["lhs"], dev["rhs"]
-        exp = a.double() @ b.double()
-        atol = ATOL
-    else:
-        a, b = dev["lhs_T"], dev["rhs"]
-        exp = a.double().t() @ b.double()
-        atol = ATOL
-    diff = (out.double() - exp).abs()
-    rep = {
-        "max_abs": float(diff.max()),
-        "max_rel": float((diff / (exp.abs() + atol)).max()),
-        "atol": atol,
-        "rtol": RTOL,
-        "nonfinite": int((~torch.isfinite(out.double())).sum()),
-        "allclose": bool((diff <= atol + RTOL * exp.abs()).all()),
-    }
-    rep["pass"] = rep["allclose"] and rep["nonfinite"] == 0
-    return rep
+    exp, atol = golden.expected_output(fam, dev)
+    return golden.compare(out, exp, atol, golden.rtol_for("float32" if fp32 else "bfloat16"))
 
 
 def refine(func_name: str, M: int, N: int, K: int, configs, seed: int = 0, dists: dict | None = None,
@@ -182,7 +153,7 @@ def refine(func_name: str, M: int, N: int, K: int, configs, seed: int = 0, dists
 def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, cache_dir: str = "",
          check: bool = True, record: bool = False, warmup: int = 10, reps: int = 50, flush_bytes: int = 0,
          dists: dict | None = None, with_gamma: bool = True, allow_jit: bool = True,
-         finalists: int = 6, rounds: int = 5, detailed: bool = False) -> TuneResult:
+         finalists: int = 6, rounds: int = 5, detailed: bool = False, baseline: bool = False) -> TuneResult:
     """Sweep ``configs`` (default: every legal prebuilt config) at (M, N, K) and pick the fastest.
 
     The sweep is ``profile`` (the reference's selection is the min of its
@@ -193,7 +164,12 @@ def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, ca
     library holds (a just-in-time winner is noted beside it), since callers
     of ``kernel_library`` only load that library.  ``detailed`` (with a
     ``cache_dir``) keeps a rocprofv3 kernel trace of every successful config
-    in its folder.
+    in its folder.  Every candidate's output is checked against a float64
+    evaluation of its inputs before selection (a failure is a failure row,
+    never a winner).  ``baseline`` times the vendor path of the same
+    expression on the same inputs (:mod:`autotune.runner.baseline`) and adds
+    it to the output's table and results.json, as the reference prints its
+    compiler baseline beside the tuned kernel (examples/tune_matmul_lhsT_rhs.py:222-242).
     """
     import kernel_library as kl
     from kernel_library.config import TileConfig, record_tuned
@@ -203,7 +179,17 @@ def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, ca
         configs = kl.legal_configs(fam, M, N, K)
     jobs = make_jobs(fam, M, N, K, configs, dists, with_gamma)
     output = profile(jobs, cache_dir, seed, "gfx950", detailed, warmup=warmup, reps=reps, flush_bytes=flush_bytes,
-                     allow_jit=allow_jit)
+                     allow_jit=allow_jit, check_numerics=check)
+    if baseline and not fam.endswith("f32"):
+        from autotune.runner.baseline import profile_torch_baseline
+        from autotune.runner.output import write_results_json
+
+        output.baseline = profile_torch_baseline(
+            M, N, K, seed=seed, warmup=warmup, reps=reps, dists=default_dists(fam, K) if dists is None else dists,
+            kernel_name=f"vendor_{fam}", flush_bytes=flush_bytes, func_name=fam,
+            lhs_layout="MK" if fam == "matmul_lhs_rhs" else "KM")
+        if cache_dir:
+            write_results_json(cache_dir, len(jobs), output.results, output.elapsed_s, output.baseline)
     best_row = output.best
     if best_row is None:
         return TuneResult(None, None, output, None)
@@ -255,7 +241,9 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--flush-mib", type=int, default=0, help="L2/MALL flush buffer before each timed launch")
     ap.add_argument("--record", action="store_true", help="store the winner in kernel_library/tuned_configs.json")
-    ap.add_argument("--baseline", action="store_true", help="also time torch.matmul (hipBLASLt) at the shape")
+    ap.add_argument("--baseline", action="store_true",
+                    help="also time the vendor path at the shape (torch.matmul / hipBLASLt; for rmsnorm_matmul the "
+                         "unfused torch composition) and list it in the results table and results.json")
     ap.add_argument("--configs", default="", help="comma-separated tile config names to time instead of a grid")
     ap.add_argument("--detailed", action="store_true",
                     help="with --cache: keep a rocprofv3 kernel trace of every successful config in its folder")
@@ -283,21 +271,11 @@ def main(argv: list[str] | None = None) -> int:
     # rmsnorm_matmul_online is the reference's contract: no gamma.
     with_gamma = args.kernel != "rmsnorm_matmul_online"
     res = tune(fam, M, N, K, configs, args.seed, args.cache, True, args.record, args.warmup, args.reps,
-               args.flush_mib << 20, with_gamma=with_gamma, detailed=args.detailed)
+               args.flush_mib << 20, with_gamma=with_gamma, detailed=args.detailed, baseline=args.baseline)
     print(res.output)
     if res.best is not None:
         print(f"\n[tune] best {fam} {M}x{N}x{K}: {res.best.name} {res.best_time_s * 1e6:.1f} us "
               f"{2 * M * N * K / res.best_time_s / 1e12:.1f} TFLOP/s; numerics {json.dumps(res.check)}")
-    if args.baseline and fam != "rmsnorm_matmul":
-        from autotune.runner.baseline import profile_torch_baseline
-
-        b = profile_torch_baseline(M, N, K, warmup=args.warmup, reps=args.reps, flush_bytes=args.flush_mib << 20,
-                                   lhs_layout="MK" if fam == "matmul_lhs_rhs" else "KM")
-        s = b.profiler_summary
-        if s:
-            print(f"[tune] hipBLASLt baseline: {s['total_time'] * 1e6:.1f} us {s['tflops']:.1f} TFLOP/s")
-        else:
-            print(f"[tune] hipBLASLt baseline unavailable: {b.hardware_output.splitlines()[-1]}")
     return 0 if res.best is not None and (res.check is None or res.check["pass"]) else 1
 
 

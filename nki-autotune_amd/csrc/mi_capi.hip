@@ -92,7 +92,7 @@ mi::Legal template_legal(int kernel_id, const mi_tile_cfg& c) {
       if (c.variant == 0 || c.variant == 1) return mi::legal_rms_plain(bm, bn, bk, w, s);
       if (c.variant == 4 || c.variant == 5) return mi::legal_rms_xreg(bm, bn, bk, w, s, c.variant - 2);
       if (c.variant == 11 || c.variant == 12) return mi::legal_rms_xreg(bm, bn, bk, w, s, c.variant - 9);
-      if (c.variant == 13) return mi::legal_mm_pipe(bm, bn, bk, w, s, false);
+      if (c.variant == 13) return mi::legal_rms2(bm, bn, bk, w, s);
       break;
     case MI_KERNEL_MATMUL_LHST_RHS_F32:
       // 16 x 16 threads with 4 x 4 outputs each, K slices of 16 or 32.

@@ -741,6 +741,26 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   // buffer that is never read again costs STAGES-1 tiles of bandwidth.
   auto clamp = [&](int kt) { return kt < KT ? kt : KT - 1; };
 
+  // Row scale (two-pass fused kernel): 1/sqrt(sum_p ssq[p][m] * inv_k + eps)
+  // for each row m of the block, p in order, into LDS past the panels
+  // (rs_lds, BM floats; the caller allocates them).  Each thread takes
+  // rows tid, tid + NT, ...; the first RSB partial sums of its rows are
+  // loaded before the prologue's panel loads, so they arrive with the first
+  // tiles, and summed after the prologue's wait.
+  constexpr int NTH = WAVES * 64, RSB = 8, RPT = RS && !SPLIT ? (BM + NTH - 1) / NTH : 1;
+  float* rs_lds = (float*)(smem + C::LDS_BYTES);
+  float rpart[RPT][RSB];
+  auto load_parts = [&](int p0) {
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int r = tid + j * NTH, m = m0 + r;
+#pragma unroll
+      for (int q = 0; q < RSB; ++q)
+        rpart[j][q] = (r < BM && m < M && p0 + q < rsc.parts) ? rsc.ssq[(size_t)(p0 + q) * (size_t)M + m] : 0.0f;
+    }
+  };
+  if constexpr (RS && !SPLIT) load_parts(0);
+
   // Prologue: tiles 0 .. STAGES-1 in flight, wait for tile 0.
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
@@ -748,6 +768,24 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
     for (int q = 0; q < LPT; ++q) issue_one(q, clamp(s), s);
   vm_wait<(STAGES - 1) * LPT>();
   __syncthreads();
+  if constexpr (RS && !SPLIT) {
+    // The compiler's wait for the partial sums drains the prologue's panel
+    // loads too (they were issued after them); no load is in flight after.
+    float rsum[RPT];
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) rsum[j] = 0.0f;
+    for (int p0 = 0;; p0 += RSB) {
+#pragma unroll
+      for (int j = 0; j < RPT; ++j)
+#pragma unroll
+        for (int q = 0; q < RSB; ++q) rsum[j] += rpart[j][q];
+      if (p0 + RSB >= rsc.parts) break;
+      load_parts(p0 + RSB);
+    }
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+      if (tid + j * NTH < BM) rs_lds[tid + j * NTH] = 1.0f / __builtin_sqrtf(rsum[j] * rsc.inv_k + rsc.eps);
+  }
   read_frags(0, 0, 0);
 
   // Steady state: every tile but the last.  At the last sub-step the wave
@@ -787,25 +825,6 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
     return true;
   });
   const int cur = (KT - 1) % STAGES;
-  // Row scale (two-pass fused kernel): lane l scales row l%32 of each of its
-  // 32-row fragments by 1/sqrt(sum_p ssq[p][m] * inv_k + eps), p in order.
-  // The first RSB partial sums of its rows are loaded here, so that they fly
-  // during the last tile's MFMAs (no load is issued after them, so the
-  // compiler's wait for them is the final vmcnt(0) below); further ones are
-  // loaded RSB at a time in the epilogue.
-  constexpr int RSB = 8;
-  float rsum[TM];
-  float rpart[RS ? TM : 1][RS ? RSB : 1];
-  auto load_parts = [&](int p0) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int m = m0 + wm0 + i * 32 + (lane & 31);
-#pragma unroll
-      for (int q = 0; q < RSB; ++q)
-        rpart[i][q] = (m < M && p0 + q < rsc.parts) ? rsc.ssq[(size_t)(p0 + q) * (size_t)M + m] : 0.0f;
-    }
-  };
-  if constexpr (RS && !SPLIT) load_parts(0);
   // Last tile: no further loads.
 #pragma unroll
   for (int kk = 0; kk < KS; ++kk) {
@@ -822,21 +841,7 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   }
   float scale[TM];
 #pragma unroll
-  for (int i = 0; i < TM; ++i) scale[i] = 1.0f;
-  if constexpr (RS) {
-#pragma unroll
-    for (int i = 0; i < TM; ++i) rsum[i] = 0.0f;
-    for (int p0 = 0;; p0 += RSB) {
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int q = 0; q < RSB; ++q) rsum[i] += rpart[i][q];
-      if (p0 + RSB >= rsc.parts) break;
-      load_parts(p0 + RSB);
-    }
-#pragma unroll
-    for (int i = 0; i < TM; ++i) scale[i] = 1.0f / __builtin_sqrtf(rsum[i] * rsc.inv_k + rsc.eps);
-  }
+  for (int i = 0; i < TM; ++i) scale[i] = RS ? rs_lds[wm0 + i * 32 + (lane & 31)] : 1.0f;
   store_tile<TM, TN, WAVES>(acc, scale, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
 }
 

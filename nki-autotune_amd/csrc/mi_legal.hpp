@@ -128,6 +128,18 @@ MI_HD constexpr Legal legal_mm_pipe(int bm, int bn, int bk, int waves, int stage
   return ok();
 }
 
+// ---- main pass of the two-pass fused kernel (rmsnorm_matmul variant 13):
+// the pipelined lhsT.rhs core plus the block's BM row scales in LDS.
+MI_HD constexpr int lds_rms2(int bm, int bn, int bk, int waves, int stages) {
+  return lds_mm_pipe(bm, bn, bk, waves, stages) + bm * 4;
+}
+MI_HD constexpr Legal legal_rms2(int bm, int bn, int bk, int waves, int stages) {
+  const Legal core = legal_mm_pipe(bm, bn, bk, waves, stages, false);
+  if (core.code != MI_OK) return core;
+  if (lds_rms2(bm, bn, bk, waves, stages) > kLdsBytesMax) return bad(MI_E_LDS, "LDS over 160 KiB");
+  return ok();
+}
+
 // ---- lhsT.rhs with a register prefetch ring (matmul variant 2); `stages`
 // is the ring depth, the LDS holds two stages.
 MI_HD constexpr int lds_mm_reg(int bm, int bn, int bk, int waves) {

@@ -303,7 +303,7 @@ hipError_t launch_rms_2pass(const MiArgs& a, hipStream_t s) {
    &launch_rms_xreg<BM, BN, BK, W, S, XS, true>, XregCfg<BM, BN, BK, W, S>::GK_MAX},
 
 #define MI_RMS2_ROW(BM, BN, BK, W, S)                                                               \
-  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 13}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 13}, lds_rms2(BM, BN, BK, W, S),         \
    &launch_rms_2pass<BM, BN, BK, W, S>},
 
 // The 72-point search grid for one (BM, BN): BK in {32,64} x waves in {4,8} x

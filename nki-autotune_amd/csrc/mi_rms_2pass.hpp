@@ -11,8 +11,10 @@
 //   pass 1, rms_pack_kernel: xt[k][m] = bf16(x[m][k] * gamma[k]) -- the
 //     lhsT layout -- and ssq[p][m] = sum of x[m][k]^2 over the columns
 //     k of chunk p (RP_KCH columns per chunk), in fp32;
-//   pass 2, the pipelined lhsT.rhs core on (xt, W); its epilogue multiplies
-//     output row m by 1/sqrt(sum_p ssq[p][m] / K + eps) (part order).
+//   pass 2, the pipelined lhsT.rhs core on (xt, W); each workgroup sums its
+//     rows' partial sums (part order) while its first K tiles load, keeps
+//     1/sqrt(sum / K + eps) per row in LDS, and its epilogue multiplies the
+//     fp32 accumulators of output row m by it.
 //
 // The arithmetic is that of the one-pass variants: x*gamma rounded once to
 // bf16 (the operand the MFMAs see), fp32 accumulation over the whole K, and
@@ -124,13 +126,16 @@ __global__ __launch_bounds__(RP_WAVES * 64) void rms_pack_kernel(const uint16_t*
 
 // Pass 2: the pipelined lhsT.rhs core on (xt, W) with the rms row scale in
 // the epilogue; SPLIT: fp32 partial products to ws, scaled by the second
-// pass of split-K (splitk_rms_sum_kernel).
+// pass of split-K (splitk_rms_sum_kernel) instead.
 template <int BM, int BN, int BK, int WAVES, int STAGES, bool SPLIT = false>
 __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_2pass_kernel(
     const uint16_t* __restrict__ xt, const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int M, int N, int K,
     int group_m, int parts, float* __restrict__ ws, const float* __restrict__ ssq, int ssq_parts, float inv_k,
     float eps) {
-  __shared__ __attribute__((aligned(1024))) char smem[PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
+  // The pipelined core's LDS, then the block's BM row scales.
+  static_assert(lds_rms2(BM, BN, BK, WAVES, STAGES) == PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES + BM * 4,
+                "host LDS budget out of step");
+  __shared__ __attribute__((aligned(1024))) char smem[lds_rms2(BM, BN, BK, WAVES, STAGES)];
   mm_pipe_body<BM, BN, BK, WAVES, STAGES, false, false, SPLIT, true>(xt, w, out, M, N, K, group_m, smem,
                                                                      SplitK{parts, ws},
                                                                      RowScale{ssq, ssq_parts, inv_k, eps});

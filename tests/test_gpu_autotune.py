@@ -67,6 +67,15 @@ def test_profile_sweep_selection_failures_and_traces(gpu, tmp_path):
         assert "error" not in row, row
         assert row["calls"] == 2 + 5 and row["avg_ns"] > 0
         assert os.path.exists(os.path.join(folder, "rocprof", "run_kernel_stats.csv"))
+        # counter passes: measured MFMA busy, engine clock and HBM-side bytes
+        c = detailed["counters"]
+        print(stem, {k: c.get(k) for k in ("mfma_busy_percent", "engine_clock_mhz", "hbm_gbps", "error")},
+              flush=True)
+        assert "error" not in c, c
+        compulsory = (M * K + K * N + M * N) * 2
+        assert 0.5 * compulsory < c["hbm_bytes"] < 64 * compulsory, (c["hbm_bytes"], compulsory)
+        assert times[r.kernel_name]["hbm_gbps_measured"] == pytest.approx(c["hbm_gbps"])
+        assert "engine_clock_mhz" not in c and "note" in c     # 512^3 calls are too short to clock
 
     # the JIT-built library computes the same product
     specs = input_specs("matmul_lhsT_rhs", M, N, K)
@@ -87,9 +96,143 @@ def test_profile_sweep_selection_failures_and_traces(gpu, tmp_path):
     assert rep["ok"], rep
 
 
+def test_counters_of_a_long_kernel(gpu, tmp_path):
+    """The counter passes on a call long enough to clock (4096^3, ~100 us):
+    MFMA busy, engine clock and HBM bytes in physical ranges, and in
+    results.json beside the timing."""
+    from autotune.runner.api import profile
+    from autotune.tune import make_jobs
+    from kernel_library.config import TileConfig
+
+    M = N = K = 4096
+    jobs = make_jobs("matmul_lhsT_rhs", M, N, K, [TileConfig(256, 256, 32, 4, 3, variant=1)])
+    cache = str(tmp_path / "cache")
+    out = profile(jobs, cache, 0, "gfx950", True, warmup=3, reps=10)
+    r = out.results[0]
+    assert r.hardware_output.startswith("["), r.hardware_output
+    c = r.profile_detailed["counters"]
+    print("4096^3 counters", {k: c.get(k) for k in ("mfma_busy_percent", "engine_clock_mhz", "hbm_gbps")},
+          flush=True)
+    assert "error" not in c, c
+    assert 20.0 < c["mfma_busy_percent"] <= 100.0
+    assert 500.0 < c["engine_clock_mhz"] <= 2450.0
+    compulsory = 3 * M * N * 2
+    assert 0.9 * compulsory < c["hbm_bytes"] < 16 * compulsory
+    doc = json.load(open(os.path.join(cache, "results.json")))
+    assert doc["kernels"][0]["mfma_busy_percent"] == pytest.approx(c["mfma_busy_percent"])
+    assert doc["kernels"][0]["engine_clock_mhz"] == pytest.approx(c["engine_clock_mhz"])
+    assert "busy" in str(out) and "MHz" in str(out)
+
+
 def test_tune_picks_a_passing_winner(gpu):
     from autotune.tune import tune
 
     res = tune("matmul_lhs_rhs", 1024, 1024, 1024, reps=5, warmup=2, finalists=3, rounds=2)
     assert res.best is not None and res.check["pass"], res.check
     assert res.best_time_s > 0
+
+
+def test_vendor_baseline_matches_oracle(gpu):
+    """The vendor rows (hipBLASLt for the matmuls; torch's unfused rmsnorm then
+    hipBLASLt for the fused kernel) compute the same function as the kernels:
+    their outputs against the oracle's float64 closed forms."""
+    import torch
+
+    from autotune.runner.baseline import profile_torch_baseline
+    from autotune.runner.benchmark import generate_tensors
+    from autotune.tune import default_dists, input_specs
+    from helpers import rms_check
+    from oracle import rmsnorm as orms
+
+    M, N, K = 256, 384, 512
+    for fam in ("matmul_lhsT_rhs", "matmul_lhs_rhs", "rmsnorm_matmul"):
+        print("vendor baseline", fam, flush=True)
+        dists = default_dists(fam, K)
+        out = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+        r = profile_torch_baseline(M, N, K, seed=3, warmup=2, reps=5, dists=dists, func_name=fam, out=out,
+                                   lhs_layout="MK" if fam == "matmul_lhs_rhs" else "KM")
+        assert r.hardware_output.startswith("["), r.hardware_output
+        assert r.profiler_summary["numerics"]["pass"], r.profiler_summary["numerics"]
+        host = {k: torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+                for k, v in generate_tensors(input_specs(fam, M, N, K), 3, dists).items()}
+        got = out.float().cpu().numpy()
+        if fam == "matmul_lhsT_rhs":
+            rep = mm_check(got, omm.closed_form(host["lhs_T"], host["rhs"]))
+        elif fam == "matmul_lhs_rhs":
+            rep = mm_check(got, omm.closed_form(host["lhs"].T, host["rhs"]))
+        else:
+            rep = rms_check(got, orms.closed_form(host["lhs"], host["rhs"], host["gamma"]))
+        assert rep["ok"], (fam, rep)
+
+
+def test_tune_from_frontier_sample_and_gate(gpu, tmp_path):
+    """The frontier sampler's configs (prebuilt and just-in-time built) go
+    through tune(): none is a compile error, every success passed the
+    numerics gate, the winner matches the oracle, and the vendor row is in
+    results.json beside them."""
+    import numpy as np
+    import torch
+
+    import kernel_library as kl
+    from autotune.runner.benchmark import Launcher, generate_tensors, upload
+    from autotune.search import TileMDP, frontier_sample
+    from autotune.tune import default_dists, input_specs, tune
+    from kernel_library import _lib
+
+    M, N, K = 512, 768, 1024
+    cfgs = frontier_sample(TileMDP("matmul_lhsT_rhs", M, N, K), 10, seed=3)
+    print("frontier sample", [c.name for c in cfgs], flush=True)
+    cache = str(tmp_path / "tune")
+    res = tune("matmul_lhsT_rhs", M, N, K, cfgs, cache_dir=cache, warmup=2, reps=5, finalists=3, rounds=2,
+               baseline=True)
+    for r in res.output.results:
+        assert "hipcc failed" not in r.hardware_output and "illegal config" not in r.hardware_output, r
+    assert res.best is not None and res.check["pass"], res.check
+    for r in res.output.results:
+        if r.profiler_summary:
+            assert r.profiler_summary["numerics"]["pass"]
+    doc = json.load(open(os.path.join(cache, "results.json")))
+    assert doc["baseline"]["kernel_name"] == "vendor_matmul_lhsT_rhs"
+    assert doc["baseline"]["numerics"]["pass"]
+    assert doc["metrics"]["best_speedup_vs_baseline"] > 0
+    winner = next(r for r in res.output.results if r.profiler_summary and
+                  kl.TileConfig(**r.profiler_summary["config"]) == res.best)
+    specs = input_specs("matmul_lhsT_rhs", M, N, K)
+    host = generate_tensors(specs, 0, default_dists("matmul_lhsT_rhs", K))
+    dev = upload(host, specs, gpu)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+    Launcher(_lib.load(winner.profiler_summary["library"]), "matmul_lhsT_rhs", res.best, dev, out, M, N, K)()
+    torch.cuda.synchronize()
+    a = dev["lhs_T"].float().cpu().numpy()
+    b = dev["rhs"].float().cpu().numpy()
+    rep = mm_check(out.float().cpu().numpy(), omm.closed_form(a, b))
+    assert rep["ok"], rep
+    assert np.isfinite(out.float().cpu().numpy()).all()
+
+
+def test_gate_turns_a_wrong_output_into_a_failure_row(gpu):
+    """A candidate whose output disagrees with the golden is a failure row
+    with its report, not a success.  The mistake is planted in the golden
+    (the host-side expected values, doubled); the kernel is correct."""
+    import torch
+
+    from autotune.runner import golden
+    from autotune.runner.benchmark import benchmark_one, generate_tensors, upload
+    from autotune.runner.types import OutputSpec
+    from autotune.tune import default_dists, input_specs
+    from kernel_library import _lib
+    from kernel_library.config import TileConfig
+
+    M = N = K = 256
+    specs = input_specs("matmul_lhsT_rhs", M, N, K)
+    dev = upload(generate_tensors(specs, 0, default_dists("matmul_lhsT_rhs", K)), specs, gpu)
+    exp, atol = golden.expected_output("matmul_lhsT_rhs", dev)
+    cfg = TileConfig(128, 128, 64, 4, 2, variant=1)
+    spec = OutputSpec("out", (M, N), "bfloat16")
+    good = benchmark_one("good.hip", str(_lib.LIB_PATH), "matmul_lhsT_rhs", cfg, dev, spec, M, N, K, 1, 3,
+                         golden=(exp, atol))
+    assert good.hardware_output.startswith("[") and good.profiler_summary["numerics"]["pass"]
+    bad = benchmark_one("bad.hip", str(_lib.LIB_PATH), "matmul_lhsT_rhs", cfg, dev, spec, M, N, K, 1, 3,
+                        golden=(exp * 2, atol))
+    assert bad.profiler_summary is None and bad.hardware_output.startswith("numerics check failed")
+    torch.cuda.synchronize()

@@ -204,7 +204,53 @@ def test_profile_requires_a_gfx950_device(tmp_path):
     with pytest.raises(RuntimeError, match="HIP device"):
         profile(jobs, str(tmp_path / "cache"), 0)
     with pytest.raises(ValueError):
-        profile(jobs, "", 0, platform_target="trn2")
+        profile(jobs, "", 0, neuron_platform_target="sm_90")
+
+
+def test_profile_takes_the_reference_call(tmp_path, monkeypatch):
+    """The reference's drivers call ``profile(jobs, cache_dir=..., seed=...,
+    neuron_platform_target=..., collect_detailed_profile=...)`` with jobs
+    built as ``KernelJob(..., neuronx_cc_args=...)``
+    (examples/tune_matmul_lhsT_rhs.py:259-265; examples/profile_hand_90mfu.py:
+    101-111): the same call, word for word, runs here.  The pipeline is
+    replaced by a recorder (no GPU on this host)."""
+    from autotune.runner import api
+    from autotune.runner.output import ProfileOutput
+
+    seen = {}
+
+    def recorder(kernels, **kw):
+        seen.update(kw, kernels=kernels)
+        return [], {}
+
+    monkeypatch.setattr(api, "run_pipeline", recorder)
+    M = N = K = 2048
+    input_specs_ref = {"lhs_T": ((K, M), "bfloat16"), "rhs": ((K, N), "bfloat16")}
+    neuronx_cc_args = ("enable-linear-scan-allocation=false", "enable-instruction-scheduling=false")
+    jobs = {
+        "hand_90mfu": KernelJob(
+            source=rcompile.render_source("matmul_lhsT_rhs_nkigym", TileConfig(256, 256, 32, 4, 3, variant=1)),
+            func_name="matmul_lhsT_rhs_nkigym",
+            output_shape=(M, N),
+            input_specs=input_specs_ref,
+            neuronx_cc_args=neuronx_cc_args,
+        )
+    }
+    cache_dir = str(tmp_path / "profile_hand_90mfu")
+    output = api.profile(
+        jobs,
+        cache_dir=cache_dir,
+        seed=0,
+        neuron_platform_target="trn2",
+        collect_detailed_profile=False,
+    )
+    assert isinstance(output, ProfileOutput) and output.results == [] and output.cache_dir == cache_dir
+    assert seen["kernels"] is jobs and seen["seed"] == 0 and seen["collect_detailed_profile"] is False
+    job = jobs["hand_90mfu"]
+    assert job.hipcc_args == () and job.ignored_args == neuronx_cc_args     # Neuron options: not hipcc flags
+    assert KernelJob(job.source, job.func_name, (M, N), input_specs_ref, ("-DX=1", "opt=1")).hipcc_args == ("-DX=1",)
+    assert (tmp_path / "profile_hand_90mfu" / "hand_90mfu" / "hand_90mfu.hip").exists()
+    assert api.resolve_target("gfx950") == api.resolve_target("trn2") == "gfx950"
 
 
 def test_make_jobs_and_cache_sources(tmp_path):
@@ -264,7 +310,8 @@ def test_detailed_profile_trace_helpers(tmp_path, monkeypatch):
     assert "pipe_kernel" in row["kernel"] and [r["calls"] for r in row["kernels"]] == [110, 110]
     monkeypatch.setattr(tr.shutil, "which", lambda name: None)
     assert "not found" in tr.trace_kernel(str(tmp_path / "k0"), path)["error"]
-    assert replay_main([]) == 2
+    with pytest.raises(SystemExit):          # usage error: no replay file
+        replay_main([])
 
 
 def test_tune_cli_named_configs_and_detailed_needs_cache(monkeypatch):
@@ -290,3 +337,82 @@ def test_tune_cli_named_configs_and_detailed_needs_cache(monkeypatch):
     assert seen["fam"] == "rmsnorm_matmul" and seen["with_gamma"] is False
     tmod.main(["--kernel", "rmsnorm_matmul", "--shape", "256", "256", "512"])
     assert seen["with_gamma"] is True
+
+
+def test_baseline_row_numerics_failures_and_counters(tmp_path):
+    """The results model renders the vendor baseline row and the measured
+    counters in the table and results.json, and a numerics failure is a
+    failure row, never a selectable success."""
+    from autotune.runner.output import ResultsModel, natural_key
+
+    fast, slow = TileConfig(256, 256, 32, 4, 3, variant=1), TileConfig(128, 128, 64, 4, 2, variant=1)
+    a = _summary_result("fast.hip", 0.0010, 0.6, fast)
+    a = a._replace(profile_detailed={"counters": {"mfma_busy_percent": 87.5, "hbm_gbps": 2100.0,
+                                                  "engine_clock_mhz": 1620.0}})
+    b = _summary_result("slow.hip", 0.0020, 0.3, slow)
+    wrong = ProfileResult("wrong.hip", "numerics check failed: max_abs 3.2, max_rel 0.8 (atol 0.005, rtol 0.01), 0 "
+                                       "non-finite values")
+    base = ProfileResult("vendor_matmul_lhsT_rhs", "[256, 256] bfloat16",
+                         {"total_time": 0.0015, "mfu_estimated_percent": 0.4, "tflops": 1.0,
+                          "library": "torch.matmul (hipBLASLt)"})
+    out = ProfileOutput([a, b, wrong], {}, 1.0, baseline=base)
+    assert out.best.kernel_name == "fast.hip" and len(out.successes) == 2
+    assert [r.kernel_name for r in out.failures] == ["wrong.hip"]
+    text = str(out)
+    assert "vendor_matmul_lhsT_rhs" in text and "1.500x faster" in text
+    assert "87.5%" in text and "1620" in text
+    write_results_json(str(tmp_path), 3, out.results, 1.0, base)
+    doc = json.loads((tmp_path / "results.json").read_text())
+    assert doc["metrics"]["numerics_mismatch"] == 1 and doc["metrics"]["success"] == 2
+    assert doc["metrics"]["best_speedup_vs_baseline"] == pytest.approx(1.5)
+    assert doc["baseline"]["library"] == "torch.matmul (hipBLASLt)"
+    row = next(k for k in doc["kernels"] if k["kernel_name"] == "fast.hip")
+    assert row["mfma_busy_percent"] == 87.5 and row["engine_clock_mhz"] == 1620.0
+    assert (tmp_path / "vendor_matmul_lhsT_rhs" / "profile_summary.json").exists()
+    # natural order: digit runs by value
+    names = ["k_10", "k_2", "bm256_x", "bm64_x"]
+    assert sorted(names, key=natural_key) == ["bm64_x", "bm256_x", "k_2", "k_10"]
+    assert ResultsModel.of([]).fastest() is None
+
+
+def test_counter_parsing_and_derivation(tmp_path):
+    """Counter passes -> per-call figures: calls grouped over the instance's
+    kernels (a split call has two), the warm-up call dropped, the median
+    call kept, byte counters scaled by the device copy before the first
+    kernel, MFMA busy = busy cycles per SIMD over active cycles per XCD,
+    clock = active cycles per XCD over the call's duration."""
+    from autotune.runner.trace import CALIBRATE_MIB, derive, per_call_counters, read_counter_csv
+
+    def csv_of(rows):
+        head = '"Dispatch_Id","Kernel_Name","Counter_Name","Counter_Value","Start_Timestamp","End_Timestamp"\n'
+        return head + "".join(f'{i},"{n}","{c}",{v},{s},{e}\n' for i, n, c, v, s, e in rows)
+
+    cal = CALIBRATE_MIB << 20
+    rows = [(1, "__amd_rocclr_copyBuffer", "FETCH_SIZE", cal / 1024 / 2, 0, 100)]   # reads count half
+    t = 1000
+    for call in range(4):                      # warm-up + 3 timed calls, 2 kernels each
+        ns = (1000, 3000, 2000, 2500)[call]
+        for k, frac in (("mi::main_kernel<1>(int)", 0.75), ("mi::sum_kernel<0>(float)", 0.25)):
+            d = 2 + 2 * call + (k.startswith("mi::sum"))
+            dur = int(ns * frac)
+            rows += [(d, k, "GRBM_GUI_ACTIVE", 8 * 1.6 * dur, t, t + dur),
+                     (d, k, "SQ_VALU_MFMA_BUSY_CYCLES", 1024 * 0.8 * 1.6 * dur if "main" in k else 0, t, t + dur),
+                     (d, k, "FETCH_SIZE", 1000.0, t, t + dur)]
+            t += dur + 10
+    p = tmp_path / "c.csv"
+    p.write_text(csv_of(rows))
+    pc = per_call_counters(read_counter_csv(str(p)), calls=4, calibrate_bytes=cal)
+    assert pc["ns"] == 2500 and pc["scale"]["FETCH_SIZE"] == pytest.approx(2.0)
+    assert pc["counters"]["FETCH_SIZE"] == 2000.0 and len(pc["kernels"]) == 2
+    pc2 = {**pc, "counters": {"WRITE_SIZE": 500.0}, "scale": {"WRITE_SIZE": 1.0}}
+    short = derive([pc, pc2])
+    assert "engine_clock_mhz" not in short and "note" in short and short["hbm_gbps"] > 0   # a 2.5 us call
+    pc = {**pc, "ns": pc["ns"] * 40, "counters": {k: v * 40 for k, v in pc["counters"].items()}}
+    pc2 = {**pc2, "ns": pc["ns"]}
+    d = derive([pc, pc2])
+    assert d["engine_clock_mhz"] == pytest.approx(1600.0)
+    assert d["mfma_busy_percent"] == pytest.approx(80.0 * 0.75)
+    assert d["hbm_bytes"] == pytest.approx(40 * 2000 * 1024 * 2.0 + 500 * 1024)
+    assert d["hbm_gbps"] == pytest.approx(d["hbm_bytes"] / pc["ns"])
+    with pytest.raises(ValueError):
+        per_call_counters(read_counter_csv(str(p)), calls=3, calibrate_bytes=cal)
