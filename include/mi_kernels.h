@@ -7,10 +7,12 @@
  * KernelJob source text.  Each entry point below replaces one reference
  * interface; the citation names it.  All pointers are device pointers owned
  * by the caller; tensors are row-major and contiguous.  bf16 tensors are
- * passed as raw 16-bit storage.  Launches are asynchronous on `stream`
- * (a hipStream_t, NULL = default stream).  No entry point throws, and only
- * a split-K call (tile config split_k > 1) allocates device memory: its
- * workspace, stream-ordered from a library-owned pool (see split_k below).
+ * passed as raw 16-bit storage; bf16 operands must be 16-byte aligned
+ * (fp32 ones 4-byte aligned).  Launches are asynchronous on `stream` (a
+ * hipStream_t, NULL = default stream).  No entry point throws, and only a
+ * call that needs device workspace allocates: a split-K config (split_k >
+ * 1) and the two-pass fused kernel (rmsnorm_matmul variant 13) take it
+ * stream-ordered from a library-owned pool (see split_k below).
  *
  * Return value: 0 on success; a positive MI_E_* legality code when the
  * request is rejected before launch; a negative value (-hipError_t) when the
@@ -39,12 +41,14 @@ enum {
   MI_E_NO_INSTANCE = 1,    /* the tile config was not compiled into this library     */
   MI_E_LDS = 2,            /* LDS bytes of the config exceed 160 KiB                 */
   MI_E_WAVE_TILE = 3,      /* a wave's share of the block is smaller than one MFMA   */
-  MI_E_ALIGN = 4,          /* M or N (or K of a K-contiguous operand) not a multiple of 8 */
+  MI_E_ALIGN = 4,          /* M or N (or K of a K-contiguous operand) not a multiple of 8,
+                              or a pointer not 16-byte aligned (4-byte for fp32)     */
   MI_E_RANGE = 5,          /* an operand is 4 GiB or larger (32-bit buffer offsets)  */
   MI_E_ARGS = 6,           /* null pointer, non-positive size, bad eps               */
   MI_E_KERNEL = 7,         /* unknown kernel id                                      */
   MI_E_SPLIT = 8,          /* split_k unsupported for this kernel / shape            */
-  MI_E_TILE = 9            /* block sizes outside the template's power-of-two range  */
+  MI_E_TILE = 9            /* tile parameters the variant's template does not take, or
+                              no such variant                                        */
 };
 
 /*
@@ -59,19 +63,22 @@ enum {
  *   split_k                   : K split over this many workgroups per output
  *                               tile (1..16; > 1 only for the pipelined matmul
  *                               body: lhsT variants 1 and 3, matmul_lhs_rhs
- *                               variants 0 and 2, and the register-staged
- *                               fused kernel: rmsnorm_matmul variants 4, 5, 11,
- *                               12, whose gamma limit then applies per part;
+ *                               variants 0 and 2, and the fused kernels on it:
+ *                               rmsnorm_matmul variants 4, 5, 11, 12 -- whose
+ *                               gamma limit then applies per part -- and 13;
  *                               every part must get at least one K tile).  The
  *                               parts write fp32 partial products (and, fused,
  *                               their rows' sums of squares) to a workspace
- *                               (split_k * (M * N + M) * 4 bytes, at most
- *                               2 GiB) that the call allocates
- *                               stream-ordered from a library-owned memory
- *                               pool and frees after the launch; a second
- *                               kernel sums them in part order into out (and
- *                               applies 1/rms, fused).  Under
- *                               HIP graph capture the workspace becomes
+ *                               (split_k * (M * N + M) * 4 bytes) that the
+ *                               call allocates stream-ordered from a
+ *                               library-owned memory pool and frees after the
+ *                               launch; a second kernel sums them in part
+ *                               order into out (and applies 1/rms, fused).
+ *                               A call's workspace is at most 2 GiB; the pool
+ *                               keeps at most 256 MiB of freed workspace
+ *                               cached per device and returns the rest to
+ *                               the device at the next synchronisation.
+ *                               Under HIP graph capture the workspace becomes
  *                               allocation and free nodes of the graph.
  *   group_m                   : L2 raster group height in tiles (0 = default 8)
  *   variant                   : kernel-specific pipeline (every variant computes
@@ -84,12 +91,15 @@ enum {
  *                    tiles per load (block_k 32 or 64); 2 as 0 with rhs read
  *                    non-temporally (skinny M)
  *     rmsnorm_matmul 0 / 1 x scaled while staged (1/rms on the accumulators /
- *                    from a prologue pass); 2 / 3 LDS ring of raw x; 4 / 5 x
- *                    through a 2 / 3 tile register ring on the pipelined
- *                    matmul core; 6..9 x loaded straight into MFMA operands
- *                    (need K <= 16384 - D*block_k); 10 x loaded two K tiles
- *                    per instruction (block_k 32, K <= 16384 - 4*block_k);
- *                    11 / 12 as 4 / 5 with W read non-temporally (skinny M)
+ *                    from a prologue pass); 4 / 5 x through a 2 / 3 tile
+ *                    register ring on the pipelined matmul core (gamma staged
+ *                    in LDS: K up to 8192 per part); 11 / 12 as 4 / 5 with W
+ *                    read non-temporally (skinny M); 13 two passes: a pack
+ *                    kernel writes bf16(x * gamma) in the lhsT layout and
+ *                    the rows' sums of squares to the workspace (K * M * 2 +
+ *                    ceil(K / 512) * M * 4 bytes), then the pipelined lhsT
+ *                    core applies 1/rms to its fp32 accumulators.  Variants
+ *                    2, 3 and 6..10 do not exist (MI_E_TILE).
  */
 typedef struct {
   int block_m, block_n, block_k, waves, lds_stages, split_k, group_m, variant;
@@ -108,8 +118,9 @@ int mi_get_config(int kernel_id, int idx, mi_tile_cfg* cfg);
 
 /* The library's default config for a kernel at a shape: always prebuilt and
  * legal there.  Generalised from the autotune winners: non-temporal variants
- * for skinny M, split-K for few output tiles with a long K (and for the fused
- * kernel past the K its gamma staging holds). */
+ * for skinny M, split-K for few output tiles with a long K; for the fused
+ * kernel past the K its gamma staging holds, the two-pass kernel when there
+ * are many output tiles and split-K otherwise. */
 int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
 
 /* out[M,N] = lhsT[K,M]^T . rhs[K,N]; bf16 storage, fp32 accumulation over

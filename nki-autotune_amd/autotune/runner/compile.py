@@ -31,16 +31,13 @@ import threading
 from pathlib import Path
 
 from autotune.runner.types import CompileResult, capture_error
+from kernel_library.config import REFERENCE_NAMES
 
 HEADER_TAG = "// mi-autotune-instance: "
 COMPILE_TIMEOUT_S = 600
 
 # func_name aliases: the reference's kernel names map onto the MI355X families.
-ALIASES = {
-    "matmul_lhsT_rhs_nkigym": "matmul_lhsT_rhs",
-    "matmul_lhs_rhs_nkigym": "matmul_lhs_rhs",
-    "rmsnorm_matmul_online": "rmsnorm_matmul",
-}
+ALIASES = REFERENCE_NAMES
 
 # Kernel families a single-config library can be generated for (fp32: no).
 _JIT_FAMILIES = ("matmul_lhsT_rhs", "matmul_lhs_rhs", "rmsnorm_matmul")

@@ -239,11 +239,18 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
     else if (mid) c = {128, 128, 64, 4, 3, 1, 8, 0};
     else c = {256, 256, 32, 8, 3, 1, 8, 1};
   } else if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16) {
-    // The register-staged kernels keep gamma in LDS (8192 entries here):
-    // past K = 8192 they split K into the fewest parts whose gamma fits
+    // The register-staged kernels keep gamma in LDS (8192 entries here).
+    // Past K = 8192, shapes with many output tiles take the two-pass kernel
+    // (variant 13: its main pass is the lhsT core, with no gamma limit and
+    // no split); the others split K into the fewest parts whose gamma fits
     // (1..16 parts, none empty); past that the LDS-staged kernel (variant 0)
     // takes any K.
-    if (K > 8192) {
+    const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
+    const mi_tile_cfg two_pass = mid ? mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, 13} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, 13};
+    if (K > 8192 && M > 128 && t128 >= 256 &&
+        mi::workspace_bytes(MI_KERNEL_RMSNORM_MATMUL_BF16, two_pass, M, N, K) <= kMaxWorkspace) {
+      c = two_pass;
+    } else if (K > 8192) {
       const long long kt = (K + 63) / 64;
       int parts = 0;
       for (int p = 2; p <= 16 && !parts; p *= 2) {

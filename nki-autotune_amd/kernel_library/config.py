@@ -99,11 +99,25 @@ class TileConfig:
         return asdict(self)
 
 
+# The reference's kernel names, and the family each one is.
+REFERENCE_NAMES = {
+    "matmul_lhsT_rhs_nkigym": "matmul_lhsT_rhs",
+    "matmul_lhs_rhs_nkigym": "matmul_lhs_rhs",
+    "rmsnorm_matmul_online": "rmsnorm_matmul",
+}
+
+
+def canonical_name(func_name: str) -> str:
+    """The kernel family of a family or reference kernel name."""
+    return REFERENCE_NAMES.get(func_name, func_name)
+
+
 def kernel_id(func_name: str) -> int:
+    """C ABI kernel id of a family or reference kernel name."""
     try:
-        return KERNEL_IDS[func_name]
+        return KERNEL_IDS[canonical_name(func_name)]
     except KeyError as exc:
-        raise ValueError(f"unknown kernel {func_name!r}; known: {sorted(KERNEL_IDS)}") from exc
+        raise ValueError(f"unknown kernel {func_name!r}; known: {sorted(KERNEL_IDS) + sorted(REFERENCE_NAMES)}") from exc
 
 
 def check(func_name: str, cfg: TileConfig, M: int, N: int, K: int) -> tuple[int, str]:

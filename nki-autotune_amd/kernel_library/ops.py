@@ -36,6 +36,13 @@ def _stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
 
+def _same_device(first: str, ref: torch.Tensor, **others: torch.Tensor | None) -> None:
+    """Every operand lives on ``ref``'s device (the kernel runs there and reads raw pointers)."""
+    for name, t in others.items():
+        if t is not None and t.device != ref.device:
+            raise ValueError(f"{name} is on {t.device}, {first} on {ref.device}: all operands must share a device")
+
+
 def _check_operand(name: str, t: torch.Tensor, dtypes: tuple[torch.dtype, ...]) -> None:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor on a HIP device, got {type(t).__name__}")
@@ -60,8 +67,7 @@ def matmul_lhsT_rhs(
     _check_operand("rhs", rhs, (torch.bfloat16, torch.float32))
     if lhs_T.dtype != rhs.dtype:
         raise ValueError(f"dtype mismatch: lhs_T {lhs_T.dtype} vs rhs {rhs.dtype}")
-    if lhs_T.device != rhs.device:
-        raise ValueError("lhs_T and rhs on different devices")
+    _same_device("lhs_T", lhs_T, rhs=rhs, out=out)
     K, M = lhs_T.shape
     K2, N = rhs.shape
     if K != K2:
@@ -92,8 +98,7 @@ def matmul_lhs_rhs(
     """``out[M,N] = lhs[M,K] @ rhs[K,N]`` on the GPU (bf16, lhs K-contiguous)."""
     _check_operand("lhs", lhs, (torch.bfloat16,))
     _check_operand("rhs", rhs, (torch.bfloat16,))
-    if lhs.device != rhs.device:
-        raise ValueError("lhs and rhs on different devices")
+    _same_device("lhs", lhs, rhs=rhs, out=out)
     M, K = lhs.shape
     K2, N = rhs.shape
     if K != K2:
@@ -122,6 +127,7 @@ def rmsnorm_matmul(
     """``out[M,N] = (lhs[M,K] / sqrt(mean_k lhs^2 + eps) * gamma[K]) @ rhs[K,N]`` (bf16)."""
     _check_operand("lhs", lhs, (torch.bfloat16,))
     _check_operand("rhs", rhs, (torch.bfloat16,))
+    _same_device("lhs", lhs, rhs=rhs, gamma=gamma, out=out)
     M, K = lhs.shape
     K2, N = rhs.shape
     if K != K2:

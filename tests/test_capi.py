@@ -195,6 +195,37 @@ def test_entry_points_reject_bad_arguments_before_any_gpu_call():
     assert L.mi_matmul_lhsT_rhs_bf16(fake, fake, fake, 8192, 8192, 8192, ctypes.byref(bad), None) == _lib.MI_E_LDS
 
 
+def test_entry_points_reject_misaligned_pointers():
+    """Kernels move 16-byte vectors (the fp32 one, 4-byte elements): an
+    operand not aligned to that is refused with MI_E_ALIGN before any launch
+    (for instance a contiguous view at an odd element offset)."""
+    L = _lib.lib()
+    c = TileConfig(128, 128, 64, 4, 2).to_c()
+    ok, odd = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x1002)
+    assert L.mi_matmul_lhsT_rhs_bf16(odd, ok, ok, 8, 8, 8, ctypes.byref(c), None) == _lib.MI_E_ALIGN
+    assert "16-byte" in _lib.last_error()
+    assert L.mi_matmul_lhsT_rhs_bf16(ok, ok, odd, 8, 8, 8, ctypes.byref(c), None) == _lib.MI_E_ALIGN
+    assert L.mi_matmul_lhs_rhs_bf16(ok, odd, ok, 8, 8, 8, ctypes.byref(c), None) == _lib.MI_E_ALIGN
+    assert L.mi_rmsnorm_matmul_bf16(ok, odd, ok, ok, 8, 8, 8, 1e-6, ctypes.byref(c), None) == _lib.MI_E_ALIGN
+    assert L.mi_rmsnorm_matmul_bf16(ok, None, ok, odd, 8, 8, 8, 1e-6, ctypes.byref(c), None) == _lib.MI_E_ALIGN
+    assert L.mi_matmul_lhsT_rhs_f32(ctypes.c_void_p(0x1002), ok, ok, 8, 8, 8, ctypes.byref(c), None) == \
+        _lib.MI_E_ALIGN
+
+
+def test_reference_kernel_names_resolve():
+    """The reference's kernel names resolve to their families everywhere a family name does."""
+    import kernel_library as kl
+    from kernel_library.config import canonical_name, kernel_id
+
+    for ref, fam in (("matmul_lhsT_rhs_nkigym", "matmul_lhsT_rhs"), ("matmul_lhs_rhs_nkigym", "matmul_lhs_rhs"),
+                     ("rmsnorm_matmul_online", "rmsnorm_matmul")):
+        assert canonical_name(ref) == fam and kernel_id(ref) == kernel_id(fam)
+        assert kl.legal_configs(ref, 2048, 2048, 2048) == kl.legal_configs(fam, 2048, 2048, 2048)
+        assert kl.check(ref, kl.default_config(ref, 3000, 2048, 1000), 3000, 2048, 1000)[0] == 0
+    with pytest.raises(ValueError, match="unknown kernel"):
+        kernel_id("matmul_nothing")
+
+
 def test_python_wrappers_validate_on_the_host():
     torch = pytest.importorskip("torch")
     import kernel_library as kl

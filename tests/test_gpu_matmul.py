@@ -195,3 +195,20 @@ def test_empty_contraction_writes_zeros(gpu):
                           torch.empty((0, N), dtype=torch.bfloat16, device=gpu), out=out)
         torch.cuda.synchronize()
         assert torch.count_nonzero(out).item() == 0, (M, N)
+
+
+def test_operands_on_another_device_are_refused(gpu):
+    """Every operand must be on the first operand's device: the kernels read raw pointers there."""
+    import torch
+
+    kl = _kl()
+    a = torch.zeros((64, 32), dtype=torch.bfloat16, device=gpu)
+    b = torch.zeros((64, 48), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="device"):
+        kl.matmul_lhsT_rhs(a, b, out=torch.empty((32, 48), dtype=torch.bfloat16))
+    x = torch.zeros((32, 64), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(ValueError, match="device"):
+        kl.matmul_lhs_rhs(x, b, out=torch.empty((32, 48), dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="device"):
+        kl.rmsnorm_matmul(x, b, torch.ones(64, dtype=torch.bfloat16), out=torch.empty((32, 48), dtype=torch.bfloat16,
+                                                                                      device=gpu))

@@ -2,12 +2,13 @@
 matmul, against the CPU oracle.
 
 With split_k = P each output tile is computed by P workgroups over disjoint
-K ranges; they write fp32 partial products to a per-stream workspace and a
+K ranges; they write fp32 partial products to a workspace that the call
+takes from the library's stream-ordered pool (one buffer per call), and a
 second kernel sums them in part order into the bf16 output.  The tests
 cover ragged M, N and K, part counts up to 8, both pipelined variants,
-repeated and interleaved launches of different shapes (the workspace is
-reused and grown), a second stream (its own workspace), run to run
-determinism and HIP-graph replay.
+repeated and interleaved launches of different shapes, a second stream,
+run to run determinism, HIP-graph replay, and the pool's cap on the memory
+it keeps after large calls.
 """
 
 from __future__ import annotations
@@ -287,16 +288,64 @@ def test_rmsnorm_split_lifts_the_gamma_limit(gpu):
     assert rep["ok"], rep
 
 
-@pytest.mark.parametrize("M,K,N", [(256, 16384, 1024), (16, 16384, 4096)])
-def test_rmsnorm_default_splits_past_the_gamma_limit(gpu, M, K, N):
-    """With no config, K > 8192 takes a split register-staged fused config; output vs the oracle."""
+@pytest.mark.parametrize("M,K,N", [(256, 16384, 1024), (16, 16384, 4096), (4096, 16384, 7168)])
+def test_rmsnorm_default_past_the_gamma_limit(gpu, M, K, N):
+    """With no config and K > 8192: few output tiles or skinny M take a split
+    register-staged fused config; many output tiles take the two-pass kernel
+    (no gamma limit, no split).  Output vs the oracle (sampled rows at the
+    large shape), and at the large shape the default against variant 0 (the
+    other config without a gamma limit), timed."""
+    import torch
+
     import kernel_library as kl
+    from autotune.runner.benchmark import time_launches
     from helpers import rms_check, rms_inputs
     from oracle import rmsnorm as orms
 
+    print(f"fused default M={M} K={K} N={N}", flush=True)
     cfg = kl.default_config("rmsnorm_matmul", M, N, K)
-    assert cfg.split_k > 1 and cfg.variant in (4, 11), cfg
+    big = M * N >= 2048 * 2048
+    if big:
+        assert cfg.variant == 13 and cfg.split_k == 1, cfg
+    else:
+        assert cfg.split_k > 1 and cfg.variant in (4, 11), cfg
     d = rms_inputs(M, K, N, seed=45)
-    out = kl.rmsnorm_matmul(_dev(d["lhs"], gpu), _dev(d["rhs"], gpu), _dev(d["gamma"], gpu))
-    rep = rms_check(_host(out), orms.closed_form(d["lhs"], d["rhs"], d["gamma"]))
+    x, w, g = _dev(d["lhs"], gpu), _dev(d["rhs"], gpu), _dev(d["gamma"], gpu)
+    out = kl.rmsnorm_matmul(x, w, g)
+    rows = np.unique(np.concatenate([[0, M - 1], np.random.default_rng(2).integers(0, M, size=min(M, 20))]))
+    rep = rms_check(_host(out)[rows], orms.closed_form(d["lhs"][rows], d["rhs"], d["gamma"]))
     assert rep["ok"], (cfg.name, rep)
+    if big:
+        v0 = kl.TileConfig(128, 256, 64, 8, 2, variant=0)
+        o0 = torch.empty_like(out)
+        t13 = sorted(time_launches(lambda: kl.rmsnorm_matmul(x, w, g, cfg=cfg, out=out), 2, 10))[5]
+        t0 = sorted(time_launches(lambda: kl.rmsnorm_matmul(x, w, g, cfg=v0, out=o0), 2, 10))[5]
+        print(f"default {cfg.name} {t13 * 1e6:.0f} us, variant 0 {v0.name} {t0 * 1e6:.0f} us", flush=True)
+        rep0 = rms_check(_host(o0)[rows], orms.closed_form(d["lhs"][rows], d["rhs"], d["gamma"]))
+        assert rep0["ok"], rep0
+        assert t13 < t0
+
+
+def test_pool_returns_memory_after_a_large_call(gpu):
+    """A split-K call whose workspace is 1 GiB: after synchronisation the
+    library's pool keeps at most 256 MiB of it cached, so the device's free
+    memory is back within that of its level before the call."""
+    import torch
+
+    import kernel_library as kl
+
+    M = N = 8192
+    K = 16384
+    tc = kl.TileConfig(256, 256, 32, 4, 3, split_k=4, variant=1)      # 4 x 8192 x 8192 x 4 B = 1 GiB
+    a = torch.zeros((K, M), dtype=torch.bfloat16, device=gpu)
+    b = torch.zeros((K, N), dtype=torch.bfloat16, device=gpu)
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+    torch.cuda.synchronize()
+    free_before = torch.cuda.mem_get_info(gpu)[0]
+    kl.matmul_lhsT_rhs(a, b, cfg=tc, out=out)
+    torch.cuda.synchronize()
+    free_after = torch.cuda.mem_get_info(gpu)[0]
+    held = free_before - free_after
+    print(f"pool holds {held / 2**20:.0f} MiB after a 1 GiB workspace call", flush=True)
+    assert held <= (256 + 32) << 20, held
+    assert torch.count_nonzero(out).item() == 0
