@@ -5,7 +5,9 @@ with ``hipcc --offload-arch=gfx950`` (in parallel, one process per unit) and
 linked into ``kernel_library/libmi_kernels.so``, which the ctypes loader in
 ``kernel_library/_lib.py`` opens.  The tile-config search space lives in the
 instance tables of those units, so building the library is the "compile"
-step of every autotune candidate at once.
+step of every autotune candidate at once.  The units under ``csrc/probe/``
+(measurement probes for bench.py, outside the kernel_library ABI) are linked
+into ``kernel_library/libmi_probe.so``.
 
 Usage: ``python nki-autotune_amd/build_lib.py [--jobs N] [--force]``.
 """
@@ -24,6 +26,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 BUILD = PKG_DIR / "_build"
 LIB = PKG_DIR / "kernel_library" / "libmi_kernels.so"
+PROBE_LIB = PKG_DIR / "kernel_library" / "libmi_probe.so"
 INCLUDE = PKG_DIR.parent / "include"
 
 ARCH = "gfx950"
@@ -59,7 +62,7 @@ def _headers() -> list[Path]:
 
 
 def _compile(src: Path, force: bool) -> tuple[Path, str]:
-    obj = BUILD / (src.stem + ".o")
+    obj = BUILD / (("probe_" if src.parent.name == "probe" else "") + src.stem + ".o")
     newest_dep = max(p.stat().st_mtime for p in [src, *_headers()])
     if not force and obj.exists() and obj.stat().st_mtime >= newest_dep:
         return obj, ""
@@ -71,26 +74,33 @@ def _compile(src: Path, force: bool) -> tuple[Path, str]:
     return obj, log
 
 
+def _link(objs: list[Path], lib: Path) -> None:
+    tmp = lib.with_suffix(".so.tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link of {lib.name} failed:\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, lib)
+
+
 def build(jobs: int | None = None, force: bool = False, verbose: bool = False) -> Path:
-    """Compile every csrc/*.hip unit and link libmi_kernels.so; return its path."""
+    """Compile every csrc/*.hip unit and link libmi_kernels.so (and csrc/probe/ into libmi_probe.so)."""
     BUILD.mkdir(parents=True, exist_ok=True)
     srcs = _sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    jobs = jobs or max(1, min(len(srcs), (os.cpu_count() or 2)))
+    probes = sorted((CSRC / "probe").glob("*.hip"))
+    jobs = jobs or max(1, min(len(srcs) + len(probes), (os.cpu_count() or 2)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        results = list(pool.map(lambda s: _compile(s, force), srcs))
-    objs = [obj for obj, _ in results]
+        results = list(pool.map(lambda s: _compile(s, force), srcs + probes))
     if verbose:
         for obj, log in results:
             if log.strip():
                 print(f"[build] {obj.name}: {log.strip()}")
-    tmp = LIB.with_suffix(".so.tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
-    proc = subprocess.run(cmd, capture_output=True, text=True)
-    if proc.returncode != 0:
-        raise RuntimeError(f"link failed:\n{proc.stdout}{proc.stderr}")
-    os.replace(tmp, LIB)
+    objs = [obj for obj, _ in results]
+    _link(objs[:len(srcs)], LIB)
+    if probes:
+        _link(objs[len(srcs):], PROBE_LIB)
     return LIB
 
 

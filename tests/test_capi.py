@@ -37,6 +37,14 @@ def test_library_exports_every_header_symbol():
     assert _lib.lib().mi_version().decode().startswith("mi_kernels")
 
 
+def test_probe_library_loads_and_exports_its_probes():
+    from kernel_library import _probe
+
+    h = _probe.lib()
+    for s in ("mi_probe_clocked_lhsT_rhs", "mi_probe_mfma"):
+        assert getattr(h, s) is not None, s
+
+
 def test_every_compiled_config_is_enumerable_and_legal():
     for fam, shape in (("matmul_lhsT_rhs", (2048, 2048, 2048)), ("rmsnorm_matmul", (2048, 2048, 2048)),
                        ("matmul_lhs_rhs", (2048, 2048, 2048)), ("matmul_lhsT_rhs_f32", (256, 512, 512))):
