@@ -31,10 +31,10 @@ one launch of that kernel on inputs resident in HBM.
   was within 2 % of the winner in interleaved re-timing (so the line's
   config is the one the committed profiles cover whenever the two tie).
 * ``clock``: the engine clock the shipped kernel runs at, measured right
-  after the timed region by its clocked twin (the same kernel reading the
-  engine-cycle and 100 MHz real-time counters around each workgroup:
-  ``kernel_library._probe``), with the twin's launch time beside the
-  product kernel's, and the share of the peak at that clock it reaches.
+  before and right after the timed region by its clocked twin (the same
+  kernel reading the engine-cycle and 100 MHz real-time counters around each
+  workgroup: ``kernel_library._probe``), with the twin's launch time beside
+  the product kernel's, and the share of the peak at that clock it reaches.
 * ``mfma_ceiling``: the rate of the MFMA work alone on the benchmark's data
   (operands from registers; then with the kernel's LDS operand reads), with
   no global traffic: what any kernel running those instructions reaches
@@ -53,7 +53,11 @@ fused rmsnorm_matmul at 4096^3 instead of the C2 matmul: the command the C3
 kernel profiles are taken with; the default line is always C2),
 ``--workload c5 --m M`` / ``--workload decode --m M`` (the skinny matmul or
 the fused kernel at (M, 28672, 8192), HBM-bound: the commands their profiles
-are taken with).
+are taken with), ``--workload c4a|c4b|c4c|c3-matmul`` (the plain lhsT.rhs
+matmul at one C4 shape or at 4096^3, tuned config or ``--config``: the
+commands their profiles are taken with), ``--workload c2-clock`` (the clock study: engine clock
+against data movement at 8192^3, printed as a line of its own; see
+clock_study()).
 """
 
 from __future__ import annotations
@@ -89,8 +93,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--sweep-reps", type=int, default=20)
     ap.add_argument("--config", default="", help="tile config name (e.g. bm256_bn256_bk32_w4_s3_v1) instead of the sweep")
-    ap.add_argument("--workload", choices=["c2", "c3", "c4a", "c4b", "c4c", "c5", "decode"], default="c2",
-                    help="c2: lhsT.rhs matmul 8192^3 (the metric); c3: rmsnorm_matmul 4096^3; c4a/b/c: the C4 "
+    ap.add_argument("--workload", choices=["c2", "c2-clock", "c3", "c3-matmul", "c4a", "c4b", "c4c", "c5", "decode"], default="c2",
+                    help="c2: lhsT.rhs matmul 8192^3 (the metric); c3: rmsnorm_matmul 4096^3; c3-matmul: the plain "
+                         "lhsT.rhs matmul at 4096^3; c4a/b/c: the C4 "
                          "lhsT.rhs shapes; c5: skinny lhsT.rhs (--m) x 28672 x 8192; decode: rmsnorm_matmul at the "
                          "c5 shape (all but c2: profiling workloads)")
     ap.add_argument("--settle-s", type=float, default=2.0,
@@ -216,6 +221,9 @@ def data_sensitivity(cfg, steps: int = 20) -> dict:
 SKINNY_N, SKINNY_K = 28672, 8192
 # Benchmark config C4: (M, K, N) of the non-square sweeps.
 C4_SHAPES = {"c4a": (2048, 8192, 1024), "c4b": (4096, 1024, 14336), "c4c": (1024, 14336, 4096)}
+# Plain lhsT.rhs shapes timed by shape_main: C4's three, and the C3 shape (the
+# fused kernel's like-for-like matmul).
+PLAIN_SHAPES = {**C4_SHAPES, "c3-matmul": (4096, 4096, 4096)}
 HBM_PEAK_GBS = 8000.0
 
 
@@ -484,8 +492,10 @@ def main() -> int:
 
     if args.workload in ("c5", "decode"):
         return skinny_main(args, dev)
-    if args.workload in C4_SHAPES:
-        return shape_main(args, dev, *C4_SHAPES[args.workload])
+    if args.workload == "c2-clock":
+        return clock_study(args, dev)
+    if args.workload in PLAIN_SHAPES:
+        return shape_main(args, dev, *PLAIN_SHAPES[args.workload])
     fam, s = ("matmul_lhsT_rhs", M) if args.workload == "c2" else ("rmsnorm_matmul", 4096)
     pin = {}
     if args.config:
@@ -579,10 +589,93 @@ def main() -> int:
     return 0
 
 
-def shape_main(args, dev, m: int, k: int, n: int) -> int:
-    """--workload c4a|c4b|c4c: the lhsT.rhs matmul at one C4 shape with its tuned config (or --config).
+# Configs of the clock study: tiles from 256x256 down to 64x128, so LDS
+# bytes read per MFMA and fabric bytes per launch both span about 3x.
+CLOCK_STUDY_CONFIGS = ("bm256_bn256_bk32_w4_s3_v1", "bm256_bn256_bk32_w8_s3_v1", "bm128_bn512_bk32_w8_s3_v1",
+                       "bm128_bn256_bk32_w4_s3_v1", "bm128_bn128_bk64_w4_s3_v1", "bm64_bn128_bk64_w4_s4_v1")
 
-    The command the C4 profiles are taken with; prints a line of its own."""
+
+def lds_bytes_per_mfma(cfg) -> int:
+    """LDS bytes a wave reads per 32x32x16 MFMA: its (tm + tn) x 16 bf16 operand slice per tm/32 x tn/32 MFMAs.
+
+    The wave tile (tm, tn) follows the kernels' wave split: the most square
+    power-of-two split of the workgroup tile into ``waves`` tiles of at
+    least 32x32."""
+    best = None
+    wm = 1
+    while wm <= cfg.waves:
+        wn = cfg.waves // wm
+        tm, tn = cfg.block_m // wm, cfg.block_n // wn
+        if wm * wn == cfg.waves and tm >= 32 and tn >= 32 and tm % 32 == 0 and tn % 32 == 0:
+            if best is None or abs(tm - tn) < abs(best[0] - best[1]):
+                best = (tm, tn)
+        wm *= 2
+    tm, tn = best
+    return (tm + tn) * 16 * 2 // ((tm // 32) * (tn // 32))
+
+
+def clock_study(args, dev) -> int:
+    """--workload c2-clock: does the engine clock rise as data movement falls?
+
+    The C2 workload (8192^3, U(-1,1) bf16) on the clocked twins of lhsT.rhs
+    configs whose tiles span 256x256 to 64x128, beside the two MFMA probes
+    that run the same MFMA count with no global traffic (operands from LDS,
+    then from registers).  Rounds interleave every row, so each row sees the
+    same power and thermal history; a row reports its median clock and
+    launch time over the rounds.  The fabric bytes of each row come from a
+    rocprofv3 FETCH_SIZE / WRITE_SIZE pass of this same command."""
+    import statistics
+
+    import torch
+
+    import kernel_library as kl
+    from autotune.runner.benchmark import generate_tensors, upload
+    from autotune.tune import default_dists, input_specs
+    from kernel_library import _probe
+
+    fam, s = "matmul_lhsT_rhs", M
+    specs = input_specs(fam, s, s, s)
+    d = upload(generate_tensors(specs, 0, default_dists(fam, s)), specs, dev)
+    out = torch.empty((s, s), dtype=torch.bfloat16, device=dev)
+    flop = 2.0 * s * s * s
+    cfgs = [kl.TileConfig.from_name(n) for n in CLOCK_STUDY_CONFIGS]
+    rounds = max(1, args.steps // 10)
+    rows = {c.name: [] for c in cfgs}
+    probes = {"mfma_lds_probe": [], "mfma_regs_probe": []}
+    settle(lambda: kl.matmul_lhsT_rhs(d["lhs_T"], d["rhs"], cfg=cfgs[0], out=out), args.settle_s)
+    for r in range(rounds):
+        for c in cfgs:
+            rows[c.name].append(_probe.clocked_lhsT_rhs(d["lhs_T"], d["rhs"], out, c, launches=10, warmup=2))
+        probes["mfma_lds_probe"].append(_probe.mfma_ceiling(d["lhs_T"], 1))
+        probes["mfma_regs_probe"].append(_probe.mfma_ceiling(d["lhs_T"], 0))
+        log(f"clock study round {r + 1}/{rounds} done")
+    table = []
+    for c in cfgs:
+        us = statistics.median(x["us"] for x in rows[c.name])
+        mhz = statistics.median(x["clock_mhz"] for x in rows[c.name])
+        tf = flop / (us * 1e-6) / 1e12
+        table.append({"config": c.name, "lds_bytes_per_mfma": lds_bytes_per_mfma(c), "us": round(us, 1),
+                      "tflops": round(tf, 1), "clock_mhz": round(mhz, 1),
+                      "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                      "frac_of_peak_at_that_clock": round(tf / (PEAK_BF16_TFLOPS * mhz / _probe.PEAK_CLOCK_MHZ), 4)})
+    for name, lst in probes.items():
+        tf = statistics.median(x["tflops"] for x in lst)
+        mhz = statistics.median(x["clock_mhz"] for x in lst)
+        table.append({"config": name, "lds_bytes_per_mfma": 512 if name == "mfma_lds_probe" else 0,
+                      "tflops": tf, "clock_mhz": mhz, "frac_of_peak": round(tf / PEAK_BF16_TFLOPS, 4),
+                      "frac_of_peak_at_that_clock": round(tf / (PEAK_BF16_TFLOPS * mhz / _probe.PEAK_CLOCK_MHZ), 4)})
+    for row in table:
+        log(json.dumps(row))
+    print(json.dumps({"workload": "c2-clock", "shape": [s, s, s], "rounds": rounds,
+                      "data": "lhsT, rhs ~ U(-1,1) seed 0 rounded to bf16", "rows": table}), flush=True)
+    return 0
+
+
+def shape_main(args, dev, m: int, k: int, n: int) -> int:
+    """--workload c4a|c4b|c4c|c3-matmul: the lhsT.rhs matmul at one shape with its tuned config (or --config).
+
+    The command the C4 profiles (and the fused kernel's like-for-like matmul
+    profile) are taken with; prints a line of its own."""
     import torch
 
     import kernel_library as kl

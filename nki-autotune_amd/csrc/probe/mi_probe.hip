@@ -162,7 +162,9 @@ __global__ __launch_bounds__(256) void mfma_lds_kernel(const uint16_t* __restric
   X(256, 256, 32, 8, 3)     \
   X(256, 256, 64, 8, 2)     \
   X(128, 512, 32, 8, 3)     \
-  X(128, 128, 64, 4, 3)
+  X(128, 256, 32, 4, 3)     \
+  X(128, 128, 64, 4, 3)     \
+  X(64, 128, 64, 4, 4)
 
 typedef void (*ClockedFn)(const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, unsigned long long*,
                           hipStream_t);

@@ -134,6 +134,12 @@ def load(path: str | os.PathLike) -> ctypes.CDLL:
     pipeline also loads per-config libraries built just in time from a
     generated instance source.  Both export the same symbols.
     """
+    given = str(path)
+    handle = _LIBS.get(given)
+    if handle is not None:
+        # Every kernel call comes through here: resolving the path (a few
+        # filesystem lookups) only on the first load keeps the call cheap.
+        return handle
     key = str(Path(path).resolve())
     handle = _LIBS.get(key)
     if handle is None:
@@ -144,6 +150,7 @@ def load(path: str | os.PathLike) -> ctypes.CDLL:
         handle = ctypes.CDLL(key)
         _declare(handle)
         _LIBS[key] = handle
+    _LIBS[given] = handle
     return handle
 
 

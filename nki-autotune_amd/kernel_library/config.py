@@ -182,13 +182,24 @@ def split_k_variants(func_name: str, grid: list[TileConfig], M: int, N: int) -> 
 
 
 def default_config(func_name: str, M: int, N: int, K: int) -> TileConfig:
-    """Tuned config from ``tuned_configs.json`` if present for this shape, else the library default."""
+    """Tuned config from ``tuned_configs.json`` if present for this shape, else the library default.
+
+    Memoised per (name, shape) until the tuned table is reloaded: a call
+    without a config pays a dict lookup, not a table scan and a library call."""
+    key = (func_name, M, N, K)
+    cfg = _DEFAULT_CACHE.get(key)
+    if cfg is not None:
+        return cfg
     tuned = tuned_table().get(table_key(func_name, M, N, K))
     if tuned is not None:
-        return TileConfig(**tuned)
-    c = _lib.MiTileCfg()
-    _lib.check_rc(_lib.lib().mi_default_config(kernel_id(func_name), M, N, K, ctypes.byref(c)), "mi_default_config")
-    return TileConfig.from_c(c)
+        cfg = TileConfig(**tuned)
+    else:
+        c = _lib.MiTileCfg()
+        _lib.check_rc(_lib.lib().mi_default_config(kernel_id(func_name), M, N, K, ctypes.byref(c)),
+                      "mi_default_config")
+        cfg = TileConfig.from_c(c)
+    _DEFAULT_CACHE[key] = cfg
+    return cfg
 
 
 def table_key(func_name: str, M: int, N: int, K: int) -> str:
@@ -196,12 +207,14 @@ def table_key(func_name: str, M: int, N: int, K: int) -> str:
 
 
 _TABLE_CACHE: dict | None = None
+_DEFAULT_CACHE: dict[tuple, TileConfig] = {}
 
 
 def tuned_table(reload: bool = False) -> dict:
     """The persisted autotune winners: ``{"<kernel>:<M>x<N>x<K>": {tile fields}}``."""
     global _TABLE_CACHE
     if _TABLE_CACHE is None or reload:
+        _DEFAULT_CACHE.clear()
         data = {}
         if TUNED_TABLE.exists():
             data = json.loads(TUNED_TABLE.read_text()).get("configs", {})
