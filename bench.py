@@ -31,7 +31,8 @@ one launch of that kernel on inputs resident in HBM.
   was within 2 % of the winner in interleaved re-timing (so the line's
   config is the one the committed profiles cover whenever the two tie).
 * ``clock``: the engine clock the shipped kernel runs at, measured right
-  before and right after the timed region by its clocked twin (the same
+  before the timed region (after its warm-up steps) and right after it by
+  its clocked twin (the same
   kernel reading the engine-cycle and 100 MHz real-time counters around each
   workgroup: ``kernel_library._probe``), with the twin's launch time beside
   the product kernel's, and the share of the peak at that clock it reaches.
@@ -384,7 +385,7 @@ def clock_of(before, after, cfg, achieved_tflops: float) -> dict:
     at_clock = PEAK_BF16_TFLOPS * mhz / _probe.PEAK_CLOCK_MHZ
     return {"clock_mhz": round(mhz, 1), "before": before, "after": after,
             "source": "clocked twin of the shipped kernel (s_memtime / s_memrealtime per workgroup), 10 launches "
-                      "right before and right after the timed steps",
+                      "after the warm-up steps, right before the timed steps, and 10 right after them",
             "peak_at_that_clock_tflops": round(at_clock, 1),
             "frac_of_peak_at_that_clock": round(achieved_tflops / at_clock, 4)}
 
@@ -516,10 +517,10 @@ def main() -> int:
             kl.rmsnorm_matmul(d["lhs"], d["rhs"], d["gamma"], cfg=cfg, out=out)
 
     settle(step, args.settle_s)
-    clock_twin = fam == "matmul_lhsT_rhs" and not args.only_kernel
-    before = twin_clock(d, out, cfg) if clock_twin else None
     for _ in range(args.warmup):
         step()
+    clock_twin = fam == "matmul_lhsT_rhs" and not args.only_kernel
+    before = twin_clock(d, out, cfg) if clock_twin else None
     stream = torch.cuda.current_stream(dev)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
