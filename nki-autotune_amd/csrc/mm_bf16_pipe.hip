@@ -18,6 +18,10 @@
   X(256, 128, 64, 4, 3)      \
   X(128, 256, 64, 4, 2)      \
   X(128, 256, 64, 4, 3)      \
+  X(128, 256, 32, 4, 3)      \
+  X(128, 256, 32, 4, 4)      \
+  X(256, 128, 32, 4, 3)      \
+  X(256, 128, 32, 4, 4)      \
   X(256, 128, 64, 8, 2)      \
   X(256, 128, 64, 8, 3)      \
   X(128, 128, 64, 4, 2)      \
