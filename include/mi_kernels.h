@@ -62,7 +62,7 @@ enum {
  *                               variant 2 the depth of its register ring
  *   split_k                   : K split over this many workgroups per output
  *                               tile (1..16; > 1 only for the pipelined matmul
- *                               body: lhsT variants 1 and 3, matmul_lhs_rhs
+ *                               body: lhsT variants 1, 3 and 4, matmul_lhs_rhs
  *                               variants 0 and 2, and the fused kernels on it:
  *                               rmsnorm_matmul variants 4, 5, 11, 12 -- whose
  *                               gamma limit then applies per part -- and 13;
@@ -85,7 +85,13 @@ enum {
  *                               the same function):
  *     matmul         0 plain double buffer; 1 software-pipelined LDS-direct
  *                    loads; 2 register prefetch ring (skinny shapes); 3 as 1
- *                    with rhs read non-temporally (streamed once: skinny M)
+ *                    with rhs read non-temporally (streamed once: skinny M);
+ *                    4 as 1 with each K tile's 16-deep sub-steps split over
+ *                    the waves, every wave accumulating the whole block (at
+ *                    most 128x128) and the epilogue adding the waves' sums
+ *                    in wave order (few output tiles, long K).  Variant 4
+ *                    adds in another fp32 order than 0..3, so its result
+ *                    may differ from theirs in the last bit
  *     matmul_lhs_rhs 0 the software-pipelined core (block_k >= 32, 2..4 stages);
  *                    1 the same with the K-contiguous A panel loaded two K
  *                    tiles per load (block_k 32 or 64); 2 as 0 with rhs read

@@ -83,6 +83,7 @@ mi::Legal template_legal(int kernel_id, const mi_tile_cfg& c) {
       if (c.variant == 0) return mi::legal_mm_plain(bm, bn, bk, w, s);
       if (c.variant == 1 || c.variant == 3) return mi::legal_mm_pipe(bm, bn, bk, w, s, false);
       if (c.variant == 2) return mi::legal_mm_reg(bm, bn, bk, w, s);
+      if (c.variant == 4) return mi::legal_mm_kw(bm, bn, bk, w, s);
       break;
     case MI_KERNEL_MATMUL_LHS_RHS_BF16:
       if (c.variant == 0 || c.variant == 2) return mi::legal_mm_pipe(bm, bn, bk, w, s, true);
@@ -109,7 +110,7 @@ mi::Legal template_legal(int kernel_id, const mi_tile_cfg& c) {
 }
 
 bool splittable(int kernel_id, int variant) {
-  return (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (variant == 1 || variant == 3)) ||
+  return (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (variant == 1 || variant == 3 || variant == 4)) ||
          (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 && (variant == 0 || variant == 2)) ||
          (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 &&
           (variant == 4 || variant == 5 || variant == 11 || variant == 12 || variant == 13));

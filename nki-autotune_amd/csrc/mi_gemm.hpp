@@ -594,6 +594,60 @@ __device__ __forceinline__ void store_partial(const f32x16_t (&acc)[TM][TN], flo
   }
 }
 
+// Epilogue of the K-split-over-waves core: every wave holds the whole
+// block's fp32 sums over its own K sub-steps.  One 32-row slice at a time,
+// each wave writes its slice to its LDS slot (32 rows, stride BN*4+16
+// bytes: the 16 lanes of a ds_write_b128 phase hit 16 different bank
+// quads), then every thread takes 8-column items of the slice, sums the
+// waves' values in wave order (so the result does not depend on timing),
+// and stores 8 bf16 to out -- or, split-K, the 8 fp32 to its part's ws.
+template <int BN, int WAVES, int TM, int TN, bool SPLIT>
+__device__ __forceinline__ void kw_reduce_store(const f32x16_t (&acc)[TM][TN], char* smem, int wave, int lane,
+                                                int tid, uint16_t* __restrict__ out, float* __restrict__ ws, int M,
+                                                int N, int m0, int n0) {
+  constexpr int RSB = BN * 4 + 16, SLOT = 32 * RSB, NTH = WAVES * 64, ITEMS = 32 * (BN / 8);
+  MI_LDS char* lds = (MI_LDS char*)smem;
+  const int r = lane & 31;
+#pragma unroll
+  for (int mt = 0; mt < TM; ++mt) {
+#pragma unroll
+    for (int nt = 0; nt < TN; ++nt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int c = nt * 32 + 8 * j + 4 * (lane >> 5);
+        const f32x4_t v = {acc[mt][nt][4 * j], acc[mt][nt][4 * j + 1], acc[mt][nt][4 * j + 2],
+                           acc[mt][nt][4 * j + 3]};
+        *(MI_LDS f32x4_t*)(lds + wave * SLOT + r * RSB + c * 4) = v;
+      }
+    __syncthreads();
+    for (int it = tid; it < ITEMS; it += NTH) {
+      const int rr = it / (BN / 8), c8 = (it % (BN / 8)) * 8;
+      const int off = rr * RSB + c8 * 4;
+      f32x4_t lo = *(MI_LDS f32x4_t*)(lds + off), hi = *(MI_LDS f32x4_t*)(lds + off + 16);
+#pragma unroll
+      for (int w = 1; w < WAVES; ++w) {
+        lo += *(MI_LDS f32x4_t*)(lds + w * SLOT + off);
+        hi += *(MI_LDS f32x4_t*)(lds + w * SLOT + off + 16);
+      }
+      const int m = m0 + mt * 32 + rr, n = n0 + c8;
+      if (m < M && n < N) {
+        if constexpr (SPLIT) {
+          *(f32x4_t*)(ws + (size_t)m * N + n) = lo;
+          *(f32x4_t*)(ws + (size_t)m * N + n + 4) = hi;
+        } else {
+          u32x4_t o;
+          o.x = pack_bf16x2(lo[0], lo[1]);
+          o.y = pack_bf16x2(lo[2], lo[3]);
+          o.z = pack_bf16x2(hi[0], hi[1]);
+          o.w = pack_bf16x2(hi[2], hi[3]);
+          *(u32x4_t*)(out + (size_t)m * N + n) = o;
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
 // out[i] = bf16(sum over p = 0 .. parts-1 of ws[p][i]), summed in part order
 // (so the result does not depend on the order the parts ran in); 8
 // elements per thread (n = M*N, a multiple of 8).  A template so that every
@@ -618,19 +672,26 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict
 }
 
 template <int BM, int BN, int BK, int WAVES, int STAGES, bool AK, bool NTB = false, bool SPLIT = false,
-          bool RS = false>
+          bool RS = false, bool KW = false>
 __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, const uint16_t* __restrict__ rhs,
                                              uint16_t* __restrict__ out, int M, int N, int K, int group_m,
                                              char* smem, const SplitK sk = SplitK{1, nullptr},
                                              const RowScale rsc = RowScale{nullptr, 0, 0.0f, 0.0f}) {
   using C = PipeCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
-  static_assert(legal_mm_pipe(BM, BN, BK, WAVES, STAGES, AK).code == MI_OK, "illegal tile config (mi_legal.hpp)");
+  static_assert(KW ? legal_mm_kw(BM, BN, BK, WAVES, STAGES).code == MI_OK
+                   : legal_mm_pipe(BM, BN, BK, WAVES, STAGES, AK).code == MI_OK,
+                "illegal tile config (mi_legal.hpp)");
   static_assert(C::LDS_BYTES == lds_mm_pipe(BM, BN, BK, WAVES, STAGES), "host LDS budget out of step");
-  static_assert(G::ok, "illegal wave grid");
+  static_assert(KW || G::ok, "illegal wave grid");
+  static_assert(!KW || (!AK && !RS), "K split over the waves: lhsT operand, no row scale");
   static_assert(BK % 32 == 0, "BK must be a multiple of 32 (even number of MFMA K steps)");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
-  constexpr int TM = G::TM, TN = G::TN, KS = BK / 16;
+  // KW: every wave covers the whole block (TM x TN MFMA tiles) over its own
+  // KSW consecutive 16-deep sub-steps of each K tile; otherwise each wave
+  // covers its wave-grid block over all KS sub-steps.
+  constexpr int TM = KW ? BM / 32 : G::TM, TN = KW ? BN / 32 : G::TN, KS = BK / 16;
+  constexpr int KSW = KW ? KS / WAVES : KS;
   using LA = std::conditional_t<AK, KPanelLoader<BK, BM, WAVES>, PanelLoader<BK, BM, WAVES>>;
   using LB = PanelLoader<BK, BN, WAVES>;
   // Loads of one K tile by this wave; vm_wait<n> with n > 0 needs every wave
@@ -646,8 +707,8 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   if constexpr (SPLIT) tile_coords_split(tiles_m, tiles_n, group_m, sk.parts, tmi, tni, part);
   else tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
   const int m0 = tmi * BM, n0 = tni * BN;
-  const int wm0 = (wave / G::WN) * G::WTM;
-  const int wn0 = (wave % G::WN) * G::WTN;
+  const int wm0 = KW ? 0 : (wave / G::WN) * G::WTM;
+  const int wn0 = KW ? 0 : (wave % G::WN) * G::WTN;
   const int lda = K;  // row stride of the K-contiguous lhs: the whole K
   int k0 = 0;
   if constexpr (SPLIT) {
@@ -676,6 +737,15 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   TrFrag<BN, TN> fb;
   if constexpr (!AK) fa.init(lane, wm0);
   fb.init(lane, wn0);
+  if constexpr (KW) {
+    // This wave's sub-steps start KSW * wave rows into each K tile (the
+    // operand swizzle repeats every 16 rows, so a row offset is enough).
+    const int kb = wave * KSW * 16;
+#pragma unroll
+    for (int t = 0; t < TM; ++t) fa.off[t] += kb * (BM * 2);
+#pragma unroll
+    for (int t = 0; t < TN; ++t) fb.off[t] += kb * (BN * 2);
+  }
   // K-contiguous A operand: lane l reads row l%32 of the fragment, K chunk
   // 2*kk + l/32 of the sub-step, at its k_swz slot (the same for every
   // 32-row fragment of the wave).
@@ -795,13 +865,21 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   // sub-step.
   // Tile t sits in stage t % STAGES; the loop is unrolled STAGES times so
   // that the stage is a compile-time constant in every body.
+  // Operand buffer of sub-step kk of the tile held in `stage`: sub-steps
+  // alternate between the two buffers across tile boundaries, so the next
+  // tile's first operands never overwrite the ones the last MFMAs of this
+  // tile still read.  With an even sub-step count per tile this is kk & 1;
+  // with an odd one (KW with one sub-step per wave) it needs STAGES * KSW
+  // even, so the ring's wrap keeps the alternation.
+  static_assert((STAGES * KSW) % 2 == 0, "operand buffers need an even sub-step count per ring turn");
+  auto bufof = [](int stage, int kk) { return (stage * KSW + kk) & 1; };
   auto tile = [&](int t, auto cur_c) __attribute__((always_inline)) {
     constexpr int cur = decltype(cur_c)::value;
     constexpr int nxt = cur + 1 == STAGES ? 0 : cur + 1;
 #pragma unroll
-    for (int kk = 0; kk + 1 < KS; ++kk) {
-      read_frags(cur, kk + 1, (kk + 1) & 1);
-      mfmas(kk & 1);
+    for (int kk = 0; kk + 1 < KSW; ++kk) {
+      read_frags(cur, kk + 1, bufof(cur, kk + 1));
+      mfmas(bufof(cur, kk));
       interleave_mfma_ds<TM * TN, 2 * NF>();
     }
     vm_wait<(STAGES - 2) * LPT>();
@@ -809,32 +887,53 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
     const int kt_new = clamp(t + STAGES);
 #pragma unroll
     for (int f = 0; f < NF; ++f) {
-      read_frag(nxt, 0, 0, f);
+      read_frag(nxt, 0, bufof(nxt, 0), f);
 #pragma unroll
       for (int q = f * LPT / NF; q < (f + 1) * LPT / NF; ++q) issue_one(q, kt_new, cur);
     }
-    mfmas((KS - 1) & 1);
+    mfmas(bufof(cur, KSW - 1));
     interleave_mfma_ds<TM * TN, 2 * NF>();
+  };
+  // Last tile: no further loads.
+  auto last_tile = [&](int cur) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kk = 0; kk < KSW; ++kk) {
+      if (kk + 1 < KSW) read_frags(cur, kk + 1, (kk + 1) & 1);
+      mfmas(kk & 1);
+      interleave_mfma_ds<TM * TN, 2 * NF>();
+    }
   };
   int t0 = 0;
   for (; t0 + STAGES < KT; t0 += STAGES)
     static_for<STAGES>([&](auto s_c) __attribute__((always_inline)) { tile(t0 + s_c(), s_c); });
-  static_while<STAGES>([&](auto s_c) __attribute__((always_inline)) {
-    if (t0 + s_c() + 1 >= KT) return false;
-    tile(t0 + s_c(), s_c);
-    return true;
-  });
-  const int cur = (KT - 1) % STAGES;
-  // Last tile: no further loads.
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) {
-    if (kk + 1 < KS) read_frags(cur, kk + 1, (kk + 1) & 1);
-    mfmas(kk & 1);
-    interleave_mfma_ds<TM * TN, 2 * NF>();
+  if constexpr (KSW % 2 == 1) {
+    // The buffer parity depends on the stage, which is a compile-time
+    // constant only inside tile(): the last tile runs through tile() too.
+    // Its extra barrier reads the next stage (a clamped re-read of the last
+    // K tile) into the unused buffer and issues one more clamped load group,
+    // which the drain below retires.
+    static_while<STAGES>([&](auto s_c) __attribute__((always_inline)) {
+      if (t0 + s_c() >= KT) return false;
+      tile(t0 + s_c(), s_c);
+      return true;
+    });
+  } else {
+    static_while<STAGES>([&](auto s_c) __attribute__((always_inline)) {
+      if (t0 + s_c() + 1 >= KT) return false;
+      tile(t0 + s_c(), s_c);
+      return true;
+    });
+    last_tile((KT - 1) % STAGES);
   }
   wait_vmem();
   __syncthreads();  // the epilogue reuses the panel buffers
 
+  if constexpr (KW) {
+    kw_reduce_store<BN, WAVES, TM, TN, SPLIT>(acc, smem, wave, lane, tid, out,
+                                             SPLIT ? sk.ws + (size_t)part * (size_t)M * (size_t)N : nullptr, M, N,
+                                             m0, n0);
+    return;
+  }
   if constexpr (SPLIT) {
     store_partial<TM, TN>(acc, sk.ws + (size_t)part * (size_t)M * (size_t)N, lane, M, N, m0 + wm0, n0 + wn0);
     return;
@@ -859,6 +958,22 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
   __shared__ __attribute__((aligned(1024))) char smem[PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
   mm_pipe_body<BM, BN, BK, WAVES, STAGES, false, NTB, SPLIT>(lhsT, rhs, out, M, N, K, group_m, smem,
                                                              SplitK{parts, ws});
+}
+
+// lhsT.rhs matmul variant 4: the pipelined core with each K tile's
+// sub-steps split over the waves (every wave accumulates the whole block;
+// the epilogue sums the waves' blocks).  Half or less of the LDS operand
+// bytes per MFMA of a wave-grid split for blocks up to 128x128, at the
+// cost of a different fp32 summation order.  SPLIT: split-K as for variant 1.
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool SPLIT = false>
+__global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_kw_kernel(const uint16_t* __restrict__ lhsT,
+                                                                        const uint16_t* __restrict__ rhs,
+                                                                        uint16_t* __restrict__ out, int M, int N,
+                                                                        int K, int group_m, int parts,
+                                                                        float* __restrict__ ws) {
+  __shared__ __attribute__((aligned(1024))) char smem[lds_mm_kw(BM, BN, BK, WAVES, STAGES)];
+  mm_pipe_body<BM, BN, BK, WAVES, STAGES, false, false, SPLIT, false, true>(lhsT, rhs, out, M, N, K, group_m, smem,
+                                                                           SplitK{parts, ws});
 }
 
 // out[M,N] = lhs[M,K] . rhs[K,N] with lhs K-contiguous (matmul_lhs_rhs);

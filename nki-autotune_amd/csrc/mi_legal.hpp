@@ -128,6 +128,34 @@ MI_HD constexpr Legal legal_mm_pipe(int bm, int bn, int bk, int waves, int stage
   return ok();
 }
 
+// ---- pipelined core with each K tile's 16-deep sub-steps split over the
+// waves (lhsT.rhs variant 4): every wave accumulates the whole block over
+// its own sub-steps, so it holds BM*BN/64 fp32 accumulators per lane, and
+// the epilogue sums the waves' blocks through LDS one 32-row slice at a time
+// (WAVES slots of 32 rows, row stride BN*4+16 bytes).
+MI_HD constexpr int lds_mm_kw(int bm, int bn, int bk, int waves, int stages) {
+  return cmax(stages * (bk * bm * 2 + bk * bn * 2), waves * 32 * (bn * 4 + 16));
+}
+MI_HD constexpr Legal legal_mm_kw(int bm, int bn, int bk, int waves, int stages) {
+  if (!block_mn_ok(bm, bn) || !is_pow2(bk) || bk < 32 || bk > 128)
+    return bad(MI_E_TILE, "block_m, block_n must be powers of two in [32, 512] and block_k in [32, 128]");
+  if (!waves_ok(waves) || (bk / 16) % waves != 0)
+    return bad(MI_E_WAVE_TILE, "the waves must split a K tile's block_k/16 sub-steps evenly");
+  if (bm * bn / 64 * ((waves + 3) / 4) > 256)
+    return bad(MI_E_WAVE_TILE, "each wave's accumulators (the whole block) exceed its share of the 512 registers");
+  if (stages < 2 || stages > 4) return bad(MI_E_TILE, "this variant takes 2..4 LDS stages");
+  // Operand registers alternate between two buffers across the ring.
+  if ((stages * (bk / 16 / waves)) % 2 != 0)
+    return bad(MI_E_TILE, "an odd number of sub-steps per wave needs an even number of LDS stages");
+  if (!mn_panel_ok(bk, bm) || !mn_panel_ok(bk, bn)) return bad(MI_E_TILE, "a K panel is smaller than one 1 KiB wave load");
+  if (stages > 2 && !(mn_panel_even(bk, bm, waves) && mn_panel_even(bk, bn, waves)))
+    return bad(MI_E_TILE, "more than 2 stages need every wave to issue the same number of panel loads");
+  if ((stages - 1) * (mn_panel_loads(bk, bm, waves) + mn_panel_loads(bk, bn, waves)) >= 64)
+    return bad(MI_E_TILE, "loads in flight exceed the 6-bit vmcnt");
+  if (lds_mm_kw(bm, bn, bk, waves, stages) > kLdsBytesMax) return bad(MI_E_LDS, "LDS over 160 KiB");
+  return ok();
+}
+
 // ---- main pass of the two-pass fused kernel (rmsnorm_matmul variant 13):
 // the pipelined lhsT.rhs core plus the block's BM row scales in LDS.
 MI_HD constexpr int lds_rms2(int bm, int bn, int bk, int waves, int stages) {

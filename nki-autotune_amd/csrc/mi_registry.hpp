@@ -99,6 +99,24 @@ hipError_t launch_mm_pipe(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// K split over the waves of a workgroup (variant 4), unsplit or split-K.
+template <int BM, int BN, int BK, int W, int S>
+hipError_t launch_mm_kw(const MiArgs& a, hipStream_t s) {
+  if (a.parts > 1) {
+    hipLaunchKernelGGL((mm_lhsT_rhs_bf16_kw_kernel<BM, BN, BK, W, S, true>),
+                       dim3(grid_tiles(a.M, a.N, BM, BN) * a.parts), dim3(W * 64), 0, s, (const uint16_t*)a.a,
+                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, (float*)a.ws);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    launch_splitk_sum((const float*)a.ws, (uint16_t*)a.out, (size_t)a.M * (size_t)a.N, a.parts, s);
+  } else {
+    hipLaunchKernelGGL((mm_lhsT_rhs_bf16_kw_kernel<BM, BN, BK, W, S, false>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                       dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N,
+                       a.K, a.group_m, 1, nullptr);
+  }
+  return hipGetLastError();
+}
+
 template <int BM, int BN, int BK, int W, int S, bool NTB = false>
 hipError_t launch_mm_lhs(const MiArgs& a, hipStream_t s) {
   if (a.parts > 1) {
@@ -213,6 +231,12 @@ hipError_t launch_rms_2pass(const MiArgs& a, hipStream_t s) {
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);    \
   template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, true>(  \
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
+// K split over the waves (variant 4), unsplit and split-K instances.
+#define MI_MMW_INST(BM, BN, BK, W, S)                                                  \
+  template __global__ void mm_lhsT_rhs_bf16_kw_kernel<BM, BN, BK, W, S, false>(       \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);  \
+  template __global__ void mm_lhsT_rhs_bf16_kw_kernel<BM, BN, BK, W, S, true>(        \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
 #define MI_MMK_INST(BM, BN, BK, W, S)                                                    \
   template __global__ void mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, false, false>( \
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);    \
@@ -272,6 +296,10 @@ hipError_t launch_rms_2pass(const MiArgs& a, hipStream_t s) {
 #define MI_MMPN_ROW(BM, BN, BK, W, S)                                                              \
   {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 3}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
    &launch_mm_pipe<BM, BN, BK, W, S, true>},
+// Pipelined matmul with each K tile's sub-steps split over the waves: variant 4.
+#define MI_MMW_ROW(BM, BN, BK, W, S)                                                               \
+  {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 4}, lds_mm_kw(BM, BN, BK, W, S), \
+   &launch_mm_kw<BM, BN, BK, W, S>},
 // matmul_lhs_rhs (K-contiguous lhs) on the pipelined core: variant 0.
 #define MI_MMK_ROW(BM, BN, BK, W, S)                                                                \
   {MI_KERNEL_MATMUL_LHS_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 0}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
@@ -337,6 +365,7 @@ const MiEntry* table_mm_bm64(int* n);
 const MiEntry* table_mm_bm128(int* n);
 const MiEntry* table_mm_bm256(int* n);
 const MiEntry* table_mm_pipe(int* n);
+const MiEntry* table_mm_kw(int* n);
 const MiEntry* table_mm_reg(int* n);
 const MiEntry* table_mm_lhs(int* n);
 const MiEntry* table_rms_xreg(int* n);

@@ -170,7 +170,7 @@ def split_k_variants(func_name: str, grid: list[TileConfig], M: int, N: int) -> 
     fewer than two waves of workgroups on the GPU (< 512 tiles): K is then
     the only axis left to spread the work over more compute units.  Part
     counts keep the grid within 1024 workgroups (four per compute unit)."""
-    splittable = {"matmul_lhsT_rhs": (1, 3), "matmul_lhsT_rhs_nkigym": (1, 3), "matmul_lhs_rhs": (0, 2),
+    splittable = {"matmul_lhsT_rhs": (1, 3, 4), "matmul_lhsT_rhs_nkigym": (1, 3, 4), "matmul_lhs_rhs": (0, 2),
                   "matmul_lhs_rhs_nkigym": (0, 2), "rmsnorm_matmul": (4, 5, 11, 12, 13),
                   "rmsnorm_matmul_online": (4, 5, 11, 12, 13)}.get(func_name, ())
     out = []

@@ -95,6 +95,13 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (MM, TileConfig(128, 128, 64, 4, 3, split_k=2, variant=1), (2048, 1024, 64), _lib.MI_E_SPLIT),   # 1 K tile
         (MM, TileConfig(128, 128, 64, 4, 3, split_k=3, variant=1), (2048, 1024, 256), _lib.MI_E_SPLIT),  # 2+2+0
         (MM, TileConfig(128, 128, 64, 4, 3, split_k=2, variant=2), (2048, 1024, 8192), _lib.MI_E_SPLIT),
+        # variant 4: K sub-steps split over the waves, each wave holding the whole block
+        (MM, TileConfig(128, 128, 64, 4, 4, variant=4), (1024, 4096, 14336), _lib.MI_OK),
+        (MM, TileConfig(128, 128, 64, 4, 4, split_k=2, variant=4), (2048, 1024, 8192), _lib.MI_OK),
+        (MM, TileConfig(128, 128, 64, 4, 3, variant=4), (1024, 1024, 1024), _lib.MI_E_TILE),        # odd stages x 1 sub-step
+        (MM, TileConfig(256, 128, 64, 4, 2, variant=4), (1024, 1024, 1024), _lib.MI_E_WAVE_TILE),   # 512 acc regs
+        (MM, TileConfig(128, 128, 32, 4, 2, variant=4), (1024, 1024, 1024), _lib.MI_E_WAVE_TILE),   # 2 sub-steps, 4 waves
+        (MM, TileConfig(128, 128, 128, 4, 3, variant=4), (1024, 1024, 1024), _lib.MI_E_LDS),        # 3 x 64 KiB
         (LHS, TileConfig(128, 128, 64, 4, 3, split_k=2), (2048, 1024, 8192), _lib.MI_OK),
         (LHS, TileConfig(128, 128, 64, 4, 3, split_k=4, variant=2), (128, 28672, 8192), _lib.MI_OK),
         (LHS, TileConfig(256, 256, 32, 8, 3, split_k=2, variant=1), (2048, 1024, 8192), _lib.MI_E_SPLIT),
@@ -134,7 +141,7 @@ def test_split_k_variants_are_named_and_legal():
     assert c.name == "bm128_bn128_bk64_w4_s3_v1_k4" and TileConfig.from_name(c.name) == c
     few = legal_configs("matmul_lhsT_rhs", 2048, 1024, 8192)
     split = [x for x in few if x.split_k > 1]
-    assert split and all(x.variant in (1, 3) for x in split)
+    assert split and all(x.variant in (1, 3, 4) for x in split)
     assert not [x for x in legal_configs("matmul_lhsT_rhs", 8192, 8192, 8192) if x.split_k > 1 and x.block_m >= 128
                 and x.block_n >= 128]
     assert split_k_variants("matmul_lhsT_rhs_f32", compiled_configs("matmul_lhsT_rhs_f32"), 16, 16) == []

@@ -78,9 +78,13 @@ def test_bf16_every_config_small_fixture(gpu):
         bits = out.view(torch.int16).cpu().numpy()
         # Same K order in every config (ascending, 16 per MFMA): bitwise equal.
         # Split-K sums fp32 partials over K ranges, so configs are bitwise
-        # equal when they split K at the same boundaries.
+        # equal when they split K at the same boundaries.  Variant 4 sums
+        # each wave's K sub-steps, then the waves: equal when its split of
+        # every K tile into waves' sub-steps is the same.
         kts = -(-(-(-K // cfg.block_k)) // cfg.split_k) * cfg.block_k
         key = tuple(range(0, K, kts)) if cfg.split_k > 1 else ()
+        if cfg.variant == 4:
+            key += ("kw", cfg.block_k, cfg.waves)
         if key not in first:
             first[key] = (cfg, bits)
         else:
