@@ -77,7 +77,8 @@ enum {
  *                               A call's workspace is at most 2 GiB; the pool
  *                               keeps at most 256 MiB of freed workspace
  *                               cached per device and returns the rest to
- *                               the device at the next synchronisation.
+ *                               the device at a synchronisation that
+ *                               begins after the call's launches finished.
  *                               Under HIP graph capture the workspace becomes
  *                               allocation and free nodes of the graph.
  *   group_m                   : L2 raster group height in tiles (0 = default 8)

@@ -276,7 +276,8 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
 // packed operand): allocated per call, stream-ordered (hipMallocFromPoolAsync
 // / hipFreeAsync), from a memory pool the library keeps per device.  The
 // pool keeps at most kPoolKeepBytes of freed memory cached for the next
-// calls and returns the rest to the device at the next synchronisation.
+// calls and returns the rest to the device at a synchronisation (stream,
+// event or device) that begins after the freeing launch has finished.
 // Each call has its own buffer (calls on different streams do not share
 // one), and a call under HIP graph capture becomes allocation and free
 // nodes of the graph.

@@ -84,7 +84,7 @@ def test_bf16_every_config_small_fixture(gpu):
         kts = -(-(-(-K // cfg.block_k)) // cfg.split_k) * cfg.block_k
         key = tuple(range(0, K, kts)) if cfg.split_k > 1 else ()
         if cfg.variant == 4:
-            key += ("kw", cfg.block_k, cfg.waves)
+            key += ("kw", cfg.block_k // 16 // cfg.waves, cfg.waves)
         if key not in first:
             first[key] = (cfg, bits)
         else:
@@ -107,6 +107,37 @@ def test_bf16_ragged_shapes(gpu, M, N, K):
         out = kl.matmul_lhsT_rhs(a, b, cfg=cfg)
         rep = mm_check(_host(out), expected)
         assert rep["ok"], (M, N, K, cfg, rep)
+
+
+@pytest.mark.parametrize("M,N,K", [(200, 136, 1040), (8, 8, 7), (264, 520, 100), (1024, 512, 14336)])
+def test_kw_variant_ragged_and_deterministic(gpu, M, N, K):
+    """Matmul variant 4 (K sub-steps split over the waves, the waves' blocks
+    summed in the epilogue) at ragged and long-K shapes, every prebuilt
+    config: against the oracle, two runs bitwise equal, and configs that
+    split each K tile over the waves the same way bitwise equal."""
+    import torch
+
+    kl = _kl()
+    d = mm_inputs(K, M, N, seed=11)
+    a, b = _dev(d["lhs_T"], torch.bfloat16, gpu), _dev(d["rhs"], torch.bfloat16, gpu)
+    expected = omm.closed_form(d["lhs_T"], d["rhs"])
+    cfgs = [c for c in kl.legal_configs("matmul_lhsT_rhs", M, N, K) if c.variant == 4 and c.split_k == 1]
+    assert cfgs
+    first = {}
+    for cfg in cfgs:
+        print("variant 4", cfg.name, M, N, K, flush=True)
+        out = kl.matmul_lhsT_rhs(a, b, cfg=cfg)
+        again = kl.matmul_lhsT_rhs(a, b, cfg=cfg)
+        torch.cuda.synchronize()
+        rep = mm_check(_host(out), expected)
+        assert rep["ok"], (M, N, K, cfg, rep)
+        assert torch.equal(out, again), cfg
+        key = (cfg.block_k // 16 // cfg.waves, cfg.waves)
+        bits = out.view(torch.int16).cpu().numpy()
+        if key in first:
+            assert np.array_equal(bits, first[key][1]), (cfg, first[key][0])
+        else:
+            first[key] = (cfg, bits)
 
 
 def test_bf16_identity_and_brute_force(gpu):

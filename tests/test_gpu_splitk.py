@@ -47,6 +47,8 @@ CONFIGS = [
     (256, 256, 32, 4, 3, 1),
     (32, 128, 128, 4, 3, 3),
     (128, 128, 64, 4, 3, 3),
+    (128, 128, 64, 4, 4, 4),   # K sub-steps split over the waves
+    (128, 128, 32, 2, 4, 4),
 ]
 
 
@@ -327,9 +329,12 @@ def test_rmsnorm_default_past_the_gamma_limit(gpu, M, K, N):
 
 
 def test_pool_returns_memory_after_a_large_call(gpu):
-    """A split-K call whose workspace is 1 GiB: after synchronisation the
-    library's pool keeps at most 256 MiB of it cached, so the device's free
-    memory is back within that of its level before the call."""
+    """A split-K call whose workspace is 1 GiB: once a synchronisation that
+    begins after the call's launches have finished has run, the library's
+    pool keeps at most 256 MiB of it cached, so the device's free memory is
+    back within that of its level before the call.  (The first
+    synchronisation below starts while the launches still run; the pool
+    releases memory at a synchronisation, not in the middle of one.)"""
     import torch
 
     import kernel_library as kl
@@ -343,6 +348,7 @@ def test_pool_returns_memory_after_a_large_call(gpu):
     torch.cuda.synchronize()
     free_before = torch.cuda.mem_get_info(gpu)[0]
     kl.matmul_lhsT_rhs(a, b, cfg=tc, out=out)
+    torch.cuda.synchronize()
     torch.cuda.synchronize()
     free_after = torch.cuda.mem_get_info(gpu)[0]
     held = free_before - free_after
