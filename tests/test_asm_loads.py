@@ -58,8 +58,8 @@ def test_async_register_loads_untouched_until_waited(unit, asm_of):
     assert total > 0
 
 
-@pytest.mark.parametrize("unit", ["mm_bf16_pipe.hip", "mm_bf16_lhs.hip", "mm_bf16_reg.hip", "rms_bf16_xreg.hip",
-                                  "rms_bf16_2pass.hip"])
+@pytest.mark.parametrize("unit", ["mm_bf16_pipe.hip", "mm_bf16_kw.hip", "mm_bf16_lhs.hip", "mm_bf16_reg.hip",
+                                  "rms_bf16_xreg.hip", "rms_bf16_2pass.hip"])
 def test_kernels_straight_line(unit, asm_of):
     """The unrolled tile lambdas are inlined: a device-function call would
     pass buffer descriptors in VGPRs and read captures through flat loads."""
