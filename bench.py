@@ -94,11 +94,13 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--sweep-reps", type=int, default=20)
     ap.add_argument("--config", default="", help="tile config name (e.g. bm256_bn256_bk32_w4_s3_v1) instead of the sweep")
-    ap.add_argument("--workload", choices=["c2", "c2-clock", "c3", "c3-matmul", "c4a", "c4b", "c4c", "c5", "decode"], default="c2",
+    ap.add_argument("--workload", choices=["c2", "c2-clock", "c3", "c3-matmul", "c4a", "c4b", "c4c", "c5", "decode",
+                                           "panel-stream"], default="c2",
                     help="c2: lhsT.rhs matmul 8192^3 (the metric); c3: rmsnorm_matmul 4096^3; c3-matmul: the plain "
                          "lhsT.rhs matmul at 4096^3; c4a/b/c: the C4 "
                          "lhsT.rhs shapes; c5: skinny lhsT.rhs (--m) x 28672 x 8192; decode: rmsnorm_matmul at the "
-                         "c5 shape (all but c2: profiling workloads)")
+                         "c5 shape; panel-stream: the K-panel loads alone from L2, MALL and HBM (all but c2: "
+                         "profiling workloads)")
     ap.add_argument("--settle-s", type=float, default=2.0,
                     help="GPU idle time before the timed region's warm-up (see settle())")
     ap.add_argument("--m", type=int, default=16, choices=[16, 64, 128], help="M of the c5 / decode workloads")
@@ -495,6 +497,8 @@ def main() -> int:
         return skinny_main(args, dev)
     if args.workload == "c2-clock":
         return clock_study(args, dev)
+    if args.workload == "panel-stream":
+        return panel_stream_study(args, dev)
     if args.workload in PLAIN_SHAPES:
         return shape_main(args, dev, *PLAIN_SHAPES[args.workload])
     fam, s = ("matmul_lhsT_rhs", M) if args.workload == "c2" else ("rmsnorm_matmul", 4096)
@@ -669,6 +673,50 @@ def clock_study(args, dev) -> int:
         log(json.dumps(row))
     print(json.dumps({"workload": "c2-clock", "shape": [s, s, s], "rounds": rounds,
                       "data": "lhsT, rhs ~ U(-1,1) seed 0 rounded to bf16", "rows": table}), flush=True)
+    return 0
+
+
+def panel_stream_study(args, dev) -> int:
+    """--workload panel-stream: how fast can a CU's LDS-direct K-panel loads run with nothing else to do?
+
+    The kernels' panel loads (1 KiB per wave instruction, straight into LDS)
+    with no LDS reads and no MFMA, one workgroup per CU, at 4 or 8 waves and
+    4..16 loads in flight per wave.  Each launch moves 1 GiB.  Rows:
+
+    * consecutive 1 KiB chunks of a 2 MiB region (held in every XCD's L2
+      after the first pass), a 64 MiB one (from the MALL) and a 1 GiB one
+      (from HBM);
+    * the panel shapes of the benchmark kernels from a 2 MiB region: K rows
+      of 64, 128 or 256 bf16 columns (128, 256, 512 bytes) out of matrix
+      rows 2048 to 16384 bytes long (the lhsT / rhs pitches of C2, C4a, C4c);
+    * the skinny weight panel (128 columns of a 28672-column rhs) over a
+      896 MiB region (HBM).
+
+    The L2 rows bound every kernel whose panels are L2 hits: its panel
+    bytes per CU over the L2 rows' bytes per clock per CU is the fewest
+    clocks it can take."""
+    import torch
+
+    from kernel_library import _probe
+
+    buf = torch.ones(1 << 28, dtype=torch.float32, device=dev)  # 1 GiB
+    cases = [("L2 contiguous", 2 << 20, 1024, 1024), ("MALL contiguous", 64 << 20, 1024, 1024),
+             ("HBM contiguous", 1 << 30, 1024, 1024),
+             ("L2 C4a lhsT panel (64 of 2048 cols)", 2 << 20, 128, 4096),
+             ("L2 C4a rhs panel (128 of 1024 cols)", 2 << 20, 256, 2048),
+             ("L2 C4c panel (128 of 4096 cols)", 2 << 20, 256, 8192),
+             ("L2 C2 panel (256 of 8192 cols)", 2 << 20, 512, 16384),
+             ("L2 64-col panel of 8192 cols", 2 << 20, 128, 16384),
+             ("HBM skinny rhs panel (128 of 28672 cols)", 57344 * 4 * 4096, 256, 57344)]
+    rows = []
+    for label, region, rb, pitch in cases:
+        for w, inf in ((4, 8), (4, 16), (8, 8)):
+            rounds = max(1, (1 << 30) // (256 * w * inf * 1024))
+            r = dict(case=label, **_probe.panel_stream(buf, region, w, inf, rounds, row_bytes=rb, pitch=pitch))
+            log(json.dumps(r))
+            rows.append(r)
+    print(json.dumps({"workload": "panel-stream", "wgs": 256, "bytes_per_launch": 1 << 30, "rows": rows}),
+          flush=True)
     return 0
 
 

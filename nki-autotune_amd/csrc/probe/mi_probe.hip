@@ -20,6 +20,14 @@
 //   On data drawn like the benchmark's, these are the rates of the MFMA
 //   pipe alone, and with its operand reads, under the chip's power limit:
 //   ceilings for any kernel that has to run those instructions.
+//
+// mi_probe_panel_stream: the kernels' K-panel loads alone -- LDS-direct
+//   buffer_load_dwordx4 ... lds, one 1 KiB chunk (64 lanes x 16 bytes) per
+//   wave instruction -- with no LDS reads and no MFMA.  One workgroup per
+//   CU (its static LDS keeps a second one off the CU), every wave streaming
+//   consecutive chunks of a `region`-byte buffer with INFLIGHT loads in
+//   flight.  A region that fits in one XCD's L2 gives the L2 -> LDS rate a
+//   CU's panel loads can reach; larger ones the MALL and HBM paths.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -152,6 +160,63 @@ __global__ __launch_bounds__(256) void mfma_lds_kernel(const uint16_t* __restric
   }
 }
 
+constexpr int kStreamLds = 128 * 1024;
+
+template <int W, int INF>
+__global__ __launch_bounds__(W * 64) void panel_stream_kernel(const char* __restrict__ src, uint32_t region,
+                                                             int row_bytes, uint32_t pitch, int rounds,
+                                                             unsigned long long* __restrict__ clk) {
+  static_assert(W * INF * 1024 <= kStreamLds && INF < 64, "ring of INF 1 KiB slots per wave");
+  __shared__ __attribute__((aligned(1024))) char smem[kStreamLds];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(src, region);
+  // The buffer is a row-major matrix of `pitch`-byte rows; a panel is
+  // `row_bytes` of each row (the K rows of an MN-contiguous operand panel).
+  // A 1 KiB load covers 1024 / row_bytes consecutive rows of one panel:
+  // lane l takes row l*16 / row_bytes, bytes (l*16) % row_bytes.  Each wave
+  // walks its panel's rows from a spread-out start; panels of different
+  // waves sit at different column offsets.
+  const uint32_t rows = region / pitch, rpc = 1024u / (uint32_t)row_bytes;
+  const uint32_t panels = pitch / (uint32_t)row_bytes;
+  const unsigned long long gw = (unsigned long long)blockIdx.x * W + (unsigned)wave;
+  const uint32_t col0 = (uint32_t)(gw % panels) * (uint32_t)row_bytes;
+  const uint32_t lrow = (uint32_t)lane * 16u / (uint32_t)row_bytes, lcol = (uint32_t)lane * 16u % (uint32_t)row_bytes;
+  uint32_t r0 = (uint32_t)(gw * 977ull % (rows / rpc)) * rpc;
+  char* ring = smem + wave * INF * 1024;
+  const unsigned long long c0 = __builtin_amdgcn_s_memtime();
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  for (int r = 0; r < rounds; ++r)
+    static_for<INF>([&](auto s_c) __attribute__((always_inline)) {
+      vm_wait<INF - 1>();  // the load that last filled this slot has landed
+      lds_dma16(rs, ring + decltype(s_c)::value * 1024, (r0 + lrow) * pitch + col0 + lcol);
+      r0 = r0 + rpc >= rows ? 0 : r0 + rpc;
+    });
+  wait_vmem();
+  const unsigned long long c1 = __builtin_amdgcn_s_memtime();
+  const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    clk[2 * blockIdx.x] = c1 - c0;
+    clk[2 * blockIdx.x + 1] = t1 - t0;
+  }
+}
+
+#define MI_STREAM_CONFIGS(X) X(4, 2) X(4, 4) X(4, 8) X(4, 16) X(4, 32) X(8, 4) X(8, 8) X(8, 16)
+
+typedef void (*StreamFn)(const char*, uint32_t, int, uint32_t, int, int, unsigned long long*, hipStream_t);
+template <int W, int INF>
+void launch_stream(const char* src, uint32_t region, int row_bytes, uint32_t pitch, int rounds, int wgs,
+                   unsigned long long* clk, hipStream_t s) {
+  hipLaunchKernelGGL((panel_stream_kernel<W, INF>), dim3(wgs), dim3(W * 64), 0, s, src, region, row_bytes, pitch,
+                     rounds, clk);
+}
+struct StreamEntry {
+  int w, inf;
+  StreamFn fn;
+};
+#define MI_STREAM_ROW(W, INF) {W, INF, &launch_stream<W, INF>},
+const StreamEntry kStream[] = {MI_STREAM_CONFIGS(MI_STREAM_ROW)};
+
 // The configs of the clocked twin: the pipelined configs the benchmark's
 // 8192^3 sweep ships.
 #define MI_PROBE_CONFIGS(X) \
@@ -233,6 +298,30 @@ int mi_probe_mfma(const void* src, long long src_elems, float* out, unsigned lon
                        (const uint16_t*)src, src_elems, out, iters, clk);
   const hipError_t err = hipGetLastError();
   return err == hipSuccess ? MI_OK : -(int)err;
+}
+
+// The panel-load stream probe: `wgs` workgroups of `waves` waves, each wave
+// issuing rounds * inflight LDS-direct 1 KiB loads with `inflight` in
+// flight (waves/inflight one of MI_STREAM_CONFIGS), reading `row_bytes`
+// of each `pitch`-byte row of src[0, region): the panel loads of an
+// operand whose rows are `pitch` bytes long.  row_bytes: a power of two in
+// [16, 1024]; pitch: a multiple of row_bytes; region: a multiple of
+// pitch * 1024 / row_bytes, below 4 GiB.  clk receives 2 uint64 per
+// workgroup.  Returns 0, MI_E_ARGS, MI_E_NO_INSTANCE or -hipError_t.
+int mi_probe_panel_stream(const void* src, unsigned long long region, int row_bytes, unsigned long long pitch,
+                          int waves, int inflight, int wgs, int rounds, unsigned long long* clk, void* stream) {
+  if (!src || !clk || row_bytes < 16 || row_bytes > 1024 || (row_bytes & (row_bytes - 1)) || pitch < 16 ||
+      pitch % row_bytes || region >= (1ull << 32) || region < pitch * (1024 / row_bytes) ||
+      region % (pitch * (1024 / row_bytes)) || wgs <= 0 || rounds <= 0 || ((uintptr_t)src & 15))
+    return MI_E_ARGS;
+  for (const mi::probe::StreamEntry& e : mi::probe::kStream) {
+    if (e.w == waves && e.inf == inflight) {
+      e.fn((const char*)src, (uint32_t)region, row_bytes, (uint32_t)pitch, rounds, wgs, clk, (hipStream_t)stream);
+      const hipError_t err = hipGetLastError();
+      return err == hipSuccess ? MI_OK : -(int)err;
+    }
+  }
+  return MI_E_NO_INSTANCE;
 }
 
 }  // extern "C"

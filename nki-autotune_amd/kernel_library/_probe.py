@@ -9,7 +9,10 @@ Not part of the kernel_library API (nothing on the kernel path calls it):
 * :func:`mfma_ceiling` runs the MFMA work of a 128x128 wave tile on every
   SIMD with operands from registers (mode 0) or read from LDS the way the
   kernel reads them (mode 1), without global memory traffic, and returns
-  its rate and clock.
+  its rate and clock;
+* :func:`panel_stream` runs the kernels' LDS-direct K-panel loads alone
+  (one workgroup per CU, no LDS reads, no MFMA) over a buffer region and
+  returns the rate they reach: from L2 when the region fits in it.
 """
 
 from __future__ import annotations
@@ -38,6 +41,8 @@ def lib() -> ctypes.CDLL:
         h.mi_probe_clocked_lhsT_rhs.argtypes = [vp, vp, vp, ci, ci, ci, ctypes.POINTER(_lib.MiTileCfg), vp, vp]
         h.mi_probe_mfma.restype = ci
         h.mi_probe_mfma.argtypes = [vp, ctypes.c_longlong, vp, vp, ci, ci, vp]
+        h.mi_probe_panel_stream.restype = ci
+        h.mi_probe_panel_stream.argtypes = [vp, ctypes.c_ulonglong, ci, ctypes.c_ulonglong, ci, ci, ci, ci, vp, vp]
         _HANDLE = h
     return _HANDLE
 
@@ -104,4 +109,43 @@ def mfma_ceiling(src, mode: int, iters: int = 512, launches: int = 10, warmup: i
             "pct_of_peak_at_that_clock": round(100 * tf / (PEAK_BF16_TFLOPS * mhz / PEAK_CLOCK_MHZ), 1)}
 
 
-__all__ = ["clocked_lhsT_rhs", "lib", "mfma_ceiling", "PROBE_PATH"]
+def panel_stream(buf, region: int, waves: int, inflight: int, rounds: int, row_bytes: int = 1024,
+                 pitch: int = 1024, wgs: int = 256, launches: int = 10, warmup: int = 3) -> dict:
+    """Rate of the LDS-direct panel loads alone over ``buf``'s first ``region`` bytes.
+
+    ``buf`` is read as a matrix of ``pitch``-byte rows, each panel load
+    taking ``row_bytes`` of 1024 / row_bytes consecutive rows (the K panel
+    of an MN-contiguous operand whose rows are ``pitch`` bytes); the default
+    reads consecutive 1 KiB chunks.  ``wgs`` workgroups (one per CU) of
+    ``waves`` waves, each wave keeping ``inflight`` 1 KiB loads in flight
+    for ``rounds * inflight`` loads.
+    Returns the median launch time, the aggregate GB/s, the engine clock,
+    bytes per clock per CU and 128-byte L2 requests per clock per XCD.
+    """
+    import torch
+
+    clk = torch.zeros((launches + warmup, wgs, 2), dtype=torch.int64, device=buf.device)
+    stream = torch.cuda.current_stream(buf.device)
+    events = []
+    for i in range(launches + warmup):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        rc = lib().mi_probe_panel_stream(buf.data_ptr(), region, row_bytes, pitch, waves, inflight, wgs, rounds,
+                                         clk[i].data_ptr(), stream.cuda_stream)
+        e1.record(stream)
+        if rc != 0:
+            raise _lib.KernelLibraryError(rc, f"panel stream probe w{waves} inflight {inflight} failed")
+        events.append((e0, e1))
+    torch.cuda.synchronize()
+    nbytes = float(wgs) * waves * rounds * inflight * 1024
+    us = statistics.median(events[i][0].elapsed_time(events[i][1]) * 1e3 for i in range(warmup, launches + warmup))
+    mhz = statistics.median(_clock_mhz(clk[i]) for i in range(warmup, launches + warmup))
+    cycles = us * mhz
+    return {"waves": waves, "inflight": inflight, "row_bytes": row_bytes, "pitch": pitch,
+            "region_mib": round(region / 2 ** 20, 2), "us": round(us, 1),
+            "gbs": round(nbytes / (us * 1e-6) / 1e9, 1), "clock_mhz": round(mhz, 1),
+            "bytes_per_clk_per_cu": round(nbytes / wgs / cycles, 1),
+            "l2_req_per_clk_per_xcd": round(nbytes / 128 / 8 / cycles, 2)}
+
+
+__all__ = ["clocked_lhsT_rhs", "lib", "mfma_ceiling", "panel_stream", "PROBE_PATH"]

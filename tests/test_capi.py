@@ -41,8 +41,24 @@ def test_probe_library_loads_and_exports_its_probes():
     from kernel_library import _probe
 
     h = _probe.lib()
-    for s in ("mi_probe_clocked_lhsT_rhs", "mi_probe_mfma"):
+    for s in ("mi_probe_clocked_lhsT_rhs", "mi_probe_mfma", "mi_probe_panel_stream"):
         assert getattr(h, s) is not None, s
+
+
+def test_panel_stream_probe_rejects_bad_arguments_before_any_gpu_call():
+    """The stream probe checks its region / row / pitch arguments on the host (fake pointers, no launch)."""
+    from kernel_library import _probe
+
+    h, fake, clk = _probe.lib(), 0x100000, 0x200000
+    args = lambda region, rb, pitch, w=4, inf=8: h.mi_probe_panel_stream(fake, region, rb, pitch, w, inf, 256, 1,
+                                                                          clk, None)
+    assert args(1 << 20, 96, 1024) == _lib.MI_E_ARGS            # row_bytes not a power of two
+    assert args(1 << 20, 2048, 2048) == _lib.MI_E_ARGS          # row_bytes above 1 KiB
+    assert args(1 << 20, 128, 1000) == _lib.MI_E_ARGS           # pitch not a multiple of row_bytes
+    assert args((1 << 20) + 4096, 128, 4096) == _lib.MI_E_ARGS  # region not a whole number of 8-row groups
+    assert args(1 << 32, 1024, 1024) == _lib.MI_E_ARGS          # region past the 32-bit buffer offsets
+    assert args(1 << 20, 1024, 1024, w=4, inf=3) == _lib.MI_E_NO_INSTANCE
+    assert h.mi_probe_panel_stream(fake + 8, 1 << 20, 1024, 1024, 4, 8, 256, 1, clk, None) == _lib.MI_E_ARGS
 
 
 def test_every_compiled_config_is_enumerable_and_legal():
