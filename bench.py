@@ -95,11 +95,12 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--sweep-reps", type=int, default=20)
     ap.add_argument("--config", default="", help="tile config name (e.g. bm256_bn256_bk32_w4_s3_v1) instead of the sweep")
     ap.add_argument("--workload", choices=["c2", "c2-clock", "c3", "c3-matmul", "c4a", "c4b", "c4c", "c5", "decode",
-                                           "panel-stream"], default="c2",
+                                           "panel-stream", "defaults"], default="c2",
                     help="c2: lhsT.rhs matmul 8192^3 (the metric); c3: rmsnorm_matmul 4096^3; c3-matmul: the plain "
                          "lhsT.rhs matmul at 4096^3; c4a/b/c: the C4 "
                          "lhsT.rhs shapes; c5: skinny lhsT.rhs (--m) x 28672 x 8192; decode: rmsnorm_matmul at the "
-                         "c5 shape; panel-stream: the K-panel loads alone from L2, MALL and HBM (all but c2: "
+                         "c5 shape; panel-stream: the K-panel loads alone from L2, MALL and HBM; defaults: the "
+                         "library's default config against the autotune sweep's best at 57 shapes (all but c2: "
                          "profiling workloads)")
     ap.add_argument("--settle-s", type=float, default=2.0,
                     help="GPU idle time before the timed region's warm-up (see settle())")
@@ -499,6 +500,8 @@ def main() -> int:
         return clock_study(args, dev)
     if args.workload == "panel-stream":
         return panel_stream_study(args, dev)
+    if args.workload == "defaults":
+        return defaults_study(args, dev)
     if args.workload in PLAIN_SHAPES:
         return shape_main(args, dev, *PLAIN_SHAPES[args.workload])
     fam, s = ("matmul_lhsT_rhs", M) if args.workload == "c2" else ("rmsnorm_matmul", 4096)
@@ -717,6 +720,61 @@ def panel_stream_study(args, dev) -> int:
             rows.append(r)
     print(json.dumps({"workload": "panel-stream", "wgs": 256, "bytes_per_launch": 1 << 30, "rows": rows}),
           flush=True)
+    return 0
+
+
+# (M, N, K) shapes of the default-config study, beside the benchmark's own.
+DEFAULTS_MM = [(1024, 1024, 1024), (2048, 2048, 2048), (3072, 3072, 3072), (4096, 4096, 4096), (6144, 6144, 6144),
+               (4096, 11008, 4096), (4096, 4096, 11008), (2048, 1024, 4096), (1024, 2048, 8192),
+               (8192, 1024, 8192), (512, 4096, 4096), (256, 14336, 4096), (1000, 2000, 3000), (8192, 8192, 1024),
+               (1024, 8192, 16384), (96, 8192, 8192), (4096, 14336, 1024), (2048, 1024, 8192),
+               (1536, 1536, 6144), (2048, 4096, 1024), (768, 3072, 3072), (4096, 1024, 2048), (12288, 4096, 4096),
+               (136, 4096, 4096), (6144, 2048, 2048), (2560, 2560, 10240), (512, 512, 32768), (16, 4096, 8192),
+               (64, 14336, 4096), (2048, 2048, 8192), (1280, 5120, 5120), (4608, 4608, 2304), (640, 10240, 2048),
+               (32, 2048, 16384), (3584, 1024, 4096), (1024, 3584, 14336), (200, 4096, 4096), (8192, 2048, 4096),
+               (6144, 768, 6144)]
+DEFAULTS_RMS = [(4096, 4096, 4096), (2048, 8192, 2048), (8192, 4096, 4096), (1024, 14336, 4096), (512, 4096, 8192),
+                (2048, 2048, 2048), (1024, 4096, 4096), (3072, 3072, 3072), (256, 8192, 4096), (1024, 1024, 4096),
+                (1536, 6144, 2048), (640, 8192, 4096), (4096, 2048, 4096), (128, 4096, 4096), (768, 6144, 4096),
+                (2560, 4096, 2048), (384, 8192, 8192), (1024, 8192, 1024)]
+
+
+def defaults_study(args, dev) -> int:
+    """--workload defaults: how close does a call without a config come to the autotuned best?
+
+    For each shape: the library default (``mi_default_config``, not the
+    tuned table) and the autotune sweep over every legal prebuilt config
+    (10 reps each, numerics-gated, the 4 fastest re-timed), then the default
+    and the sweep's winner re-timed together in 5 interleaved rounds.  One
+    JSON row per shape on stderr, the whole table as one line on stdout."""
+    import ctypes
+    import statistics
+
+    import kernel_library as kl
+    from autotune.tune import refine, tune
+    from kernel_library import _lib
+    from kernel_library.config import kernel_id
+
+    rows = []
+    for fam, shapes in (("matmul_lhsT_rhs", DEFAULTS_MM), ("rmsnorm_matmul", DEFAULTS_RMS)):
+        for m, n, k in shapes:
+            c = _lib.MiTileCfg()
+            _lib.check_rc(_lib.lib().mi_default_config(kernel_id(fam), m, n, k, ctypes.byref(c)), "mi_default_config")
+            dflt = kl.TileConfig.from_c(c)
+            res = tune(fam, m, n, k, check=True, warmup=3, reps=10, allow_jit=False, finalists=4, rounds=3)
+            if res.best is None:
+                raise RuntimeError(f"no working config for {fam} {m}x{n}x{k}")
+            cfgs = [dflt] if res.best.name == dflt.name else [dflt, res.best]
+            t = refine(fam, m, n, k, cfgs, rounds=5, reps=20)
+            row = {"kernel": fam, "shape": [m, n, k], "default": dflt.name, "default_us": round(t[dflt.name] * 1e6, 1),
+                   "best": res.best.name, "best_us": round(t[res.best.name] * 1e6, 1),
+                   "default_over_best": round(t[dflt.name] / t[res.best.name], 3),
+                   "best_tflops": round(2.0 * m * n * k / t[res.best.name] / 1e12, 1)}
+            log(json.dumps(row))
+            rows.append(row)
+    ratios = [r["default_over_best"] for r in rows]
+    print(json.dumps({"workload": "defaults", "shapes": len(rows), "median_default_over_best": statistics.median(ratios),
+                      "max_default_over_best": max(ratios), "rows": rows}), flush=True)
     return 0
 
 

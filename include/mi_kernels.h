@@ -124,10 +124,12 @@ int mi_num_configs(int kernel_id);
 int mi_get_config(int kernel_id, int idx, mi_tile_cfg* cfg);
 
 /* The library's default config for a kernel at a shape: always prebuilt and
- * legal there.  Generalised from the autotune winners: non-temporal variants
- * for skinny M, split-K for few output tiles with a long K; for the fused
- * kernel past the K its gamma staging holds, the two-pass kernel when there
- * are many output tiles and split-K otherwise. */
+ * legal there.  Generalised from the autotune winners: the block whose
+ * rounds of tiles take the least estimated time (rounds on the busiest CU
+ * times the block's area over its measured rate per CU), split-K when that
+ * grid leaves CUs idle, non-temporal variants for skinny M whose grid fills
+ * the chip; for the fused kernel past the K its gamma staging holds, the
+ * two-pass kernel when there are many output tiles and split-K otherwise. */
 int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
 
 /* out[M,N] = lhsT[K,M]^T . rhs[K,N]; bf16 storage, fp32 accumulation over

@@ -205,40 +205,127 @@ int zero_output(void* out, size_t n, void* stream) {
   return e == hipSuccess ? MI_OK : hip_fail(e, "zero fill");
 }
 
+// Default configs.  A grid fills the chip with one workgroup per CU on 256
+// CUs; 224 (28 per XCD) still counts as full.
+constexpr long long kFillTiles = 224;
+constexpr long long kCUs = 256;
+
+long long tiles_of(int M, int N, int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+
+// The most parts (a power of two, at most 16) that keep the grid within one
+// workgroup per CU, every part at least 4 K tiles of block_k, and no part
+// empty; 1 when no split qualifies.
+int fill_parts(long long tiles, int K, int block_k) {
+  const long long kt = ((long long)K + block_k - 1) / block_k;
+  int parts = 1;
+  for (int next = 2; next <= 16; next *= 2) {
+    const long long kts = (kt + next - 1) / next;
+    if (tiles * next > kCUs || kt < 4LL * next || (long long)(next - 1) * kts >= kt) break;
+    parts = next;
+  }
+  return parts;
+}
+
+// A candidate block and its relative throughput per CU (output area per
+// unit time at the same K, the 256 x 256 block = 1), measured with the
+// autotuner at shapes that give every CU one tile.
+struct Cand {
+  mi_tile_cfg c;
+  double rate;
+};
+
+// The candidate with the least estimated time: the rounds of tiles the
+// busiest CU runs, times a tile's area over its rate.  Ties go to the
+// earlier (larger) block.  Then, if its grid leaves CUs idle, K is split
+// (when the variant allows it) so the grid fills the chip.
+mi_tile_cfg fastest_estimate(const Cand* cands, int n, int M, int N, int K, bool split_ok) {
+  int best = 0;
+  double best_t = 0.0;
+  for (int i = 0; i < n; ++i) {
+    const mi_tile_cfg& c = cands[i].c;
+    const long long rounds = (tiles_of(M, N, c.block_m, c.block_n) + kCUs - 1) / kCUs;
+    const double t = (double)rounds * c.block_m * c.block_n / cands[i].rate;
+    if (i == 0 || t < best_t) {
+      best = i;
+      best_t = t;
+    }
+  }
+  mi_tile_cfg c = cands[best].c;
+  const long long tiles = tiles_of(M, N, c.block_m, c.block_n);
+  if (split_ok && tiles < kFillTiles) c.split_k = fill_parts(tiles, K, c.block_k);
+  return c;
+}
+
+// As fastest_estimate, but each candidate is first split by fill_parts when
+// its grid leaves CUs idle, and its estimated time (microseconds) adds the
+// split's fp32 partial products: written once and read back once at about
+// 5 TB/s.  R0 is the fused kernel's 128 x 512 rate per CU at 4096^3, in
+// multiply-adds per second.
+mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K) {
+  constexpr double R0 = 2.28e12, kSplitBytesPerUs = 5e6;
+  int best = 0;
+  double best_t = 0.0;
+  mi_tile_cfg best_c = cands[0].c;
+  for (int i = 0; i < n; ++i) {
+    mi_tile_cfg c = cands[i].c;
+    const long long tiles = tiles_of(M, N, c.block_m, c.block_n);
+    c.split_k = tiles < kFillTiles ? fill_parts(tiles, K, c.block_k) : 1;
+    const long long rounds = (tiles * c.split_k + kCUs - 1) / kCUs;
+    const double kp = (double)((K + c.split_k - 1) / c.split_k);
+    double t = (double)rounds * c.block_m * c.block_n * kp / (cands[i].rate * R0) * 1e6;
+    if (c.split_k > 1) t += (double)c.split_k * M * N * 8.0 / kSplitBytesPerUs;
+    if (i == 0 || t < best_t) {
+      best = i;
+      best_t = t;
+      best_c = c;
+    }
+  }
+  (void)best;
+  return best_c;
+}
+
 int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
-  // The autotune winners at the benchmark shapes, generalised by size:
-  // skinny M (decode) streams the weight once and takes the non-temporal
-  // variants; mid-size products take 128 x 128 tiles for enough workgroups;
-  // large ones the 256 x 256 pipelined core.
-  const bool mid = (long long)M * N <= 2048LL * 2048LL;
+  // Generalised from the autotune winners at the benchmark shapes and a
+  // study of 30 other shapes: the block whose rounds of tiles take the
+  // least time (a block that leaves CUs idle can still beat a smaller one
+  // whose grid needs a second, partial round), with K split when the chosen
+  // grid leaves CUs idle.  Skinny M (decode) streams the weight once with
+  // the non-temporal variants when their grid fills the chip, and takes
+  // 64 x 64 blocks when it does not.  A 256-long block lies with its long
+  // side along the shorter output side (128 x 256 when M >= N), a 128-long
+  // one along N unless N is at least four times M, as the winners do.
   mi_tile_cfg c = {256, 256, 64, 8, 2, 1, 8, 0};
+  const bool m_long = M >= N, n_much_longer = (long long)N >= 4LL * M;
   if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_F32) {
     c = {64, 64, 16, 4, 1, 1, 0, 0};
-  } else if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16) {
-    if (M <= 32) c = {32, 128, 128, 4, 3, 1, 8, 3};
-    else if (M <= 64) c = {64, 128, 64, 4, 4, 1, 8, 3};
-    else if (M <= 128) c = {128, 128, 64, 4, 3, 1, 8, 3};
-    else if (mid) c = {128, 128, 64, 4, 3, 1, 8, 1};
-    else c = {256, 256, 32, 4, 3, 1, 8, 1};
-    // Few output tiles: 64 x 64 tiles, and K split (doubling the parts)
-    // while the grid stays within one workgroup per compute unit (the sweep's
-    // winners at 512x512x32768 and 256x1024x16384), every part keeps at
-    // least 4 K tiles and no part is empty.
-    const long long t64 = (long long)((M + 63) / 64) * ((N + 63) / 64);
-    if (M > 128 && t64 < 256) {
-      const long long kt = (K + 63) / 64;
-      int parts = 1;
-      for (int next = 2; next <= 16; next *= 2) {
-        const long long kts = (kt + next - 1) / next;
-        if (t64 * next > 256 || kt < 4LL * next || (long long)(next - 1) * kts >= kt) break;
-        parts = next;
-      }
-      if (parts > 1) c = {64, 64, 64, 4, 4, parts, 8, 1};
+  } else if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 || kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16) {
+    const bool lhs = kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16;
+    // lhsT.rhs: pipelined variant 1 (3: rhs non-temporal); lhs.rhs: variant
+    // 0 (2: rhs non-temporal), its 256 x 256 block the paired-load variant 1.
+    const int v = lhs ? 0 : 1, v_nt = lhs ? 2 : 3;
+    mi_tile_cfg skinny = lhs ? mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt}
+                        : M <= 32 ? mi_tile_cfg{32, 128, 128, 4, 3, 1, 8, v_nt}
+                        : M <= 64 ? mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt}
+                                  : mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt};
+    const mi_tile_cfg small = {64, 64, 64, 4, 4, 1, 8, v};
+    if (M <= 128 && tiles_of(M, N, skinny.block_m, skinny.block_n) >= kFillTiles) {
+      c = skinny;
+    } else if (M <= 128) {
+      c = small;
+      const long long tiles = tiles_of(M, N, 64, 64);
+      if (tiles < 64) c.split_k = fill_parts(tiles, K, 64);
+    } else {
+      const Cand cands[] = {
+          {lhs ? mi_tile_cfg{256, 256, 32, 8, 3, 1, 8, 1} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, v}, 1.0},
+          {m_long ? mi_tile_cfg{128, 256, lhs ? 64 : 32, 4, 3, 1, 8, v}
+                  : mi_tile_cfg{256, 128, lhs ? 64 : 32, 4, 3, 1, 8, v}, 0.93},
+          {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v}, 0.62},
+          {n_much_longer ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v}, 0.60},
+          {small, 0.35}};
+      c = fastest_estimate(cands, 5, M, N, K, true);
+      // The 256 x 256 lhs.rhs block (paired loads) has no split copy.
+      if (c.split_k > 1 && c.variant != v) c.split_k = 1;
     }
-  } else if (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16) {
-    if (M <= 128) c = {128, 128, 64, 4, 3, 1, 8, 2};
-    else if (mid) c = {128, 128, 64, 4, 3, 1, 8, 0};
-    else c = {256, 256, 32, 8, 3, 1, 8, 1};
   } else if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16) {
     // The register-staged kernels keep gamma in LDS (8192 entries here).
     // Past K = 8192, shapes with many output tiles take the two-pass kernel
@@ -246,7 +333,8 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
     // no split); the others split K into the fewest parts whose gamma fits
     // (1..16 parts, none empty); past that the LDS-staged kernel (variant 0)
     // takes any K.
-    const long long t128 = (long long)((M + 127) / 128) * ((N + 127) / 128);
+    const bool mid = (long long)M * N <= 2048LL * 2048LL;
+    const long long t128 = tiles_of(M, N, 128, 128);
     const mi_tile_cfg two_pass = mid ? mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, 13} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, 13};
     if (K > 8192 && M > 128 && t128 >= 256 &&
         mi::workspace_bytes(MI_KERNEL_RMSNORM_MATMUL_BF16, two_pass, M, N, K) <= kMaxWorkspace) {
@@ -262,11 +350,19 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
       if (!parts) c = M <= 128 ? mi_tile_cfg{64, 128, 64, 4, 2, 1, 8, 0} : mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0};
       else if (M <= 128) c = {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, parts, 8, 11};
       else c = {128, 128, 64, 4, 2, parts, 8, 4};
-    } else if (M <= 32) c = {32, 128, 64, 4, 3, 1, 8, 11};
-    else if (M <= 64) c = {64, 128, 64, 4, 3, 1, 8, 11};
-    else if (M <= 128) c = {128, 128, 64, 4, 3, 1, 8, 11};
-    else if (mid) c = {128, 128, 64, 4, 2, 1, 8, 4};
-    else c = {128, 512, 32, 8, 3, 1, 8, 4};
+    } else if (M <= 128) {
+      c = {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, 1, 8, 11};
+      c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
+    } else {
+      // Each workgroup scales its x rows once per column tile, so narrow
+      // blocks pay that work many times over: per CU, 128 x 256 runs at 0.83
+      // and 128 x 128 at 0.54 of the rate of 128 x 512.  Few-tile shapes
+      // split K, which the estimate charges for its fp32 partial products.
+      const Cand cands[] = {{mi_tile_cfg{128, 512, 32, 8, 3, 1, 8, 4}, 1.0},
+                            {mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 5}, 0.83},
+                            {mi_tile_cfg{128, 128, 64, 4, 2, 1, 8, 4}, 0.54}};
+      c = fastest_split_estimate(cands, 3, M, N, K);
+    }
   }
   *cfg = c;
   return MI_OK;

@@ -202,6 +202,32 @@ def test_library_default_is_legal_everywhere():
                     assert rc == _lib.MI_OK, (kid, M, N, K, TileConfig.from_c(c), _lib.last_error())
 
 
+@pytest.mark.parametrize("fam,shape,name", [
+    ("matmul_lhsT_rhs", (1024, 1024, 1024), "bm64_bn64_bk64_w4_s4_v1"),       # 64x64 fills the CUs; 128x128 gives 64 tiles
+    ("matmul_lhsT_rhs", (3072, 3072, 3072), "bm256_bn256_bk32_w4_s3_v1"),     # one round of 144 big tiles beats two of 128x256
+    ("matmul_lhsT_rhs", (8192, 8192, 8192), "bm256_bn256_bk32_w4_s3_v1"),
+    ("matmul_lhsT_rhs", (8192, 1024, 8192), "bm128_bn256_bk32_w4_s3_v1"),     # 256x256 would give 128 tiles
+    ("matmul_lhsT_rhs", (1024, 8192, 16384), "bm256_bn128_bk32_w4_s3_v1"),    # long side along the shorter output side
+    ("matmul_lhsT_rhs", (4096, 14336, 1024), "bm256_bn128_bk32_w4_s3_v1"),
+    ("matmul_lhsT_rhs", (2048, 1024, 8192), "bm64_bn128_bk64_w4_s4_v1"),
+    ("matmul_lhsT_rhs", (512, 4096, 4096), "bm128_bn64_bk64_w4_s4_v1"),       # N >= 4M: 128 along M
+    ("matmul_lhsT_rhs", (512, 512, 32768), "bm64_bn64_bk64_w4_s4_v1_k4"),     # few tiles, long K: split
+    ("matmul_lhsT_rhs", (16, 28672, 8192), "bm32_bn128_bk128_w4_s3_v3"),      # skinny, weight streamed non-temporally
+    ("matmul_lhsT_rhs", (96, 8192, 8192), "bm64_bn64_bk64_w4_s4_v1"),         # skinny with too few 128-wide tiles
+    ("rmsnorm_matmul", (4096, 4096, 4096), "bm128_bn512_bk32_w8_s3_v4"),
+    ("rmsnorm_matmul", (4096, 2048, 4096), "bm128_bn256_bk32_w4_s3_v5"),
+    ("rmsnorm_matmul", (512, 4096, 8192), "bm128_bn256_bk32_w4_s3_v5_k4"),
+    ("rmsnorm_matmul", (2048, 2048, 2048), "bm128_bn128_bk64_w4_s2_v4"),
+])
+def test_library_default_picks_the_measured_winners(fam, shape, name):
+    """mi_default_config's rounds-of-tiles estimate reproduces the sweep winners it was fitted to."""
+    c = _lib.MiTileCfg()
+    from kernel_library.config import kernel_id
+
+    assert _lib.lib().mi_default_config(kernel_id(fam), *shape, ctypes.byref(c)) == _lib.MI_OK
+    assert TileConfig.from_c(c).name == name
+
+
 def test_entry_points_reject_bad_arguments_before_any_gpu_call():
     """Negative sizes, null pointers and a non-finite eps are refused on the host; empty outputs are no-ops."""
     L = _lib.lib()
