@@ -100,7 +100,7 @@ def parse() -> argparse.Namespace:
                          "lhsT.rhs matmul at 4096^3; c4a/b/c: the C4 "
                          "lhsT.rhs shapes; c5: skinny lhsT.rhs (--m) x 28672 x 8192; decode: rmsnorm_matmul at the "
                          "c5 shape; panel-stream: the K-panel loads alone from L2, MALL and HBM; defaults: the "
-                         "library's default config against the autotune sweep's best at 57 shapes (all but c2: "
+                         "library's default config against the autotune sweep's best at 71 shapes (all but c2: "
                          "profiling workloads)")
     ap.add_argument("--settle-s", type=float, default=2.0,
                     help="GPU idle time before the timed region's warm-up (see settle())")
@@ -733,6 +733,9 @@ DEFAULTS_MM = [(1024, 1024, 1024), (2048, 2048, 2048), (3072, 3072, 3072), (4096
                (64, 14336, 4096), (2048, 2048, 8192), (1280, 5120, 5120), (4608, 4608, 2304), (640, 10240, 2048),
                (32, 2048, 16384), (3584, 1024, 4096), (1024, 3584, 14336), (200, 4096, 4096), (8192, 2048, 4096),
                (6144, 768, 6144)]
+DEFAULTS_LHS = [(1024, 1024, 1024), (2048, 2048, 2048), (3072, 3072, 3072), (4096, 4096, 4096), (8192, 1024, 8192),
+                (2048, 1024, 4096), (512, 4096, 4096), (1024, 8192, 16384), (96, 8192, 8192), (4096, 14336, 1024),
+                (16, 28672, 8192), (1536, 1536, 6144), (512, 512, 32768), (8192, 8192, 8192)]
 DEFAULTS_RMS = [(4096, 4096, 4096), (2048, 8192, 2048), (8192, 4096, 4096), (1024, 14336, 4096), (512, 4096, 8192),
                 (2048, 2048, 2048), (1024, 4096, 4096), (3072, 3072, 3072), (256, 8192, 4096), (1024, 1024, 4096),
                 (1536, 6144, 2048), (640, 8192, 4096), (4096, 2048, 4096), (128, 4096, 4096), (768, 6144, 4096),
@@ -756,7 +759,8 @@ def defaults_study(args, dev) -> int:
     from kernel_library.config import kernel_id
 
     rows = []
-    for fam, shapes in (("matmul_lhsT_rhs", DEFAULTS_MM), ("rmsnorm_matmul", DEFAULTS_RMS)):
+    for fam, shapes in (("matmul_lhsT_rhs", DEFAULTS_MM), ("matmul_lhs_rhs", DEFAULTS_LHS),
+                        ("rmsnorm_matmul", DEFAULTS_RMS)):
         for m, n, k in shapes:
             c = _lib.MiTileCfg()
             _lib.check_rc(_lib.lib().mi_default_config(kernel_id(fam), m, n, k, ctypes.byref(c)), "mi_default_config")

@@ -236,9 +236,9 @@ struct Cand {
 
 // The candidate with the least estimated time: the rounds of tiles the
 // busiest CU runs, times a tile's area over its rate.  Ties go to the
-// earlier (larger) block.  Then, if its grid leaves CUs idle, K is split
-// (when the variant allows it) so the grid fills the chip.
-mi_tile_cfg fastest_estimate(const Cand* cands, int n, int M, int N, int K, bool split_ok) {
+// earlier (larger) block.  Then, if its grid leaves CUs idle and K is long
+// enough to split, K is split so the grid fills the chip.
+mi_tile_cfg fastest_estimate(const Cand* cands, int n, int M, int N, int K, int kernel_id) {
   int best = 0;
   double best_t = 0.0;
   for (int i = 0; i < n; ++i) {
@@ -252,17 +252,34 @@ mi_tile_cfg fastest_estimate(const Cand* cands, int n, int M, int N, int K, bool
   }
   mi_tile_cfg c = cands[best].c;
   const long long tiles = tiles_of(M, N, c.block_m, c.block_n);
-  if (split_ok && tiles < kFillTiles) c.split_k = fill_parts(tiles, K, c.block_k);
+  if (tiles >= kFillTiles || fill_parts(tiles, K, c.block_k) == 1) return c;
+  // The grid needs a split: the largest splittable block whose split grid
+  // is as large as any (a bigger block moves fewer operand bytes per
+  // multiply-add for the same workgroup count).
+  long long most = 0;
+  for (int i = 0; i < n; ++i) {
+    const mi_tile_cfg& ci = cands[i].c;
+    if (!splittable(kernel_id, ci.variant)) continue;
+    const long long t = tiles_of(M, N, ci.block_m, ci.block_n);
+    const long long wgs = t * fill_parts(t, K, ci.block_k);
+    if (wgs > most) {
+      most = wgs;
+      c = ci;
+    }
+  }
+  c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
   return c;
 }
 
 // As fastest_estimate, but each candidate is first split by fill_parts when
 // its grid leaves CUs idle, and its estimated time (microseconds) adds the
-// split's fp32 partial products: written once and read back once at about
-// 5 TB/s.  R0 is the fused kernel's 128 x 512 rate per CU at 4096^3, in
-// multiply-adds per second.
+// split's fp32 partial products, written once and read back once at about
+// 5 TB/s, and for the two-pass fused kernel (variant 13) its pack pass (x
+// read, x * gamma written: 4 bytes per x element at about 5 TB/s) and 3 us
+// for the second launch.  R0 is the fused kernel's 128 x 512 rate per CU at
+// 4096^3, in multiply-adds per second.
 mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K) {
-  constexpr double R0 = 2.28e12, kSplitBytesPerUs = 5e6;
+  constexpr double R0 = 2.28e12, kSplitBytesPerUs = 5e6, kPackBytesPerUs = 5e6, kLaunchUs = 3.0;
   int best = 0;
   double best_t = 0.0;
   mi_tile_cfg best_c = cands[0].c;
@@ -274,6 +291,7 @@ mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K
     const double kp = (double)((K + c.split_k - 1) / c.split_k);
     double t = (double)rounds * c.block_m * c.block_n * kp / (cands[i].rate * R0) * 1e6;
     if (c.split_k > 1) t += (double)c.split_k * M * N * 8.0 / kSplitBytesPerUs;
+    if (c.variant == 13) t += (double)M * K * 4.0 / kPackBytesPerUs + kLaunchUs;
     if (i == 0 || t < best_t) {
       best = i;
       best_t = t;
@@ -291,9 +309,11 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
   // whose grid needs a second, partial round), with K split when the chosen
   // grid leaves CUs idle.  Skinny M (decode) streams the weight once with
   // the non-temporal variants when their grid fills the chip, and takes
-  // 64 x 64 blocks when it does not.  A 256-long block lies with its long
-  // side along the shorter output side (128 x 256 when M >= N), a 128-long
-  // one along N unless N is at least four times M, as the winners do.
+  // 64 x 64 blocks when it does not.  For lhsT.rhs a 256-long block lies
+  // with its long side along the shorter output side (128 x 256 when M >=
+  // N), a 128-long one along N unless N is at least four times M, as the
+  // winners do; lhs.rhs keeps block_m the short side (fewer rows of its
+  // K-contiguous operand per tile).
   mi_tile_cfg c = {256, 256, 64, 8, 2, 1, 8, 0};
   const bool m_long = M >= N, n_much_longer = (long long)N >= 4LL * M;
   if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_F32) {
@@ -301,7 +321,9 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
   } else if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 || kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16) {
     const bool lhs = kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16;
     // lhsT.rhs: pipelined variant 1 (3: rhs non-temporal); lhs.rhs: variant
-    // 0 (2: rhs non-temporal), its 256 x 256 block the paired-load variant 1.
+    // 0 (2: rhs non-temporal), its blocks of 256 rows or columns the
+    // paired-load variant 1 (block_k 32, the K-contiguous panel loaded as
+    // whole 128-byte lines).
     const int v = lhs ? 0 : 1, v_nt = lhs ? 2 : 3;
     mi_tile_cfg skinny = lhs ? mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt}
                         : M <= 32 ? mi_tile_cfg{32, 128, 128, 4, 3, 1, 8, v_nt}
@@ -317,14 +339,14 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
     } else {
       const Cand cands[] = {
           {lhs ? mi_tile_cfg{256, 256, 32, 8, 3, 1, 8, 1} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, v}, 1.0},
-          {m_long ? mi_tile_cfg{128, 256, lhs ? 64 : 32, 4, 3, 1, 8, v}
-                  : mi_tile_cfg{256, 128, lhs ? 64 : 32, 4, 3, 1, 8, v}, 0.93},
+          {lhs ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 1}
+               : (m_long ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v} : mi_tile_cfg{256, 128, 32, 4, 3, 1, 8, v}),
+           0.93},
           {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v}, 0.62},
-          {n_much_longer ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v}, 0.60},
+          {n_much_longer && !lhs ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v},
+           0.60},
           {small, 0.35}};
-      c = fastest_estimate(cands, 5, M, N, K, true);
-      // The 256 x 256 lhs.rhs block (paired loads) has no split copy.
-      if (c.split_k > 1 && c.variant != v) c.split_k = 1;
+      c = fastest_estimate(cands, 5, M, N, K, kernel_id);
     }
   } else if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16) {
     // The register-staged kernels keep gamma in LDS (8192 entries here).
@@ -351,17 +373,26 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
       else if (M <= 128) c = {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, parts, 8, 11};
       else c = {128, 128, 64, 4, 2, parts, 8, 4};
     } else if (M <= 128) {
+      // Weight streamed once (variant 11); a grid short of the CUs takes
+      // 64-row blocks before splitting K.
       c = {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, 1, 8, 11};
+      if (c.block_m == 128 && tiles_of(M, N, 128, 128) < kFillTiles) c.block_m = 64;
       c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
     } else {
-      // Each workgroup scales its x rows once per column tile, so narrow
-      // blocks pay that work many times over: per CU, 128 x 256 runs at 0.83
-      // and 128 x 128 at 0.54 of the rate of 128 x 512.  Few-tile shapes
-      // split K, which the estimate charges for its fp32 partial products.
+      // Each workgroup of the one-pass kernels scales its x rows once per
+      // column tile, so narrow blocks pay that work many times over: per CU,
+      // 128 x 256 runs at 0.83 and 128 x 128 at 0.54 of the rate of 128 x
+      // 512.  The two-pass kernel scales x once, in a pass of its own, and
+      // its main pass runs the lhsT core (256 x 256 at 1.10 of that rate).
+      // Few-tile shapes split K, which the estimate charges for its fp32
+      // partial products.
       const Cand cands[] = {{mi_tile_cfg{128, 512, 32, 8, 3, 1, 8, 4}, 1.0},
                             {mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 5}, 0.83},
-                            {mi_tile_cfg{128, 128, 64, 4, 2, 1, 8, 4}, 0.54}};
-      c = fastest_split_estimate(cands, 3, M, N, K);
+                            {mi_tile_cfg{128, 128, 64, 4, 2, 1, 8, 4}, 0.54},
+                            {mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, 13}, 1.10},
+                            {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, 13}, 0.68},
+                            {mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, 13}, 0.66}};
+      c = fastest_split_estimate(cands, 6, M, N, K);
     }
   }
   *cfg = c;
