@@ -271,8 +271,10 @@ mi_tile_cfg fastest_estimate(const Cand* cands, int n, int M, int N, int K, int 
   return c;
 }
 
-// As fastest_estimate, but each candidate is first split by fill_parts when
-// its grid leaves CUs idle, and its estimated time (microseconds) adds the
+// As fastest_estimate, for the fused kernel (whose first candidate needs no
+// workspace), but each candidate is first split by fill_parts when its grid
+// leaves CUs idle, a candidate whose device workspace would pass the 2 GiB
+// limit is skipped, and its estimated time (microseconds) adds the
 // split's fp32 partial products, written once and read back once at about
 // 5 TB/s, and for the two-pass fused kernel (variant 13) its pack pass (x
 // read, x * gamma written: 4 bytes per x element at about 5 TB/s) and 3 us
@@ -280,25 +282,26 @@ mi_tile_cfg fastest_estimate(const Cand* cands, int n, int M, int N, int K, int 
 // 4096^3, in multiply-adds per second.
 mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K) {
   constexpr double R0 = 2.28e12, kSplitBytesPerUs = 5e6, kPackBytesPerUs = 5e6, kLaunchUs = 3.0;
-  int best = 0;
   double best_t = 0.0;
   mi_tile_cfg best_c = cands[0].c;
+  bool found = false;
   for (int i = 0; i < n; ++i) {
     mi_tile_cfg c = cands[i].c;
     const long long tiles = tiles_of(M, N, c.block_m, c.block_n);
     c.split_k = tiles < kFillTiles ? fill_parts(tiles, K, c.block_k) : 1;
+    // A candidate whose workspace the call could not allocate is out.
+    if (mi::workspace_bytes(MI_KERNEL_RMSNORM_MATMUL_BF16, c, M, N, K) > kMaxWorkspace) continue;
     const long long rounds = (tiles * c.split_k + kCUs - 1) / kCUs;
     const double kp = (double)((K + c.split_k - 1) / c.split_k);
     double t = (double)rounds * c.block_m * c.block_n * kp / (cands[i].rate * R0) * 1e6;
     if (c.split_k > 1) t += (double)c.split_k * M * N * 8.0 / kSplitBytesPerUs;
     if (c.variant == 13) t += (double)M * K * 4.0 / kPackBytesPerUs + kLaunchUs;
-    if (i == 0 || t < best_t) {
-      best = i;
+    if (!found || t < best_t) {
+      found = true;
       best_t = t;
       best_c = c;
     }
   }
-  (void)best;
   return best_c;
 }
 

@@ -232,6 +232,19 @@ def test_library_default_picks_the_measured_winners(fam, shape, name):
     assert TileConfig.from_c(c).name == name
 
 
+def test_library_default_is_legal_at_large_shapes():
+    """Very tall operands (x or lhsT of 1-2 GiB): the default never takes a config whose workspace or
+    operand spans the call would reject."""
+    L = _lib.lib()
+    for kid in (MM, LHS, RMS):
+        for M, N, K in ((131072, 4096, 8192), (262144, 1024, 4096), (131072, 256, 8192), (65536, 8192, 16384),
+                        (512, 131072, 8192)):
+            c = _lib.MiTileCfg()
+            assert L.mi_default_config(kid, M, N, K, ctypes.byref(c)) == _lib.MI_OK
+            rc = L.mi_cfg_check(kid, ctypes.byref(c), M, N, K)
+            assert rc == _lib.MI_OK, (kid, M, N, K, TileConfig.from_c(c), _lib.last_error())
+
+
 def test_entry_points_reject_bad_arguments_before_any_gpu_call():
     """Negative sizes, null pointers and a non-finite eps are refused on the host; empty outputs are no-ops."""
     L = _lib.lib()
