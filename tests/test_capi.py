@@ -10,6 +10,8 @@ import re
 from pathlib import Path
 
 import pytest
+from hypothesis import given, settings
+from hypothesis import strategies as st
 
 from kernel_library import _lib
 from kernel_library.config import TileConfig, check, compiled_configs, default_config
@@ -243,6 +245,22 @@ def test_library_default_is_legal_at_large_shapes():
             assert L.mi_default_config(kid, M, N, K, ctypes.byref(c)) == _lib.MI_OK
             rc = L.mi_cfg_check(kid, ctypes.byref(c), M, N, K)
             assert rc == _lib.MI_OK, (kid, M, N, K, TileConfig.from_c(c), _lib.last_error())
+
+
+@settings(max_examples=400, deadline=None)
+@given(kid=st.sampled_from([MM, LHS, RMS]), m=st.integers(1, 16384), n=st.integers(1, 16384),
+       k=st.integers(1, 16384), big=st.sampled_from([1, 1, 1, 8]))
+def test_library_default_is_legal_for_random_shapes(kid, m, n, k, big):
+    """Property: for any shape the C ABI accepts (M, N multiples of 8, K too for the K-contiguous families,
+    operand spans under 4 GiB), the library default is a prebuilt config that mi_cfg_check accepts there."""
+    M, N, K = 8 * m * big, 8 * n, 8 * k if kid != MM else k * big
+    if 2 * (K + 1024) * max(M, N) >= 2 ** 32 or 2 * (M + 512) * K >= 2 ** 32:
+        return  # an operand span past the 32-bit buffer offsets: no config takes it
+    c = _lib.MiTileCfg()
+    L = _lib.lib()
+    assert L.mi_default_config(kid, M, N, K, ctypes.byref(c)) == _lib.MI_OK
+    assert L.mi_cfg_check(kid, ctypes.byref(c), M, N, K) == _lib.MI_OK, (kid, M, N, K, TileConfig.from_c(c),
+                                                                          _lib.last_error())
 
 
 def test_entry_points_reject_bad_arguments_before_any_gpu_call():
