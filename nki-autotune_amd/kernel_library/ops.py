@@ -43,6 +43,18 @@ def _same_device(first: str, ref: torch.Tensor, **others: torch.Tensor | None) -
             raise ValueError(f"{name} is on {t.device}, {first} on {ref.device}: all operands must share a device")
 
 
+def _no_overlap(out: torch.Tensor, **inputs: torch.Tensor | None) -> None:
+    """``out`` shares no bytes with an input: the kernels read the inputs while they write ``out``."""
+    o0 = out.data_ptr()
+    o1 = o0 + out.numel() * out.element_size()
+    for name, t in inputs.items():
+        if t is None or t.numel() == 0 or out.numel() == 0:
+            continue
+        t0 = t.data_ptr()
+        if t0 < o1 and o0 < t0 + t.numel() * t.element_size():
+            raise ValueError(f"out overlaps {name}: the output must not alias an input")
+
+
 def _check_operand(name: str, t: torch.Tensor, dtypes: tuple[torch.dtype, ...]) -> None:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor on a HIP device, got {type(t).__name__}")
@@ -76,6 +88,8 @@ def matmul_lhsT_rhs(
         out = torch.empty((M, N), dtype=lhs_T.dtype, device=lhs_T.device)
     elif out.shape != (M, N) or out.dtype != lhs_T.dtype or not out.is_contiguous():
         raise ValueError(f"out must be a contiguous {lhs_T.dtype} [{M},{N}] tensor")
+    else:
+        _no_overlap(out, lhs_T=lhs_T, rhs=rhs)
     fp32 = lhs_T.dtype == torch.float32
     name = "matmul_lhsT_rhs_f32" if fp32 else "matmul_lhsT_rhs"
     cfg = cfg if cfg is not None else default_config(name, M, N, K)
@@ -107,6 +121,8 @@ def matmul_lhs_rhs(
         out = torch.empty((M, N), dtype=lhs.dtype, device=lhs.device)
     elif out.shape != (M, N) or out.dtype != lhs.dtype or not out.is_contiguous():
         raise ValueError(f"out must be a contiguous bf16 [{M},{N}] tensor")
+    else:
+        _no_overlap(out, lhs=lhs, rhs=rhs)
     cfg = cfg if cfg is not None else default_config("matmul_lhs_rhs", M, N, K)
     c = cfg.to_c()
     with torch.cuda.device(lhs.device):
@@ -140,6 +156,8 @@ def rmsnorm_matmul(
         out = torch.empty((M, N), dtype=lhs.dtype, device=lhs.device)
     elif out.shape != (M, N) or out.dtype != lhs.dtype or not out.is_contiguous():
         raise ValueError(f"out must be a contiguous bf16 [{M},{N}] tensor")
+    else:
+        _no_overlap(out, lhs=lhs, rhs=rhs, gamma=gamma)
     if cfg is None:
         # Without gamma (the reference's contract) a no-gamma winner tuned for
         # the shape takes precedence.

@@ -331,3 +331,19 @@ def test_python_wrappers_validate_on_the_host():
         kl.rmsnorm_matmul(a, a, eps=1e-6)
     with pytest.raises(ValueError, match="HIP device"):
         kl.matmul_lhs_rhs(a, a.t().contiguous())
+
+
+def test_output_aliasing_an_input_is_rejected():
+    """The wrappers refuse an ``out`` that shares bytes with an input (host-side pointer ranges)."""
+    import torch
+
+    from kernel_library.ops import _no_overlap
+
+    buf = torch.zeros(4096, dtype=torch.bfloat16)
+    a, b = buf[:1024].view(32, 32), buf[1024:2048].view(32, 32)
+    _no_overlap(buf[2048:3072].view(32, 32), lhs=a, rhs=b)            # disjoint: accepted
+    _no_overlap(buf[2048:3072].view(32, 32), lhs=a, rhs=b, gamma=None)
+    with pytest.raises(ValueError, match="overlaps rhs"):
+        _no_overlap(buf[1500:2524].view(32, 32), lhs=a, rhs=b)
+    with pytest.raises(ValueError, match="overlaps lhs"):
+        _no_overlap(a, lhs=a, rhs=b)
