@@ -8,7 +8,8 @@
  * interface; the citation names it.  All pointers are device pointers owned
  * by the caller; tensors are row-major and contiguous.  bf16 tensors are
  * passed as raw 16-bit storage; bf16 operands must be 16-byte aligned
- * (fp32 ones 4-byte aligned).  Launches are asynchronous on `stream` (a
+ * (fp32 ones 4-byte aligned), and the output must not overlap an input
+ * (MI_E_ARGS).  Launches are asynchronous on `stream` (a
  * hipStream_t, NULL = default stream).  No entry point throws, and only a
  * call that needs device workspace allocates: a split-K config (split_k >
  * 1) and the two-pass fused kernel (rmsnorm_matmul variant 13) take it
@@ -44,7 +45,8 @@ enum {
   MI_E_ALIGN = 4,          /* M or N (or K of a K-contiguous operand) not a multiple of 8,
                               or a pointer not 16-byte aligned (4-byte for fp32)     */
   MI_E_RANGE = 5,          /* an operand is 4 GiB or larger (32-bit buffer offsets)  */
-  MI_E_ARGS = 6,           /* null pointer, non-positive size, bad eps               */
+  MI_E_ARGS = 6,           /* null pointer, non-positive size, bad eps, or an output
+                              that overlaps an input                                 */
   MI_E_KERNEL = 7,         /* unknown kernel id                                      */
   MI_E_SPLIT = 8,          /* split_k unsupported for this kernel / shape            */
   MI_E_TILE = 9            /* tile parameters the variant's template does not take, or

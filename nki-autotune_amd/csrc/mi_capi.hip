@@ -486,6 +486,13 @@ int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, voi
 
 // Device pointers are read and written in 16-byte vectors (bf16 kernels)
 // or as fp32 elements (the fp32 kernel).
+// [p, p + pb) and [q, q + qb) share a byte (null or empty ranges never do).
+bool overlaps(const void* p, size_t pb, const void* q, size_t qb) {
+  if (!p || !q || pb == 0 || qb == 0) return false;
+  const uintptr_t a = (uintptr_t)p, b = (uintptr_t)q;
+  return a < b + qb && b < a + pb;
+}
+
 bool misaligned(const void* p, uintptr_t align) { return p && ((uintptr_t)p & (align - 1)) != 0; }
 
 }  // namespace
@@ -504,6 +511,9 @@ int matmul_lhsT_rhs_bf16(const void* lhsT, const void* rhs, void* out, int M, in
   if (!lhsT || !rhs) return fail(MI_E_ARGS, "null input pointer");
   if (misaligned(lhsT, 16) || misaligned(rhs, 16) || misaligned(out, 16))
     return fail(MI_E_ALIGN, "lhsT, rhs and out must be 16-byte aligned");
+  const size_t ob = (size_t)M * N * 2;
+  if (overlaps(out, ob, lhsT, (size_t)K * M * 2) || overlaps(out, ob, rhs, (size_t)K * N * 2))
+    return fail(MI_E_ARGS, "out overlaps an input");
   mi::MiArgs a = {lhsT, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
   return run(MI_KERNEL_MATMUL_LHST_RHS_BF16, cfg, a, stream, fixed_ws, fixed_cap);
 }
@@ -559,6 +569,9 @@ int mi_matmul_lhs_rhs_bf16(const void* lhs, const void* rhs, void* out, int M, i
   if (!lhs || !rhs) return fail(MI_E_ARGS, "null input pointer");
   if (misaligned(lhs, 16) || misaligned(rhs, 16) || misaligned(out, 16))
     return fail(MI_E_ALIGN, "lhs, rhs and out must be 16-byte aligned");
+  const size_t ob = (size_t)M * N * 2;
+  if (overlaps(out, ob, lhs, (size_t)M * K * 2) || overlaps(out, ob, rhs, (size_t)K * N * 2))
+    return fail(MI_E_ARGS, "out overlaps an input");
   mi::MiArgs a = {lhs, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
   return run(MI_KERNEL_MATMUL_LHS_RHS_BF16, cfg, a, stream);
 }
@@ -574,6 +587,9 @@ int mi_matmul_lhsT_rhs_f32(const float* lhsT, const float* rhs, float* out, int 
   if (!lhsT || !rhs) return fail(MI_E_ARGS, "null input pointer");
   if (misaligned(lhsT, 4) || misaligned(rhs, 4) || misaligned(out, 4))
     return fail(MI_E_ALIGN, "lhsT, rhs and out must be 4-byte aligned");
+  const size_t ob = (size_t)M * N * 4;
+  if (overlaps(out, ob, lhsT, (size_t)K * M * 4) || overlaps(out, ob, rhs, (size_t)K * N * 4))
+    return fail(MI_E_ARGS, "out overlaps an input");
   mi::MiArgs a = {lhsT, rhs, nullptr, out, M, N, K, 0.0f, 0.0f, 8};
   return run(MI_KERNEL_MATMUL_LHST_RHS_F32, cfg, a, stream);
 }
@@ -586,6 +602,10 @@ int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void
   if (!x || !W || !out) return fail(MI_E_ARGS, "null pointer");
   if (misaligned(x, 16) || misaligned(gamma, 16) || misaligned(W, 16) || misaligned(out, 16))
     return fail(MI_E_ALIGN, "x, gamma, W and out must be 16-byte aligned");
+  const size_t ob = (size_t)M * N * 2;
+  if (overlaps(out, ob, x, (size_t)M * K * 2) || overlaps(out, ob, W, (size_t)K * N * 2) ||
+      overlaps(out, ob, gamma, (size_t)K * 2))
+    return fail(MI_E_ARGS, "out overlaps an input");
   mi::MiArgs a = {x, W, gamma, out, M, N, K, eps, 1.0f / (float)K, 8};
   return run(MI_KERNEL_RMSNORM_MATMUL_BF16, cfg, a, stream);
 }

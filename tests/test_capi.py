@@ -282,9 +282,10 @@ def test_entry_points_reject_bad_arguments_before_any_gpu_call():
     assert L.mi_rmsnorm_matmul_bf16(fake, None, fake, fake, 8, 8, 8, -1.0, ctypes.byref(c), None) == _lib.MI_E_ARGS
     assert L.mi_rmsnorm_matmul_bf16(fake, None, None, fake, 8, 8, 8, 1e-6, ctypes.byref(c), None) == _lib.MI_E_ARGS
     assert "null" in _lib.last_error()
-    # an illegal config is refused before the launch as well
+    # an illegal config is refused before the launch as well (operands 128 MiB apart: no overlap)
     bad = TileConfig(256, 256, 128, 8, 2).to_c()
-    assert L.mi_matmul_lhsT_rhs_bf16(fake, fake, fake, 8192, 8192, 8192, ctypes.byref(bad), None) == _lib.MI_E_LDS
+    a, b, o = (ctypes.c_void_p(0x10000000 + i * (1 << 28)) for i in range(3))
+    assert L.mi_matmul_lhsT_rhs_bf16(a, b, o, 8192, 8192, 8192, ctypes.byref(bad), None) == _lib.MI_E_LDS
 
 
 def test_entry_points_reject_misaligned_pointers():
@@ -331,6 +332,21 @@ def test_python_wrappers_validate_on_the_host():
         kl.rmsnorm_matmul(a, a, eps=1e-6)
     with pytest.raises(ValueError, match="HIP device"):
         kl.matmul_lhs_rhs(a, a.t().contiguous())
+
+
+def test_c_abi_rejects_an_output_that_overlaps_an_input():
+    """The entry points compare pointer ranges on the host (fake pointers, nothing launched)."""
+    L = _lib.lib()
+    c = TileConfig(128, 128, 64, 4, 2).to_c()
+    base = 0x10000000
+    p = lambda off: ctypes.c_void_p(base + off)  # noqa: E731
+    M = N = K = 64  # 8 KiB per bf16 operand
+    assert L.mi_matmul_lhsT_rhs_bf16(p(0), p(1 << 20), p(4096), M, N, K, ctypes.byref(c), None) == _lib.MI_E_ARGS
+    assert L.mi_matmul_lhs_rhs_bf16(p(0), p(1 << 20), p((1 << 20) + 8192 - 16), M, N, K, ctypes.byref(c),
+                                    None) == _lib.MI_E_ARGS
+    assert L.mi_rmsnorm_matmul_bf16(p(0), p(1 << 19), p(1 << 20), p((1 << 19) + 64), M, N, K, 1e-6,
+                                    ctypes.byref(c), None) == _lib.MI_E_ARGS   # out over gamma
+    assert "overlaps" in _lib.last_error()
 
 
 def test_output_aliasing_an_input_is_rejected():
