@@ -100,7 +100,7 @@ def parse() -> argparse.Namespace:
                          "lhsT.rhs matmul at 4096^3; c4a/b/c: the C4 "
                          "lhsT.rhs shapes; c5: skinny lhsT.rhs (--m) x 28672 x 8192; decode: rmsnorm_matmul at the "
                          "c5 shape; panel-stream: the K-panel loads alone from L2, MALL and HBM; defaults: the "
-                         "library's default config against the autotune sweep's best at 71 shapes (all but c2: "
+                         "library's default config against the autotune sweep's best at 83 shapes (all but c2: "
                          "profiling workloads)")
     ap.add_argument("--settle-s", type=float, default=2.0,
                     help="GPU idle time before the timed region's warm-up (see settle())")
@@ -733,6 +733,9 @@ DEFAULTS_MM = [(1024, 1024, 1024), (2048, 2048, 2048), (3072, 3072, 3072), (4096
                (64, 14336, 4096), (2048, 2048, 8192), (1280, 5120, 5120), (4608, 4608, 2304), (640, 10240, 2048),
                (32, 2048, 16384), (3584, 1024, 4096), (1024, 3584, 14336), (200, 4096, 4096), (8192, 2048, 4096),
                (6144, 768, 6144)]
+DEFAULTS_SKINNY = [(128, 16384, 8192), (64, 12288, 16384), (32, 8192, 16384), (16, 28672, 8192), (128, 28672, 8192),
+                   (16, 8192, 8192), (32, 14336, 4096), (64, 4096, 4096), (128, 4096, 14336), (128, 8192, 4096),
+                   (64, 28672, 8192), (8, 11008, 4096)]
 DEFAULTS_LHS = [(1024, 1024, 1024), (2048, 2048, 2048), (3072, 3072, 3072), (4096, 4096, 4096), (8192, 1024, 8192),
                 (2048, 1024, 4096), (512, 4096, 4096), (1024, 8192, 16384), (96, 8192, 8192), (4096, 14336, 1024),
                 (16, 28672, 8192), (1536, 1536, 6144), (512, 512, 32768), (8192, 8192, 8192)]
@@ -748,8 +751,10 @@ def defaults_study(args, dev) -> int:
     For each shape: the library default (``mi_default_config``, not the
     tuned table) and the autotune sweep over every legal prebuilt config
     (10 reps each, numerics-gated, the 4 fastest re-timed), then the default
-    and the sweep's winner re-timed together in 5 interleaved rounds.  One
-    JSON row per shape on stderr, the whole table as one line on stdout."""
+    and the sweep's winner re-timed together in 5 interleaved rounds.  Skinny
+    shapes (M <= 128) overwrite a 512 MiB buffer before every launch, so the
+    weight streams from HBM as it does in decode.  One JSON row per shape on
+    stderr, the whole table as one line on stdout."""
     import ctypes
     import statistics
 
@@ -759,17 +764,21 @@ def defaults_study(args, dev) -> int:
     from kernel_library.config import kernel_id
 
     rows = []
-    for fam, shapes in (("matmul_lhsT_rhs", DEFAULTS_MM), ("matmul_lhs_rhs", DEFAULTS_LHS),
+    for fam, shapes in (("matmul_lhsT_rhs", DEFAULTS_MM + DEFAULTS_SKINNY), ("matmul_lhs_rhs", DEFAULTS_LHS),
                         ("rmsnorm_matmul", DEFAULTS_RMS)):
         for m, n, k in shapes:
             c = _lib.MiTileCfg()
             _lib.check_rc(_lib.lib().mi_default_config(kernel_id(fam), m, n, k, ctypes.byref(c)), "mi_default_config")
             dflt = kl.TileConfig.from_c(c)
-            res = tune(fam, m, n, k, check=True, warmup=3, reps=10, allow_jit=False, finalists=4, rounds=3)
+            # Skinny M (decode): the weight streams from HBM, as in the C5
+            # measurements (a 512 MiB buffer overwritten before every launch).
+            flush = 512 << 20 if m <= 128 else 0
+            res = tune(fam, m, n, k, check=True, warmup=3, reps=10, allow_jit=False, finalists=4, rounds=3,
+                       flush_bytes=flush)
             if res.best is None:
                 raise RuntimeError(f"no working config for {fam} {m}x{n}x{k}")
             cfgs = [dflt] if res.best.name == dflt.name else [dflt, res.best]
-            t = refine(fam, m, n, k, cfgs, rounds=5, reps=20)
+            t = refine(fam, m, n, k, cfgs, rounds=5, reps=20, flush_bytes=flush)
             row = {"kernel": fam, "shape": [m, n, k], "default": dflt.name, "default_us": round(t[dflt.name] * 1e6, 1),
                    "best": res.best.name, "best_us": round(t[res.best.name] * 1e6, 1),
                    "default_over_best": round(t[dflt.name] / t[res.best.name], 3),

@@ -307,12 +307,12 @@ mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K
 
 int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
   // Generalised from the autotune winners at the benchmark shapes and a
-  // study of 30 other shapes: the block whose rounds of tiles take the
+  // study of 70 other shapes: the block whose rounds of tiles take the
   // least time (a block that leaves CUs idle can still beat a smaller one
   // whose grid needs a second, partial round), with K split when the chosen
   // grid leaves CUs idle.  Skinny M (decode) streams the weight once with
-  // the non-temporal variants when their grid fills the chip, and takes
-  // 64 x 64 blocks when it does not.  For lhsT.rhs a 256-long block lies
+  // the non-temporal variants, in the block that gives the most tiles up to
+  // one per CU.  For lhsT.rhs a 256-long block lies
   // with its long side along the shorter output side (128 x 256 when M >=
   // N), a 128-long one along N unless N is at least four times M, as the
   // winners do; lhs.rhs keeps block_m the short side (fewer rows of its
@@ -333,12 +333,39 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
                         : M <= 64 ? mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt}
                                   : mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt};
     const mi_tile_cfg small = {64, 64, 64, 4, 4, 1, 8, v};
-    if (M <= 128 && tiles_of(M, N, skinny.block_m, skinny.block_n) >= kFillTiles) {
-      c = skinny;
-    } else if (M <= 128) {
-      c = small;
-      const long long tiles = tiles_of(M, N, 64, 64);
-      if (tiles < 64) c.split_k = fill_parts(tiles, K, 64);
+    if (M <= 128) {
+      // The weight is streamed once, non-temporally.  A grid of the skinny
+      // block that fills the chip runs unsplit.  Otherwise, with a long K
+      // (8192 or more), 256-wide column blocks (512-byte weight row segments
+      // per workgroup) split over K, when that fills three quarters of the
+      // CUs or more with at least 16 K steps per part; otherwise the block with the most tiles up to
+      // one per CU (ties to the larger), split only when that grid still
+      // leaves CUs idle.
+      mi_tile_cfg wide = lhs ? (M <= 32 ? mi_tile_cfg{32, 256, 64, 4, 4, 1, 8, v_nt}
+                                        : mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt})
+                             : (M <= 64 ? mi_tile_cfg{64, 256, 64, 4, 3, 1, 8, v_nt}
+                                        : mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v_nt});
+      const long long wide_tiles = tiles_of(M, N, wide.block_m, wide.block_n);
+      wide.split_k = fill_parts(wide_tiles, K, wide.block_k);
+      const bool wide_fills = wide_tiles * wide.split_k >= 3 * kCUs / 4 &&
+                              (long long)K / wide.split_k >= 16LL * wide.block_k;
+      if (tiles_of(M, N, skinny.block_m, skinny.block_n) >= kFillTiles) {
+        c = skinny;
+      } else if (K >= 8192 && wide_fills) {
+        c = wide;
+      } else {
+        const mi_tile_cfg skinny_cands[] = {skinny, mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt},
+                                            lhs ? small : mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v_nt}};
+        long long most = 0;
+        for (const mi_tile_cfg& ci : skinny_cands) {
+          const long long t = tiles_of(M, N, ci.block_m, ci.block_n), capped = t < kCUs ? t : kCUs;
+          if (capped > most) {
+            most = capped;
+            c = ci;
+          }
+        }
+        if (most < kFillTiles) c.split_k = fill_parts(most, K, c.block_k);
+      }
     } else {
       const Cand cands[] = {
           {lhs ? mi_tile_cfg{256, 256, 32, 8, 3, 1, 8, 1} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, v}, 1.0},

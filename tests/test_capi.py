@@ -215,7 +215,12 @@ def test_library_default_is_legal_everywhere():
     ("matmul_lhsT_rhs", (512, 4096, 4096), "bm128_bn64_bk64_w4_s4_v1"),       # N >= 4M: 128 along M
     ("matmul_lhsT_rhs", (512, 512, 32768), "bm128_bn128_bk64_w4_s3_v1_k16"),  # few tiles, long K: the largest block a split fills the chip with
     ("matmul_lhsT_rhs", (16, 28672, 8192), "bm32_bn128_bk128_w4_s3_v3"),      # skinny, weight streamed non-temporally
-    ("matmul_lhsT_rhs", (96, 8192, 8192), "bm64_bn64_bk64_w4_s4_v1"),         # skinny with too few 128-wide tiles
+    ("matmul_lhsT_rhs", (32, 14336, 4096), "bm64_bn64_bk64_w4_s4_v3"),        # skinny, short K: the most tiles
+    ("matmul_lhsT_rhs", (64, 4096, 4096), "bm64_bn64_bk64_w4_s4_v3_k4"),
+    ("matmul_lhsT_rhs", (16, 4096, 8192), "bm64_bn64_bk64_w4_s4_v3_k4"),     # long K, too few 256-wide K steps
+    ("matmul_lhsT_rhs", (32, 2048, 16384), "bm64_bn64_bk64_w4_s4_v3_k8"),    # long K, 256-wide grid too small
+    ("matmul_lhsT_rhs", (64, 12288, 16384), "bm64_bn256_bk64_w4_s3_v3_k4"),
+    ("matmul_lhsT_rhs", (96, 8192, 8192), "bm128_bn256_bk32_w4_s3_v3_k8"),   # skinny, long K: 256-wide blocks split over K
     ("rmsnorm_matmul", (4096, 4096, 4096), "bm128_bn512_bk32_w8_s3_v4"),
     ("rmsnorm_matmul", (4096, 2048, 4096), "bm128_bn256_bk32_w4_s3_v5"),
     ("rmsnorm_matmul", (512, 4096, 8192), "bm128_bn256_bk32_w4_s3_v5_k4"),
