@@ -294,7 +294,7 @@ mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K
     const long long rounds = (tiles * c.split_k + kCUs - 1) / kCUs;
     const double kp = (double)((K + c.split_k - 1) / c.split_k);
     double t = (double)rounds * c.block_m * c.block_n * kp / (cands[i].rate * R0) * 1e6;
-    if (c.split_k > 1) t += (double)c.split_k * M * N * 8.0 / kSplitBytesPerUs;
+    if (c.split_k > 1) t += (double)c.split_k * M * N * 8.0 / kSplitBytesPerUs + kLaunchUs;
     if (c.variant == 13) t += (double)M * K * 4.0 / kPackBytesPerUs + kLaunchUs;
     if (!found || t < best_t) {
       found = true;
@@ -314,8 +314,8 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
   // the non-temporal variants, in the block that gives the most tiles up to
   // one per CU.  For lhsT.rhs a 256-long block lies
   // with its long side along the shorter output side (128 x 256 when M >=
-  // N), a 128-long one along N unless N is at least four times M, as the
-  // winners do; lhs.rhs keeps block_m the short side (fewer rows of its
+  // N), or along N at any shape when K <= 2048, a 128-long one along N
+  // unless N is at least four times M, as the winners do; lhs.rhs keeps block_m the short side (fewer rows of its
   // K-contiguous operand per tile).
   mi_tile_cfg c = {256, 256, 64, 8, 2, 1, 8, 0};
   const bool m_long = M >= N, n_much_longer = (long long)N >= 4LL * M;
@@ -370,7 +370,8 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
       const Cand cands[] = {
           {lhs ? mi_tile_cfg{256, 256, 32, 8, 3, 1, 8, 1} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, v}, 1.0},
           {lhs ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 1}
-               : (m_long ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v} : mi_tile_cfg{256, 128, 32, 4, 3, 1, 8, v}),
+               : (m_long || K <= 2048 ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v}
+                                      : mi_tile_cfg{256, 128, 32, 4, 3, 1, 8, v}),
            0.93},
           {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v}, 0.62},
           {n_much_longer && !lhs ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v},
@@ -415,13 +416,13 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
       // 512.  The two-pass kernel scales x once, in a pass of its own, and
       // its main pass runs the lhsT core (256 x 256 at 1.10 of that rate).
       // Few-tile shapes split K, which the estimate charges for its fp32
-      // partial products.
+      // partial products and the launch of the summing kernel.
       const Cand cands[] = {{mi_tile_cfg{128, 512, 32, 8, 3, 1, 8, 4}, 1.0},
                             {mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 5}, 0.83},
                             {mi_tile_cfg{128, 128, 64, 4, 2, 1, 8, 4}, 0.54},
                             {mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, 13}, 1.10},
                             {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, 13}, 0.68},
-                            {mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, 13}, 0.66}};
+                            {mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, 13}, 0.57}};
       c = fastest_split_estimate(cands, 6, M, N, K);
     }
   }

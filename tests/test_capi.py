@@ -210,7 +210,8 @@ def test_library_default_is_legal_everywhere():
     ("matmul_lhsT_rhs", (8192, 8192, 8192), "bm256_bn256_bk32_w4_s3_v1"),
     ("matmul_lhsT_rhs", (8192, 1024, 8192), "bm128_bn256_bk32_w4_s3_v1"),     # 256x256 would give 128 tiles
     ("matmul_lhsT_rhs", (1024, 8192, 16384), "bm256_bn128_bk32_w4_s3_v1"),    # long side along the shorter output side
-    ("matmul_lhsT_rhs", (4096, 14336, 1024), "bm256_bn128_bk32_w4_s3_v1"),
+    ("matmul_lhsT_rhs", (4096, 14336, 1024), "bm128_bn256_bk32_w4_s3_v1"),    # K <= 2048: long side along N
+    ("matmul_lhsT_rhs", (640, 10240, 2048), "bm128_bn256_bk32_w4_s3_v1"),
     ("matmul_lhsT_rhs", (2048, 1024, 8192), "bm64_bn128_bk64_w4_s4_v1"),
     ("matmul_lhsT_rhs", (512, 4096, 4096), "bm128_bn64_bk64_w4_s4_v1"),       # N >= 4M: 128 along M
     ("matmul_lhsT_rhs", (512, 512, 32768), "bm128_bn128_bk64_w4_s3_v1_k16"),  # few tiles, long K: the largest block a split fills the chip with
@@ -224,6 +225,7 @@ def test_library_default_is_legal_everywhere():
     ("rmsnorm_matmul", (4096, 4096, 4096), "bm128_bn512_bk32_w8_s3_v4"),
     ("rmsnorm_matmul", (4096, 2048, 4096), "bm128_bn256_bk32_w4_s3_v5"),
     ("rmsnorm_matmul", (512, 4096, 8192), "bm128_bn256_bk32_w4_s3_v5_k4"),
+    ("rmsnorm_matmul", (1024, 4096, 4096), "bm128_bn128_bk64_w4_s3_v13"),     # one full round of two-pass tiles beats a split
     ("rmsnorm_matmul", (2048, 2048, 2048), "bm128_bn128_bk64_w4_s2_v4"),
     ("rmsnorm_matmul", (256, 8192, 4096), "bm64_bn128_bk64_w4_s4_v13"),       # x scaled once, then the lhsT core
     ("rmsnorm_matmul", (128, 4096, 4096), "bm64_bn128_bk64_w4_s3_v11_k4"),    # skinny, few tiles: 64-row blocks, split
