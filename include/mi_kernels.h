@@ -131,7 +131,8 @@ int mi_get_config(int kernel_id, int idx, mi_tile_cfg* cfg);
  * times the block's area over its measured rate per CU), split-K when that
  * grid leaves CUs idle, non-temporal variants for skinny M whose grid fills
  * the chip; for the fused kernel past the K its gamma staging holds, the
- * two-pass kernel when there are many output tiles and split-K otherwise. */
+ * two-pass kernel when there are many output tiles and split-K otherwise.
+ * A negative size is MI_E_ARGS. */
 int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
 
 /* out[M,N] = lhsT[K,M]^T . rhs[K,N]; bf16 storage, fp32 accumulation over

@@ -210,7 +210,9 @@ int zero_output(void* out, size_t n, void* stream) {
 constexpr long long kFillTiles = 224;
 constexpr long long kCUs = 256;
 
-long long tiles_of(int M, int N, int bm, int bn) { return (long long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); }
+long long tiles_of(int M, int N, int bm, int bn) {
+  return (((long long)M + bm - 1) / bm) * (((long long)N + bn - 1) / bn);
+}
 
 // The most parts (a power of two, at most 16) that keep the grid within one
 // workgroup per CU, every part at least 4 K tiles of block_k, and no part
@@ -578,6 +580,7 @@ int mi_get_config(int kernel_id, int idx, mi_tile_cfg* cfg) {
 int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
   if (kernel_id < 0 || kernel_id >= MI_NUM_KERNELS) return fail(MI_E_KERNEL, "unknown kernel id %d", kernel_id);
   if (!cfg) return fail(MI_E_ARGS, "null config");
+  if (M < 0 || N < 0 || K < 0) return fail(MI_E_ARGS, "negative size M=%d N=%d K=%d", M, N, K);
   return pick_default(kernel_id, M, N, K, cfg);
 }
 

@@ -241,6 +241,18 @@ def test_library_default_picks_the_measured_winners(fam, shape, name):
     assert TileConfig.from_c(c).name == name
 
 
+def test_library_default_rejects_negative_sizes_and_survives_huge_ones():
+    """A negative size is MI_E_ARGS; sizes near INT_MAX still give a config (no overflow in the tile counts)."""
+    L = _lib.lib()
+    c = _lib.MiTileCfg()
+    for kid in (MM, LHS, RMS):
+        assert L.mi_default_config(kid, -8, 8, 8, ctypes.byref(c)) == _lib.MI_E_ARGS
+        assert L.mi_default_config(kid, 8, 8, -1, ctypes.byref(c)) == _lib.MI_E_ARGS
+        for M, N in ((2 ** 31 - 8, 8), (8, 2 ** 31 - 8), (2 ** 31 - 8, 2 ** 31 - 8)):
+            assert L.mi_default_config(kid, M, N, 4096, ctypes.byref(c)) == _lib.MI_OK
+            assert c.block_m > 0 and c.block_n > 0 and 1 <= c.split_k <= 16
+
+
 def test_library_default_is_legal_at_large_shapes():
     """Very tall operands (x or lhsT of 1-2 GiB): the default never takes a config whose workspace or
     operand spans the call would reject."""
