@@ -2,8 +2,9 @@
 
 Such a call runs the library default (``mi_default_config``): a block chosen
 by its estimated rounds-of-tiles time, split-K when the grid leaves CUs
-idle, the paired-load lhs blocks, the two-pass fused kernel, 64-row skinny
-blocks.  Each case checks that the default is the config the estimate is
+idle, the paired-load lhs blocks, the two-pass fused kernel, and for skinny M
+the non-temporal blocks (256-wide and split over a long K, or the block with
+the most tiles).  Each case checks that the default is the config the estimate is
 meant to pick (so the case exercises that path), then the whole output
 against a float64 product of the same bf16 inputs on the GPU and sampled
 rows against the CPU oracle.
@@ -42,6 +43,9 @@ def _rows(M: int) -> np.ndarray:
     ("matmul_lhsT_rhs", (512, 512, 32768), "bm128_bn128_bk64_w4_s3_v1_k16"),
     ("matmul_lhsT_rhs", (96, 8192, 8192), "bm128_bn256_bk32_w4_s3_v3_k8"),
     ("matmul_lhsT_rhs", (3072, 3072, 3072), "bm256_bn256_bk32_w4_s3_v1"),
+    ("matmul_lhsT_rhs", (16, 8192, 8192), "bm64_bn256_bk64_w4_s3_v3_k8"),
+    ("matmul_lhsT_rhs", (32, 2048, 16384), "bm64_bn64_bk64_w4_s4_v3_k8"),
+    ("matmul_lhsT_rhs", (640, 10240, 2048), "bm128_bn256_bk32_w4_s3_v1"),
     ("matmul_lhs_rhs", (2048, 4096, 1024), "bm128_bn256_bk32_w4_s3_v1"),
     ("matmul_lhs_rhs", (512, 4096, 4096), "bm64_bn128_bk64_w4_s4"),
 ])
@@ -73,6 +77,7 @@ def test_matmul_without_config(gpu, fam, shape, expect):
     ((256, 8192, 4096), "bm64_bn128_bk64_w4_s4_v13"),
     ((128, 4096, 4096), "bm64_bn128_bk64_w4_s3_v11_k4"),
     ((512, 4096, 8192), "bm128_bn256_bk32_w4_s3_v5_k4"),
+    ((1024, 4096, 4096), "bm128_bn128_bk64_w4_s3_v13"),
     ((640, 2048, 1024), None),
 ])
 def test_rmsnorm_matmul_without_config(gpu, shape, expect):
