@@ -230,7 +230,9 @@ def main(argv: list[str] | None = None) -> int:
                     choices=["matmul_lhsT_rhs", "matmul_lhsT_rhs_f32", "rmsnorm_matmul", "matmul_lhs_rhs",
                              "matmul_lhsT_rhs_nkigym", "rmsnorm_matmul_online", "matmul_lhs_rhs_nkigym"])
     ap.add_argument("--shape", nargs=3, type=int, metavar=("M", "N", "K"), default=[8192, 8192, 8192])
-    ap.add_argument("--cache", default="", help="cache dir for sources / results.json (empty: none)")
+    ap.add_argument("--cache", default="",
+                    help="cache dir for sources / results.json, cleared first (empty: none; a non-empty directory "
+                         "without results.json is refused)")
     ap.add_argument("--grid", choices=["compiled", "baseline", "frontier"], default="compiled",
                     help="compiled: every prebuilt config; baseline: the 72-point search grid (JIT-built if needed); "
                          "frontier: --num-kernels configs sampled by frontier expansion from the default config")
@@ -266,6 +268,13 @@ def main(argv: list[str] | None = None) -> int:
     if args.detailed and not args.cache:
         ap.error("--detailed needs --cache (the traces are kept in the config folders)")
     if args.cache:
+        # The cache is cleared before the sweep; a directory that holds other
+        # files and no results.json is not a previous tune's cache, and is
+        # left alone.
+        if os.path.isdir(args.cache) and os.listdir(args.cache) and \
+                not os.path.isfile(os.path.join(args.cache, "results.json")):
+            ap.error(f"--cache {args.cache}: a non-empty directory without results.json (not a tune cache); "
+                     "refusing to clear it")
         shutil.rmtree(args.cache, ignore_errors=True)
         os.makedirs(args.cache, exist_ok=True)
     # rmsnorm_matmul_online is the reference's contract: no gamma.

@@ -339,6 +339,28 @@ def test_tune_cli_named_configs_and_detailed_needs_cache(monkeypatch):
     assert seen["with_gamma"] is True
 
 
+def test_tune_cli_clears_only_a_tune_cache(monkeypatch, tmp_path):
+    """--cache is cleared before the sweep, but a non-empty directory without results.json is refused untouched."""
+    from autotune import tune as tmod
+
+    monkeypatch.setattr(tmod, "tune", lambda *a, **kw: tmod.TuneResult(None, None, "", None))
+    other = tmp_path / "home"
+    other.mkdir()
+    (other / "notes.txt").write_text("keep me")
+    with pytest.raises(SystemExit):
+        tmod.main(["--configs", "bm64_bn64_bk64_w4_s4_v1", "--cache", str(other)])
+    assert (other / "notes.txt").read_text() == "keep me"
+    old = tmp_path / "cache"
+    old.mkdir()
+    (old / "results.json").write_text("{}")
+    (old / "stale.hip").write_text("")
+    tmod.main(["--configs", "bm64_bn64_bk64_w4_s4_v1", "--cache", str(old)])
+    assert old.is_dir() and not any(old.iterdir())
+    fresh = tmp_path / "new" / "cache"
+    tmod.main(["--configs", "bm64_bn64_bk64_w4_s4_v1", "--cache", str(fresh)])
+    assert fresh.is_dir()
+
+
 def test_baseline_row_numerics_failures_and_counters(tmp_path):
     """The results model renders the vendor baseline row and the measured
     counters in the table and results.json, and a numerics failure is a
