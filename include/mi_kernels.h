@@ -172,7 +172,8 @@ int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void
  * the workspace of a split-K config (split_k * M * N * 4 bytes of fp32
  * partial products) is a static device array of MI_NOALLOC_SCRATCH_BYTES
  * that each GPU holds from the first call there until the process ends, and
- * a config needing more returns MI_E_RANGE.  Calls on one GPU share that
+ * a config needing more returns MI_E_RANGE (cfg == NULL never does: the
+ * default splits at most 256 blocks of 256 x 256).  Calls on one GPU share that
  * array: calls ordered on one stream are safe, calls that overlap on one GPU
  * race. */
 #define MI_NOALLOC_SCRATCH_BYTES (64ull * 1024ull * 1024ull)

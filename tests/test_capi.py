@@ -282,6 +282,18 @@ def test_library_default_is_legal_for_random_shapes(kid, m, n, k, big):
                                                                           _lib.last_error())
 
 
+@settings(max_examples=300, deadline=None)
+@given(m=st.integers(1, 4096), n=st.integers(1, 4096), k=st.integers(1, 65536))
+def test_library_default_split_fits_the_noalloc_scratch(m, n, k):
+    """With no config, the no-allocation entry point never meets MI_E_RANGE: the default splits only
+    grids of at most one workgroup per CU, so its fp32 partials stay within 256 blocks of 256 x 256."""
+    M, N, K = 8 * m, 8 * n, k
+    c = _lib.MiTileCfg()
+    assert _lib.lib().mi_default_config(MM, M, N, K, ctypes.byref(c)) == _lib.MI_OK
+    ws = c.split_k * M * N * 4 if c.split_k > 1 else 0
+    assert ws <= 64 << 20, (M, N, K, TileConfig.from_c(c).name, ws)
+
+
 def test_entry_points_reject_bad_arguments_before_any_gpu_call():
     """Negative sizes, null pointers and a non-finite eps are refused on the host; empty outputs are no-ops."""
     L = _lib.lib()
