@@ -95,13 +95,14 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--sweep-reps", type=int, default=20)
     ap.add_argument("--config", default="", help="tile config name (e.g. bm256_bn256_bk32_w4_s3_v1) instead of the sweep")
     ap.add_argument("--workload", choices=["c2", "c2-clock", "c3", "c3-matmul", "c4a", "c4b", "c4c", "c5", "decode",
-                                           "panel-stream", "defaults"], default="c2",
+                                           "panel-stream", "defaults", "defaults-random"], default="c2",
                     help="c2: lhsT.rhs matmul 8192^3 (the metric); c3: rmsnorm_matmul 4096^3; c3-matmul: the plain "
                          "lhsT.rhs matmul at 4096^3; c4a/b/c: the C4 "
                          "lhsT.rhs shapes; c5: skinny lhsT.rhs (--m) x 28672 x 8192; decode: rmsnorm_matmul at the "
                          "c5 shape; panel-stream: the K-panel loads alone from L2, MALL and HBM; defaults: the "
-                         "library's default config against the autotune sweep's best at 83 shapes (all but c2: "
-                         "profiling workloads)")
+                         "library's default config against the autotune sweep's best at 83 shapes; "
+                         "defaults-random: the same at 30 seeded random shapes the default was not fitted to (all "
+                         "but c2: profiling workloads)")
     ap.add_argument("--settle-s", type=float, default=2.0,
                     help="GPU idle time before the timed region's warm-up (see settle())")
     ap.add_argument("--m", type=int, default=16, choices=[16, 64, 128], help="M of the c5 / decode workloads")
@@ -501,7 +502,11 @@ def main() -> int:
     if args.workload == "panel-stream":
         return panel_stream_study(args, dev)
     if args.workload == "defaults":
-        return defaults_study(args, dev)
+        return defaults_study(args, dev, [(f, sh) for f, shapes in (
+            ("matmul_lhsT_rhs", DEFAULTS_MM + DEFAULTS_SKINNY), ("matmul_lhs_rhs", DEFAULTS_LHS),
+            ("rmsnorm_matmul", DEFAULTS_RMS)) for sh in shapes], "defaults")
+    if args.workload == "defaults-random":
+        return defaults_study(args, dev, random_default_shapes(), "defaults-random")
     if args.workload in PLAIN_SHAPES:
         return shape_main(args, dev, *PLAIN_SHAPES[args.workload])
     fam, s = ("matmul_lhsT_rhs", M) if args.workload == "c2" else ("rmsnorm_matmul", 4096)
@@ -745,10 +750,31 @@ DEFAULTS_RMS = [(4096, 4096, 4096), (2048, 8192, 2048), (8192, 4096, 4096), (102
                 (2560, 4096, 2048), (384, 8192, 8192), (1024, 8192, 1024)]
 
 
-def defaults_study(args, dev) -> int:
-    """--workload defaults: how close does a call without a config come to the autotuned best?
+def random_default_shapes(seed: int = 2026, count: int = 30) -> list:
+    """Shapes the default config was not fitted to: 14 lhsT.rhs, 6 lhs.rhs and 10 rmsnorm_matmul shapes,
+    drawn from a fixed seed.  A quarter are skinny (M from 8 to 128); the others have M of 256 to 8192, N of
+    512 to 14336 and K of 512 to 16384, in steps of 64, at most 5e11 FLOP each (so the sweep stays short)."""
+    import numpy as np
 
-    For each shape: the library default (``mi_default_config``, not the
+    rng = np.random.default_rng(seed)
+    fams = ["matmul_lhsT_rhs"] * 14 + ["matmul_lhs_rhs"] * 6 + ["rmsnorm_matmul"] * 10
+    out = []
+    for fam in fams[:count]:
+        while True:
+            skinny = rng.random() < 0.25
+            m = int(rng.choice([8, 16, 32, 48, 64, 96, 128])) if skinny else int(rng.integers(4, 129)) * 64
+            n = int(rng.integers(8, 225)) * 64
+            k = int(rng.integers(8, 257)) * 64
+            if 2.0 * m * n * k <= 5e11:
+                break
+        out.append((fam, (m, n, k)))
+    return out
+
+
+def defaults_study(args, dev, jobs: list, name: str) -> int:
+    """--workload defaults / defaults-random: how close does a call without a config come to the autotuned best?
+
+    For each (kernel, shape) of ``jobs``: the library default (``mi_default_config``, not the
     tuned table) and the autotune sweep over every legal prebuilt config
     (10 reps each, numerics-gated, the 4 fastest re-timed), then the default
     and the sweep's winner re-timed together in 5 interleaved rounds.  Skinny
@@ -764,29 +790,27 @@ def defaults_study(args, dev) -> int:
     from kernel_library.config import kernel_id
 
     rows = []
-    for fam, shapes in (("matmul_lhsT_rhs", DEFAULTS_MM + DEFAULTS_SKINNY), ("matmul_lhs_rhs", DEFAULTS_LHS),
-                        ("rmsnorm_matmul", DEFAULTS_RMS)):
-        for m, n, k in shapes:
-            c = _lib.MiTileCfg()
-            _lib.check_rc(_lib.lib().mi_default_config(kernel_id(fam), m, n, k, ctypes.byref(c)), "mi_default_config")
-            dflt = kl.TileConfig.from_c(c)
-            # Skinny M (decode): the weight streams from HBM, as in the C5
-            # measurements (a 512 MiB buffer overwritten before every launch).
-            flush = 512 << 20 if m <= 128 else 0
-            res = tune(fam, m, n, k, check=True, warmup=3, reps=10, allow_jit=False, finalists=4, rounds=3,
-                       flush_bytes=flush)
-            if res.best is None:
-                raise RuntimeError(f"no working config for {fam} {m}x{n}x{k}")
-            cfgs = [dflt] if res.best.name == dflt.name else [dflt, res.best]
-            t = refine(fam, m, n, k, cfgs, rounds=5, reps=20, flush_bytes=flush)
-            row = {"kernel": fam, "shape": [m, n, k], "default": dflt.name, "default_us": round(t[dflt.name] * 1e6, 1),
-                   "best": res.best.name, "best_us": round(t[res.best.name] * 1e6, 1),
-                   "default_over_best": round(t[dflt.name] / t[res.best.name], 3),
-                   "best_tflops": round(2.0 * m * n * k / t[res.best.name] / 1e12, 1)}
-            log(json.dumps(row))
-            rows.append(row)
+    for fam, (m, n, k) in jobs:
+        c = _lib.MiTileCfg()
+        _lib.check_rc(_lib.lib().mi_default_config(kernel_id(fam), m, n, k, ctypes.byref(c)), "mi_default_config")
+        dflt = kl.TileConfig.from_c(c)
+        # Skinny M (decode): the weight streams from HBM, as in the C5
+        # measurements (a 512 MiB buffer overwritten before every launch).
+        flush = 512 << 20 if m <= 128 else 0
+        res = tune(fam, m, n, k, check=True, warmup=3, reps=10, allow_jit=False, finalists=4, rounds=3,
+                   flush_bytes=flush)
+        if res.best is None:
+            raise RuntimeError(f"no working config for {fam} {m}x{n}x{k}")
+        cfgs = [dflt] if res.best.name == dflt.name else [dflt, res.best]
+        t = refine(fam, m, n, k, cfgs, rounds=5, reps=20, flush_bytes=flush)
+        row = {"kernel": fam, "shape": [m, n, k], "default": dflt.name, "default_us": round(t[dflt.name] * 1e6, 1),
+               "best": res.best.name, "best_us": round(t[res.best.name] * 1e6, 1),
+               "default_over_best": round(t[dflt.name] / t[res.best.name], 3),
+               "best_tflops": round(2.0 * m * n * k / t[res.best.name] / 1e12, 1)}
+        log(json.dumps(row))
+        rows.append(row)
     ratios = [r["default_over_best"] for r in rows]
-    print(json.dumps({"workload": "defaults", "shapes": len(rows), "median_default_over_best": statistics.median(ratios),
+    print(json.dumps({"workload": name, "shapes": len(rows), "median_default_over_best": statistics.median(ratios),
                       "max_default_over_best": max(ratios), "rows": rows}), flush=True)
     return 0
 

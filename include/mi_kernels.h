@@ -186,6 +186,18 @@ int mi_matmul_lhsT_rhs_bf16_noalloc(const void* lhsT, const void* rhs, void* out
  * (reference autotune/src/autotune/runner/detect.py:7-20). */
 int mi_device_info(int* num_devices, char* arch, int arch_len, int* num_cus);
 
+/* Returns the device memory the library holds for split-K and two-pass
+ * workspace freed by earlier calls to the device, on every device the
+ * library has used; synchronises the null stream of each.  Memory behind a
+ * call whose launches have not finished is kept.  Without it, the runtime
+ * hands a call's freed workspace back to the library's pool only at the
+ * pool's next allocation (the next call that needs workspace), which then
+ * keeps at most 256 MiB cached: between calls the library holds up to the
+ * last such call's workspace plus 256 MiB.  Not under graph capture.  No
+ * counterpart in the reference (its kernels allocate nothing beyond their
+ * output).  Returns 0 or -error. */
+int mi_release_workspace(void);
+
 /* Message of the last failure on the calling thread ("" if none). */
 const char* mi_last_error(void);
 

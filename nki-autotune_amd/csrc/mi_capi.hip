@@ -282,20 +282,47 @@ mi_tile_cfg fastest_estimate(const Cand* cands, int n, int M, int N, int K, int 
 // read, x * gamma written: 4 bytes per x element at about 5 TB/s) and 3 us
 // for the second launch.  R0 is the fused kernel's 128 x 512 rate per CU at
 // 4096^3, in multiply-adds per second.
-mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K) {
+// The fewest parts, from c.split_k up by powers of two, that leave every K
+// part within the gamma entries the fused instance stages in LDS and no part
+// empty; 0 when none up to kMaxSplit does (or the instance is not built).
+int gamma_fit_parts(const mi_tile_cfg& c, int K) {
+  const mi::MiEntry* e = find(MI_KERNEL_RMSNORM_MATMUL_BF16, c);
+  if (!e) return 0;
+  const long long kt = ((long long)K + c.block_k - 1) / c.block_k;
+  for (int p = c.split_k; p <= kMaxSplit; p *= 2) {
+    const long long kts = (kt + p - 1) / p;
+    if (p > 1 && (long long)(p - 1) * kts >= kt) return 0;
+    if (e->gamma_kmax <= 0 || kts * c.block_k <= e->gamma_kmax) return p;
+  }
+  return 0;
+}
+
+mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K, const mi_tile_cfg& fallback) {
   constexpr double R0 = 2.28e12, kSplitBytesPerUs = 5e6, kPackBytesPerUs = 5e6, kLaunchUs = 3.0;
   double best_t = 0.0;
-  mi_tile_cfg best_c = cands[0].c;
+  mi_tile_cfg best_c = fallback;
   bool found = false;
   for (int i = 0; i < n; ++i) {
     mi_tile_cfg c = cands[i].c;
     const long long tiles = tiles_of(M, N, c.block_m, c.block_n);
     c.split_k = tiles < kFillTiles ? fill_parts(tiles, K, c.block_k) : 1;
-    // A candidate whose workspace the call could not allocate is out.
+    // Past the gamma entries an instance stages, K splits further; a
+    // candidate no split makes legal, or whose workspace the call could not
+    // allocate, is out.
+    c.split_k = gamma_fit_parts(c, K);
+    if (c.split_k == 0) continue;
     if (mi::workspace_bytes(MI_KERNEL_RMSNORM_MATMUL_BF16, c, M, N, K) > kMaxWorkspace) continue;
-    const long long rounds = (tiles * c.split_k + kCUs - 1) / kCUs;
+    const long long wgs = tiles * c.split_k, rounds = (wgs + kCUs - 1) / kCUs;
     const double kp = (double)((K + c.split_k - 1) / c.split_k);
     double t = (double)rounds * c.block_m * c.block_n * kp / (cands[i].rate * R0) * 1e6;
+    // The chip is power-limited under this load, so a single round that
+    // leaves CUs idle runs each busy CU faster (its clock rises): by up to
+    // 0.88 / (the busy fraction), at most 1.65 times (fitted to the fused
+    // candidates timed at 23 shapes).
+    if (rounds == 1) {
+      const double busy = (double)wgs / kCUs, speed = 0.88 / busy;
+      t /= speed > 1.65 ? 1.65 : speed < 1.0 ? 1.0 : speed;
+    }
     if (c.split_k > 1) t += (double)c.split_k * M * N * 8.0 / kSplitBytesPerUs + kLaunchUs;
     if (c.variant == 13) t += (double)M * K * 4.0 / kPackBytesPerUs + kLaunchUs;
     if (!found || t < best_t) {
@@ -335,18 +362,25 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
                         : M <= 64 ? mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt}
                                   : mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt};
     const mi_tile_cfg small = {64, 64, 64, 4, 4, 1, 8, v};
-    if (M <= 128) {
+    if (M <= 128 && lhs) {
+      // lhs.rhs: the non-temporal 128 x 128 block when its grid fills the
+      // chip; otherwise the non-temporal block with the fewest wasted rows
+      // (64 x 128 up to M = 64), split over K to up to one workgroup per CU.
+      if (tiles_of(M, N, skinny.block_m, skinny.block_n) >= kFillTiles) {
+        c = skinny;
+      } else {
+        c = M <= 64 ? mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt} : skinny;
+        c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
+      }
+    } else if (M <= 128) {
       // The weight is streamed once, non-temporally.  A grid of the skinny
       // block that fills the chip runs unsplit.  Otherwise, with a long K
       // (8192 or more), 256-wide column blocks (512-byte weight row segments
       // per workgroup) split over K, when that fills three quarters of the
-      // CUs or more with at least 16 K steps per part; otherwise the block with the most tiles up to
-      // one per CU (ties to the larger), split only when that grid still
-      // leaves CUs idle.
-      mi_tile_cfg wide = lhs ? (M <= 32 ? mi_tile_cfg{32, 256, 64, 4, 4, 1, 8, v_nt}
-                                        : mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt})
-                             : (M <= 64 ? mi_tile_cfg{64, 256, 64, 4, 3, 1, 8, v_nt}
-                                        : mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v_nt});
+      // CUs or more with at least 16 K steps per part; otherwise the block
+      // with the most tiles up to one per CU (ties to the larger), split only
+      // when that grid still leaves CUs idle.
+      mi_tile_cfg wide = M <= 64 ? mi_tile_cfg{64, 256, 64, 4, 3, 1, 8, v_nt} : mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v_nt};
       const long long wide_tiles = tiles_of(M, N, wide.block_m, wide.block_n);
       wide.split_k = fill_parts(wide_tiles, K, wide.block_k);
       const bool wide_fills = wide_tiles * wide.split_k >= 3 * kCUs / 4 &&
@@ -357,7 +391,7 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
         c = wide;
       } else {
         const mi_tile_cfg skinny_cands[] = {skinny, mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt},
-                                            lhs ? small : mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v_nt}};
+                                            mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v_nt}};
         long long most = 0;
         for (const mi_tile_cfg& ci : skinny_cands) {
           const long long t = tiles_of(M, N, ci.block_m, ci.block_n), capped = t < kCUs ? t : kCUs;
@@ -383,18 +417,10 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
     }
   } else if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16) {
     // The register-staged kernels keep gamma in LDS (8192 entries here).
-    // Past K = 8192, shapes with many output tiles take the two-pass kernel
-    // (variant 13: its main pass is the lhsT core, with no gamma limit and
-    // no split); the others split K into the fewest parts whose gamma fits
+    // Skinny M past K = 8192 splits K into the fewest parts whose gamma fits
     // (1..16 parts, none empty); past that the LDS-staged kernel (variant 0)
     // takes any K.
-    const bool mid = (long long)M * N <= 2048LL * 2048LL;
-    const long long t128 = tiles_of(M, N, 128, 128);
-    const mi_tile_cfg two_pass = mid ? mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, 13} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, 13};
-    if (K > 8192 && M > 128 && t128 >= 256 &&
-        mi::workspace_bytes(MI_KERNEL_RMSNORM_MATMUL_BF16, two_pass, M, N, K) <= kMaxWorkspace) {
-      c = two_pass;
-    } else if (K > 8192) {
+    if (M <= 128 && K > 8192) {
       const long long kt = (K + 63) / 64;
       int parts = 0;
       for (int p = 2; p <= 16 && !parts; p *= 2) {
@@ -402,30 +428,40 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
         const unsigned long long ws = (unsigned long long)p * ((unsigned long long)M * N + M) * 4ull;
         if (kts * 64 <= 8192 && (long long)(p - 1) * kts < kt && ws <= kMaxWorkspace) parts = p;
       }
-      if (!parts) c = M <= 128 ? mi_tile_cfg{64, 128, 64, 4, 2, 1, 8, 0} : mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0};
-      else if (M <= 128) c = {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, parts, 8, 11};
-      else c = {128, 128, 64, 4, 2, parts, 8, 4};
+      if (!parts) c = {64, 128, 64, 4, 2, 1, 8, 0};
+      else c = {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, parts, 8, 11};
     } else if (M <= 128) {
-      // Weight streamed once (variant 11); a grid short of the CUs takes
-      // 64-row blocks before splitting K.
-      c = {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, 1, 8, 11};
+      // Weight streamed once (variant 11).  With a weight of 16 MiB or less
+      // (re-read from the caches), 32-row blocks (more tiles) win at any M
+      // (measured up to 16 MiB; at 32 MiB the 64-row block won); a larger
+      // one takes the block that covers M,
+      // with 64-row blocks before a split when 128-row ones leave CUs idle.
+      // Below K = 4096 the summing launch of a split costs more than the
+      // idle CUs do.
+      const bool cached_w = (long long)K * N * 2 <= (16LL << 20);
+      c = {cached_w || M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, 1, 8, 11};
       if (c.block_m == 128 && tiles_of(M, N, 128, 128) < kFillTiles) c.block_m = 64;
-      c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
+      if (K >= 4096) c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
     } else {
       // Each workgroup of the one-pass kernels scales its x rows once per
       // column tile, so narrow blocks pay that work many times over: per CU,
       // 128 x 256 runs at 0.83 and 128 x 128 at 0.54 of the rate of 128 x
       // 512.  The two-pass kernel scales x once, in a pass of its own, and
-      // its main pass runs the lhsT core (256 x 256 at 1.10 of that rate).
-      // Few-tile shapes split K, which the estimate charges for its fp32
-      // partial products and the launch of the summing kernel.
+      // its main pass runs the lhsT core (256 x 256 at 1.10 of that rate;
+      // past K = 8192 also 256 x 128, its long side along the shorter output
+      // side, at 0.95).  Few-tile shapes split K, which the estimate charges
+      // for its fp32 partial products and the launch of the summing kernel;
+      // past K = 8192 the one-pass kernels split at least until each part's
+      // gamma fits.
       const Cand cands[] = {{mi_tile_cfg{128, 512, 32, 8, 3, 1, 8, 4}, 1.0},
                             {mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 5}, 0.83},
                             {mi_tile_cfg{128, 128, 64, 4, 2, 1, 8, 4}, 0.54},
                             {mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, 13}, 1.10},
                             {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, 13}, 0.68},
-                            {mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, 13}, 0.57}};
-      c = fastest_split_estimate(cands, 6, M, N, K);
+                            {mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, 13}, 0.57},
+                            {M <= N ? mi_tile_cfg{256, 128, 64, 4, 3, 1, 8, 13}
+                                    : mi_tile_cfg{128, 256, 64, 4, 3, 1, 8, 13}, 0.95}};
+      c = fastest_split_estimate(cands, K > 8192 ? 7 : 6, M, N, K, mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0});
     }
   }
   *cfg = c;
@@ -435,9 +471,12 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
 // Device workspace (split-K partial products, the two-pass fused kernel's
 // packed operand): allocated per call, stream-ordered (hipMallocFromPoolAsync
 // / hipFreeAsync), from a memory pool the library keeps per device.  The
-// pool keeps at most kPoolKeepBytes of freed memory cached for the next
-// calls and returns the rest to the device at a synchronisation (stream,
-// event or device) that begins after the freeing launch has finished.
+// runtime hands a call's freed workspace back to the pool at the pool's
+// next allocation (measured: not at a synchronisation), and the pool's
+// release threshold, kPoolKeepBytes, then returns what it holds beyond that
+// to the device.  So between calls the library holds up to the last
+// workspace call's buffer plus kPoolKeepBytes; mi_release_workspace returns
+// all of it.
 // Each call has its own buffer (calls on different streams do not share
 // one), and a call under HIP graph capture becomes allocation and free
 // nodes of the graph.
@@ -657,6 +696,29 @@ int mi_device_info(int* num_devices, char* arch, int arch_len, int* num_cus) {
     if (num_cus) *num_cus = p.multiProcessorCount;
   }
   return MI_OK;
+}
+
+int mi_release_workspace(void) {
+  std::lock_guard<std::mutex> lock(g_pool_mu);
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  int rc = MI_OK;
+  for (const auto& kv : g_pools) {
+    // The runtime hands memory freed by hipFreeAsync back to its pool at the
+    // pool's next allocation, not at a synchronisation: one small
+    // allocation and free, completed, makes the earlier frees trimmable.
+    void* p = nullptr;
+    if ((e = hipSetDevice(kv.first)) != hipSuccess || (e = hipMallocFromPoolAsync(&p, 256, kv.second, nullptr)) != hipSuccess ||
+        (e = hipFreeAsync(p, nullptr)) != hipSuccess || (e = hipStreamSynchronize(nullptr)) != hipSuccess ||
+        (e = hipMemPoolTrimTo(kv.second, 0)) != hipSuccess) {
+      rc = hip_fail(e, "releasing the workspace pool");
+      break;
+    }
+  }
+  e = hipSetDevice(cur);
+  if (rc == MI_OK && e != hipSuccess) rc = hip_fail(e, "hipSetDevice");
+  return rc;
 }
 
 const char* mi_last_error(void) { return g_err; }

@@ -7,7 +7,8 @@ Public kernels (torch device tensors in, torch device tensor out):
 * :func:`rmsnorm_matmul` -- ``rmsnorm(lhs) * gamma @ rhs``, bf16
 
 plus the reference names ``matmul_lhsT_rhs_nkigym``, ``matmul_lhs_rhs_nkigym`` and
-``rmsnorm_matmul_online``, and the tile search space (:class:`TileConfig`).
+``rmsnorm_matmul_online``, the tile search space (:class:`TileConfig`), and
+:func:`release_workspace` (returns the cached split-K workspace memory).
 """
 
 from kernel_library.config import (
@@ -24,6 +25,7 @@ from kernel_library.ops import (
     matmul_lhs_rhs_nkigym,
     matmul_lhsT_rhs,
     matmul_lhsT_rhs_nkigym,
+    release_workspace,
     rmsnorm_matmul,
     rmsnorm_matmul_online,
 )
@@ -40,6 +42,7 @@ __all__ = [
     "matmul_lhs_rhs_nkigym",
     "matmul_lhsT_rhs",
     "matmul_lhsT_rhs_nkigym",
+    "release_workspace",
     "rmsnorm_matmul",
     "rmsnorm_matmul_online",
 ]

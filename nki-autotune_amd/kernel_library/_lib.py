@@ -56,6 +56,7 @@ EXPORTED_SYMBOLS = (
     "mi_matmul_lhsT_rhs_f32",
     "mi_rmsnorm_matmul_bf16",
     "mi_device_info",
+    "mi_release_workspace",
     "mi_last_error",
     "mi_version",
 )
@@ -116,6 +117,7 @@ def _declare(lib: ctypes.CDLL) -> None:
             [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_float, cfgp, c_void_p],
         ),
         "mi_device_info": (c_int, [ctypes.POINTER(c_int), c_char_p, c_int, ctypes.POINTER(c_int)]),
+        "mi_release_workspace": (c_int, []),
         "mi_last_error": (c_char_p, []),
         "mi_version": (c_char_p, []),
     }

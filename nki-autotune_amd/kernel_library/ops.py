@@ -172,6 +172,13 @@ def rmsnorm_matmul(
     return out
 
 
+def release_workspace() -> None:
+    """Return the device memory cached for split-K and two-pass workspace (``mi_release_workspace``).
+
+    Memory behind a call still running is kept; after ``torch.cuda.synchronize()`` everything goes."""
+    _lib.check_rc(_lib.lib().mi_release_workspace(), "release_workspace")
+
+
 # Reference names (drop-in aliases).
 matmul_lhsT_rhs_nkigym = matmul_lhsT_rhs
 matmul_lhs_rhs_nkigym = matmul_lhs_rhs

@@ -226,6 +226,11 @@ def test_library_default_is_legal_everywhere():
     ("rmsnorm_matmul", (4096, 2048, 4096), "bm128_bn256_bk32_w4_s3_v5"),
     ("rmsnorm_matmul", (512, 4096, 8192), "bm128_bn256_bk32_w4_s3_v5_k4"),
     ("rmsnorm_matmul", (1024, 4096, 4096), "bm128_bn128_bk64_w4_s3_v13"),     # one full round of two-pass tiles beats a split
+    ("rmsnorm_matmul", (48, 5504, 704), "bm32_bn128_bk64_w4_s3_v11"),         # cached weight, short K: 32-row, unsplit
+    ("rmsnorm_matmul", (128, 1024, 5248), "bm32_bn128_bk64_w4_s3_v11_k8"),
+    ("rmsnorm_matmul", (768, 8064, 12992), "bm256_bn128_bk64_w4_s3_v13"),     # K > 8192: the estimate, 256 x 128 two-pass
+    ("rmsnorm_matmul", (384, 4096, 16384), "bm128_bn512_bk32_w8_s3_v4_k8"),   # K > 8192: one-pass split until gamma fits
+    ("matmul_lhs_rhs", (48, 2880, 14912), "bm64_bn128_bk64_w4_s4_v2_k8"),     # skinny lhs: non-temporal 64 x 128, split
     ("rmsnorm_matmul", (2048, 2048, 2048), "bm128_bn128_bk64_w4_s2_v4"),
     ("rmsnorm_matmul", (256, 8192, 4096), "bm64_bn128_bk64_w4_s4_v13"),       # x scaled once, then the lhsT core
     ("rmsnorm_matmul", (128, 4096, 4096), "bm64_bn128_bk64_w4_s3_v11_k4"),    # skinny, few tiles: 64-row blocks, split

@@ -48,6 +48,7 @@ def _rows(M: int) -> np.ndarray:
     ("matmul_lhsT_rhs", (640, 10240, 2048), "bm128_bn256_bk32_w4_s3_v1"),
     ("matmul_lhs_rhs", (2048, 4096, 1024), "bm128_bn256_bk32_w4_s3_v1"),
     ("matmul_lhs_rhs", (512, 4096, 4096), "bm64_bn128_bk64_w4_s4"),
+    ("matmul_lhs_rhs", (48, 2880, 14912), "bm64_bn128_bk64_w4_s4_v2_k8"),
 ])
 def test_matmul_without_config(gpu, fam, shape, expect):
     import torch
@@ -78,6 +79,9 @@ def test_matmul_without_config(gpu, fam, shape, expect):
     ((128, 4096, 4096), "bm64_bn128_bk64_w4_s3_v11_k4"),
     ((512, 4096, 8192), "bm128_bn256_bk32_w4_s3_v5_k4"),
     ((1024, 4096, 4096), "bm128_bn128_bk64_w4_s3_v13"),
+    ((48, 5504, 704), "bm32_bn128_bk64_w4_s3_v11"),
+    ((768, 8064, 12992), "bm256_bn128_bk64_w4_s3_v13"),
+    ((384, 4096, 16384), "bm128_bn512_bk32_w8_s3_v4_k8"),
     ((640, 2048, 1024), None),
 ])
 def test_rmsnorm_matmul_without_config(gpu, shape, expect):
