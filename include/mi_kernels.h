@@ -129,9 +129,10 @@ int mi_get_config(int kernel_id, int idx, mi_tile_cfg* cfg);
  * legal there.  Generalised from the autotune winners: the block whose
  * rounds of tiles take the least estimated time (rounds on the busiest CU
  * times the block's area over its measured rate per CU), split-K when that
- * grid leaves CUs idle, non-temporal variants for skinny M whose grid fills
- * the chip; for the fused kernel past the K its gamma staging holds, the
- * two-pass kernel when there are many output tiles and split-K otherwise.
+ * grid leaves CUs idle, non-temporal variants for skinny M; for the fused
+ * kernel past the K its gamma staging holds, the two-pass kernel or a
+ * register-staged one split until each part's gamma fits, by the same
+ * estimate.
  * A negative size is MI_E_ARGS. */
 int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
 
