@@ -334,137 +334,141 @@ mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K
   return best_c;
 }
 
-int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
-  // Generalised from the autotune winners at the benchmark shapes and a
-  // study of 70 other shapes: the block whose rounds of tiles take the
-  // least time (a block that leaves CUs idle can still beat a smaller one
-  // whose grid needs a second, partial round), with K split when the chosen
-  // grid leaves CUs idle.  Skinny M (decode) streams the weight once with
-  // the non-temporal variants, in the block that gives the most tiles up to
-  // one per CU.  For lhsT.rhs a 256-long block lies
-  // with its long side along the shorter output side (128 x 256 when M >=
-  // N), or along N at any shape when K <= 2048, a 128-long one along N
-  // unless N is at least four times M, as the winners do; lhs.rhs keeps block_m the short side (fewer rows of its
-  // K-contiguous operand per tile).
-  mi_tile_cfg c = {256, 256, 64, 8, 2, 1, 8, 0};
-  const bool m_long = M >= N, n_much_longer = (long long)N >= 4LL * M;
-  if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_F32) {
-    c = {64, 64, 16, 4, 1, 1, 0, 0};
-  } else if (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 || kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16) {
-    const bool lhs = kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16;
-    // lhsT.rhs: pipelined variant 1 (3: rhs non-temporal); lhs.rhs: variant
-    // 0 (2: rhs non-temporal), its blocks of 256 rows or columns the
-    // paired-load variant 1 (block_k 32, the K-contiguous panel loaded as
-    // whole 128-byte lines).
-    const int v = lhs ? 0 : 1, v_nt = lhs ? 2 : 3;
-    mi_tile_cfg skinny = lhs ? mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt}
-                        : M <= 32 ? mi_tile_cfg{32, 128, 128, 4, 3, 1, 8, v_nt}
-                        : M <= 64 ? mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt}
-                                  : mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt};
-    const mi_tile_cfg small = {64, 64, 64, 4, 4, 1, 8, v};
-    if (M <= 128 && lhs) {
-      // lhs.rhs: the non-temporal 128 x 128 block when its grid fills the
-      // chip; otherwise the non-temporal block with the fewest wasted rows
-      // (64 x 128 up to M = 64), split over K to up to one workgroup per CU.
-      if (tiles_of(M, N, skinny.block_m, skinny.block_n) >= kFillTiles) {
-        c = skinny;
-      } else {
-        c = M <= 64 ? mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt} : skinny;
-        c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
-      }
-    } else if (M <= 128) {
-      // The weight is streamed once, non-temporally.  A grid of the skinny
-      // block that fills the chip runs unsplit.  Otherwise, with a long K
-      // (8192 or more), 256-wide column blocks (512-byte weight row segments
-      // per workgroup) split over K, when that fills three quarters of the
-      // CUs or more with at least 16 K steps per part; otherwise the block
-      // with the most tiles up to one per CU (ties to the larger), split only
-      // when that grid still leaves CUs idle.
-      mi_tile_cfg wide = M <= 64 ? mi_tile_cfg{64, 256, 64, 4, 3, 1, 8, v_nt} : mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v_nt};
-      const long long wide_tiles = tiles_of(M, N, wide.block_m, wide.block_n);
-      wide.split_k = fill_parts(wide_tiles, K, wide.block_k);
-      const bool wide_fills = wide_tiles * wide.split_k >= 3 * kCUs / 4 &&
-                              (long long)K / wide.split_k >= 16LL * wide.block_k;
-      if (tiles_of(M, N, skinny.block_m, skinny.block_n) >= kFillTiles) {
-        c = skinny;
-      } else if (K >= 8192 && wide_fills) {
-        c = wide;
-      } else {
-        const mi_tile_cfg skinny_cands[] = {skinny, mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt},
-                                            mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v_nt}};
-        long long most = 0;
-        for (const mi_tile_cfg& ci : skinny_cands) {
-          const long long t = tiles_of(M, N, ci.block_m, ci.block_n), capped = t < kCUs ? t : kCUs;
-          if (capped > most) {
-            most = capped;
-            c = ci;
-          }
-        }
-        if (most < kFillTiles) c.split_k = fill_parts(most, K, c.block_k);
-      }
-    } else {
-      const Cand cands[] = {
-          {lhs ? mi_tile_cfg{256, 256, 32, 8, 3, 1, 8, 1} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, v}, 1.0},
-          {lhs ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 1}
-               : (m_long || K <= 2048 ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v}
-                                      : mi_tile_cfg{256, 128, 32, 4, 3, 1, 8, v}),
-           0.93},
-          {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v}, 0.62},
-          {n_much_longer && !lhs ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v},
-           0.60},
-          {small, 0.35}};
-      c = fastest_estimate(cands, 5, M, N, K, kernel_id);
-    }
-  } else if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16) {
-    // The register-staged kernels keep gamma in LDS (8192 entries here).
-    // Skinny M past K = 8192 splits K into the fewest parts whose gamma fits
-    // (1..16 parts, none empty); past that the LDS-staged kernel (variant 0)
-    // takes any K.
-    if (M <= 128 && K > 8192) {
-      const long long kt = (K + 63) / 64;
-      int parts = 0;
-      for (int p = 2; p <= 16 && !parts; p *= 2) {
-        const long long kts = (kt + p - 1) / p;
-        const unsigned long long ws = (unsigned long long)p * ((unsigned long long)M * N + M) * 4ull;
-        if (kts * 64 <= 8192 && (long long)(p - 1) * kts < kt && ws <= kMaxWorkspace) parts = p;
-      }
-      if (!parts) c = {64, 128, 64, 4, 2, 1, 8, 0};
-      else c = {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, parts, 8, 11};
-    } else if (M <= 128) {
-      // Weight streamed once (variant 11).  With a weight of 16 MiB or less
-      // (re-read from the caches), 32-row blocks (more tiles) win at any M
-      // (measured up to 16 MiB; at 32 MiB the 64-row block won); a larger
-      // one takes the block that covers M,
-      // with 64-row blocks before a split when 128-row ones leave CUs idle.
-      // Below K = 4096 the summing launch of a split costs more than the
-      // idle CUs do.
-      const bool cached_w = (long long)K * N * 2 <= (16LL << 20);
-      c = {cached_w || M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, 1, 8, 11};
-      if (c.block_m == 128 && tiles_of(M, N, 128, 128) < kFillTiles) c.block_m = 64;
-      if (K >= 4096) c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
-    } else {
-      // Each workgroup of the one-pass kernels scales its x rows once per
-      // column tile, so narrow blocks pay that work many times over: per CU,
-      // 128 x 256 runs at 0.83 and 128 x 128 at 0.54 of the rate of 128 x
-      // 512.  The two-pass kernel scales x once, in a pass of its own, and
-      // its main pass runs the lhsT core (256 x 256 at 1.10 of that rate;
-      // past K = 8192 also 256 x 128, its long side along the shorter output
-      // side, at 0.95).  Few-tile shapes split K, which the estimate charges
-      // for its fp32 partial products and the launch of the summing kernel;
-      // past K = 8192 the one-pass kernels split at least until each part's
-      // gamma fits.
-      const Cand cands[] = {{mi_tile_cfg{128, 512, 32, 8, 3, 1, 8, 4}, 1.0},
-                            {mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 5}, 0.83},
-                            {mi_tile_cfg{128, 128, 64, 4, 2, 1, 8, 4}, 0.54},
-                            {mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, 13}, 1.10},
-                            {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, 13}, 0.68},
-                            {mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, 13}, 0.57},
-                            {M <= N ? mi_tile_cfg{256, 128, 64, 4, 3, 1, 8, 13}
-                                    : mi_tile_cfg{128, 256, 64, 4, 3, 1, 8, 13}, 0.95}};
-      c = fastest_split_estimate(cands, K > 8192 ? 7 : 6, M, N, K, mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0});
+// Skinny M (decode-like), either matmul: the weight is streamed once with
+// the non-temporal variants (lhsT.rhs 3, lhs.rhs 2).
+mi_tile_cfg skinny_matmul_default(bool lhs, int M, int N, int K) {
+  const int v_nt = lhs ? 2 : 3;
+  const mi_tile_cfg skinny = lhs ? mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt}
+                             : M <= 32 ? mi_tile_cfg{32, 128, 128, 4, 3, 1, 8, v_nt}
+                             : M <= 64 ? mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt}
+                                       : mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt};
+  // A grid of the skinny block that fills the chip runs unsplit.
+  if (tiles_of(M, N, skinny.block_m, skinny.block_n) >= kFillTiles) return skinny;
+  mi_tile_cfg c = skinny;
+  if (lhs) {
+    // lhs.rhs: the non-temporal block with the fewest wasted rows (64 x 128
+    // up to M = 64), split over K to up to one workgroup per CU.
+    if (M <= 64) c = {64, 128, 64, 4, 4, 1, 8, v_nt};
+    c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
+    return c;
+  }
+  // lhsT.rhs with a long K (8192 or more): 256-wide column blocks (512-byte
+  // weight row segments per workgroup) split over K, when that fills three
+  // quarters of the CUs or more with at least 16 K steps per part.
+  mi_tile_cfg wide = M <= 64 ? mi_tile_cfg{64, 256, 64, 4, 3, 1, 8, v_nt} : mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v_nt};
+  const long long wide_tiles = tiles_of(M, N, wide.block_m, wide.block_n);
+  wide.split_k = fill_parts(wide_tiles, K, wide.block_k);
+  if (K >= 8192 && wide_tiles * wide.split_k >= 3 * kCUs / 4 && (long long)K / wide.split_k >= 16LL * wide.block_k)
+    return wide;
+  // Otherwise the block with the most tiles up to one per CU (ties to the
+  // larger), split only when that grid still leaves CUs idle.
+  const mi_tile_cfg cands[] = {skinny, mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt},
+                               mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v_nt}};
+  long long most = 0;
+  for (const mi_tile_cfg& ci : cands) {
+    const long long t = tiles_of(M, N, ci.block_m, ci.block_n), capped = t < kCUs ? t : kCUs;
+    if (capped > most) {
+      most = capped;
+      c = ci;
     }
   }
-  *cfg = c;
+  if (most < kFillTiles) c.split_k = fill_parts(most, K, c.block_k);
+  return c;
+}
+
+// Either matmul past skinny M: the block whose rounds of tiles take the
+// least time (a block that leaves CUs idle can still beat a smaller one
+// whose grid needs a second, partial round), K split when the chosen grid
+// leaves CUs idle.  lhsT.rhs runs the pipelined variant 1; a 256-long block
+// lies with its long side along the shorter output side (128 x 256 when
+// M >= N), or along N at any shape when K <= 2048, and a 128-long one along
+// N unless N is at least four times M, as the winners do.  lhs.rhs runs
+// variant 0 and keeps block_m the short side (fewer rows of its
+// K-contiguous operand per tile); its 256-long blocks take the paired-load
+// variant 1 (block_k 32, the K-contiguous panel loaded as whole 128-byte
+// lines).
+mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
+  const int v = lhs ? 0 : 1;
+  const bool m_long = M >= N, n_much_longer = (long long)N >= 4LL * M;
+  const Cand cands[] = {
+      {lhs ? mi_tile_cfg{256, 256, 32, 8, 3, 1, 8, 1} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, v}, 1.0},
+      {lhs ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 1}
+           : (m_long || K <= 2048 ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v} : mi_tile_cfg{256, 128, 32, 4, 3, 1, 8, v}),
+       0.93},
+      {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v}, 0.62},
+      {n_much_longer && !lhs ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v}, 0.60},
+      {mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v}, 0.35}};
+  return fastest_estimate(cands, 5, M, N, K, kernel_id);
+}
+
+// rmsnorm_matmul.  The register-staged kernels keep gamma in LDS (8192
+// entries here).
+mi_tile_cfg fused_default(int M, int N, int K) {
+  if (M <= 128 && K > 8192) {
+    // Skinny M past K = 8192: the skinny variant 11 split into the fewest
+    // parts whose gamma fits (1..16 parts, none empty); past that the
+    // LDS-staged kernel (variant 0) takes any K.
+    const long long kt = (K + 63) / 64;
+    for (int p = 2; p <= 16; p *= 2) {
+      const long long kts = (kt + p - 1) / p;
+      const unsigned long long ws = (unsigned long long)p * ((unsigned long long)M * N + M) * 4ull;
+      if (kts * 64 <= 8192 && (long long)(p - 1) * kts < kt && ws <= kMaxWorkspace)
+        return {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, p, 8, 11};
+    }
+    return {64, 128, 64, 4, 2, 1, 8, 0};
+  }
+  if (M <= 128) {
+    // Weight streamed once (variant 11).  With a weight of 16 MiB or less
+    // (re-read from the caches), 32-row blocks (more tiles) win at any M
+    // (measured up to 16 MiB; at 32 MiB the 64-row block won); a larger one
+    // takes the block that covers M, with 64-row blocks before a split when
+    // 128-row ones leave CUs idle.  Below K = 4096 the summing launch of a
+    // split costs more than the idle CUs do.
+    const bool cached_w = (long long)K * N * 2 <= (16LL << 20);
+    mi_tile_cfg c = {cached_w || M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, 1, 8, 11};
+    if (c.block_m == 128 && tiles_of(M, N, 128, 128) < kFillTiles) c.block_m = 64;
+    if (K >= 4096) c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
+    return c;
+  }
+  // Each workgroup of the one-pass kernels scales its x rows once per column
+  // tile, so narrow blocks pay that work many times over: per CU, 128 x 256
+  // runs at 0.83 and 128 x 128 at 0.54 of the rate of 128 x 512.  The
+  // two-pass kernel scales x once, in a pass of its own, and its main pass
+  // runs the lhsT core (256 x 256 at 1.10 of that rate; past K = 8192 also
+  // 256 x 128, its long side along the shorter output side, at 0.95).
+  // Few-tile shapes split K, which the estimate charges for its fp32 partial
+  // products and the launch of the summing kernel; past K = 8192 the
+  // one-pass kernels split at least until each part's gamma fits.
+  const Cand cands[] = {{mi_tile_cfg{128, 512, 32, 8, 3, 1, 8, 4}, 1.0},
+                        {mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 5}, 0.83},
+                        {mi_tile_cfg{128, 128, 64, 4, 2, 1, 8, 4}, 0.54},
+                        {mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, 13}, 1.10},
+                        {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, 13}, 0.68},
+                        {mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, 13}, 0.57},
+                        {M <= N ? mi_tile_cfg{256, 128, 64, 4, 3, 1, 8, 13} : mi_tile_cfg{128, 256, 64, 4, 3, 1, 8, 13},
+                         0.95}};
+  return fastest_split_estimate(cands, K > 8192 ? 7 : 6, M, N, K, mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0});
+}
+
+// The library default, generalised from the autotune winners at the
+// benchmark shapes and studies of 83 other shapes and 30 seeded random ones.
+int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
+  const bool lhs = kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16;
+  switch (kernel_id) {
+    case MI_KERNEL_MATMUL_LHST_RHS_F32:
+      *cfg = {64, 64, 16, 4, 1, 1, 0, 0};
+      break;
+    case MI_KERNEL_MATMUL_LHST_RHS_BF16:
+    case MI_KERNEL_MATMUL_LHS_RHS_BF16:
+      *cfg = M <= 128 ? skinny_matmul_default(lhs, M, N, K) : matmul_default(kernel_id, lhs, M, N, K);
+      break;
+    case MI_KERNEL_RMSNORM_MATMUL_BF16:
+      *cfg = fused_default(M, N, K);
+      break;
+    default:
+      *cfg = {256, 256, 64, 8, 2, 1, 8, 0};
+      break;
+  }
   return MI_OK;
 }
 
