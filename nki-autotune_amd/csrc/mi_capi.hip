@@ -704,6 +704,7 @@ int mi_device_info(int* num_devices, char* arch, int arch_len, int* num_cus) {
 
 int mi_release_workspace(void) {
   std::lock_guard<std::mutex> lock(g_pool_mu);
+  if (g_pools.empty()) return MI_OK;  // no call has needed workspace yet
   int cur = 0;
   hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");

@@ -246,6 +246,11 @@ def test_library_default_picks_the_measured_winners(fam, shape, name):
     assert TileConfig.from_c(c).name == name
 
 
+def test_release_workspace_without_pools_is_a_no_op():
+    """Before any call has needed workspace there is no pool: release returns 0 and touches no device."""
+    assert _lib.lib().mi_release_workspace() == _lib.MI_OK
+
+
 def test_library_default_rejects_negative_sizes_and_survives_huge_ones():
     """A negative size is MI_E_ARGS; sizes near INT_MAX still give a config (no overflow in the tile counts)."""
     L = _lib.lib()
