@@ -130,19 +130,27 @@ def parse_source(source: str):
 _CAPI_LOCK = threading.Lock()
 
 
-def _capi_object(work_dir: Path, hipcc_args: tuple[str, ...]) -> Path:
-    """Object of mi_capi.hip, built once per work dir."""
+# The C ABI units every per-config library links: the entry points and the
+# library default config.
+CAPI_UNITS = ("mi_capi.hip", "mi_defaults.hip")
+
+
+def _capi_objects(work_dir: Path, hipcc_args: tuple[str, ...]) -> list[Path]:
+    """Objects of the C ABI units, built once per work dir."""
     import build_lib
 
-    obj = work_dir / "mi_capi.o"
+    objs = []
     with _CAPI_LOCK:
-        if not obj.exists():
-            cmd = [build_lib.hipcc(), *build_lib.HIPCC_FLAGS, *hipcc_args, "-c", str(build_lib.CSRC / "mi_capi.hip"),
-                   "-o", str(obj)]
-            proc = subprocess.run(cmd, capture_output=True, text=True, timeout=COMPILE_TIMEOUT_S)
-            if proc.returncode != 0:
-                raise RuntimeError(f"hipcc failed for mi_capi.hip:\n{proc.stderr}")
-    return obj
+        for unit in CAPI_UNITS:
+            obj = work_dir / unit.replace(".hip", ".o")
+            if not obj.exists():
+                cmd = [build_lib.hipcc(), *build_lib.HIPCC_FLAGS, *hipcc_args, "-c", str(build_lib.CSRC / unit),
+                       "-o", str(obj)]
+                proc = subprocess.run(cmd, capture_output=True, text=True, timeout=COMPILE_TIMEOUT_S)
+                if proc.returncode != 0:
+                    raise RuntimeError(f"hipcc failed for {unit}:\n{proc.stderr}")
+            objs.append(obj)
+    return objs
 
 
 def build_instance(source: str, out_dir: Path, stem: str, hipcc_args: tuple[str, ...] = (),
@@ -155,14 +163,14 @@ def build_instance(source: str, out_dir: Path, stem: str, hipcc_args: tuple[str,
     src.write_text(source)
     obj = out_dir / f"{stem}.o"
     lib = out_dir / f"lib{stem}.so"
-    capi = _capi_object(out_dir.parent, hipcc_args)
+    capi = _capi_objects(out_dir.parent, hipcc_args)
     cmd = [build_lib.hipcc(), *build_lib.HIPCC_FLAGS, *hipcc_args, f"-I{build_lib.CSRC}", "-c", str(src), "-o",
            str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s)
     log = "\n".join(ln for ln in (proc.stdout + proc.stderr).splitlines() if "packed-fp32-ops" not in ln)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{log}")
-    cmd = [build_lib.hipcc(), f"--offload-arch={build_lib.ARCH}", "-shared", "-fPIC", str(obj), str(capi), "-o",
+    cmd = [build_lib.hipcc(), f"--offload-arch={build_lib.ARCH}", "-shared", "-fPIC", str(obj), *map(str, capi), "-o",
            str(lib)]
     proc = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout_s)
     if proc.returncode != 0:

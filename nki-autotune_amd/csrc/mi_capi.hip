@@ -64,15 +64,36 @@ bool same_instance(const mi_tile_cfg& a, const mi_tile_cfg& b) {
          a.lds_stages == b.lds_stages && a.variant == b.variant;
 }
 
-const mi::MiEntry* find(int kernel_id, const mi_tile_cfg& cfg) {
-  for (const mi::MiEntry& e : registry())
+}  // namespace
+
+namespace mi {
+namespace capi {
+
+const MiEntry* find(int kernel_id, const mi_tile_cfg& cfg) {
+  for (const MiEntry& e : registry())
     if (e.kernel_id == kernel_id && same_instance(e.cfg, cfg)) return &e;
   return nullptr;
 }
 
+bool splittable(int kernel_id, int variant) {
+  return (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (variant == 1 || variant == 3 || variant == 4)) ||
+         (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 && (variant == 0 || variant == 2)) ||
+         (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 &&
+          (variant == 4 || variant == 5 || variant == 11 || variant == 12 || variant == 13));
+}
+
+}  // namespace capi
+}  // namespace mi
+
+namespace {
+
+using mi::capi::find;
+using mi::capi::kMaxSplit;
+using mi::capi::kMaxWorkspace;
+using mi::capi::pick_default;
+using mi::capi::splittable;
+
 constexpr unsigned long long kMaxOffset = 0xFFFFFFFFull;        // 32-bit buffer offsets
-constexpr int kMaxSplit = 16;                                    // split-K parts
-constexpr unsigned long long kMaxWorkspace = 1ull << 31;         // bytes of device workspace per call
 
 // The template rules of the variant `c` names (mi_legal.hpp: the same
 // predicates the kernel templates assert when they are instantiated).
@@ -107,13 +128,6 @@ mi::Legal template_legal(int kernel_id, const mi_tile_cfg& c) {
       break;
   }
   return mi::bad(MI_E_TILE, "no such variant of this kernel");
-}
-
-bool splittable(int kernel_id, int variant) {
-  return (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (variant == 1 || variant == 3 || variant == 4)) ||
-         (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 && (variant == 0 || variant == 2)) ||
-         (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 &&
-          (variant == 4 || variant == 5 || variant == 11 || variant == 12 || variant == 13));
 }
 
 int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::MiEntry** out) {
@@ -203,273 +217,6 @@ int zero_output(void* out, size_t n, void* stream) {
                      (hipStream_t)stream, (T*)out, n);
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? MI_OK : hip_fail(e, "zero fill");
-}
-
-// Default configs.  A grid fills the chip with one workgroup per CU on 256
-// CUs; 224 (28 per XCD) still counts as full.
-constexpr long long kFillTiles = 224;
-constexpr long long kCUs = 256;
-
-long long tiles_of(int M, int N, int bm, int bn) {
-  return (((long long)M + bm - 1) / bm) * (((long long)N + bn - 1) / bn);
-}
-
-// The most parts (a power of two, at most 16) that keep the grid within one
-// workgroup per CU, every part at least 4 K tiles of block_k, and no part
-// empty; 1 when no split qualifies.
-int fill_parts(long long tiles, int K, int block_k) {
-  const long long kt = ((long long)K + block_k - 1) / block_k;
-  int parts = 1;
-  for (int next = 2; next <= 16; next *= 2) {
-    const long long kts = (kt + next - 1) / next;
-    if (tiles * next > kCUs || kt < 4LL * next || (long long)(next - 1) * kts >= kt) break;
-    parts = next;
-  }
-  return parts;
-}
-
-// A candidate block and its relative throughput per CU (output area per
-// unit time at the same K, the 256 x 256 block = 1), measured with the
-// autotuner at shapes that give every CU one tile.
-struct Cand {
-  mi_tile_cfg c;
-  double rate;
-};
-
-// The candidate with the least estimated time: the rounds of tiles the
-// busiest CU runs, times a tile's area over its rate.  Ties go to the
-// earlier (larger) block.  Then, if its grid leaves CUs idle and K is long
-// enough to split, K is split so the grid fills the chip.
-mi_tile_cfg fastest_estimate(const Cand* cands, int n, int M, int N, int K, int kernel_id) {
-  int best = 0;
-  double best_t = 0.0;
-  for (int i = 0; i < n; ++i) {
-    const mi_tile_cfg& c = cands[i].c;
-    const long long rounds = (tiles_of(M, N, c.block_m, c.block_n) + kCUs - 1) / kCUs;
-    const double t = (double)rounds * c.block_m * c.block_n / cands[i].rate;
-    if (i == 0 || t < best_t) {
-      best = i;
-      best_t = t;
-    }
-  }
-  mi_tile_cfg c = cands[best].c;
-  const long long tiles = tiles_of(M, N, c.block_m, c.block_n);
-  if (tiles >= kFillTiles || fill_parts(tiles, K, c.block_k) == 1) return c;
-  // The grid needs a split: the largest splittable block whose split grid
-  // is as large as any (a bigger block moves fewer operand bytes per
-  // multiply-add for the same workgroup count).
-  long long most = 0;
-  for (int i = 0; i < n; ++i) {
-    const mi_tile_cfg& ci = cands[i].c;
-    if (!splittable(kernel_id, ci.variant)) continue;
-    const long long t = tiles_of(M, N, ci.block_m, ci.block_n);
-    const long long wgs = t * fill_parts(t, K, ci.block_k);
-    if (wgs > most) {
-      most = wgs;
-      c = ci;
-    }
-  }
-  c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
-  return c;
-}
-
-// As fastest_estimate, for the fused kernel (whose first candidate needs no
-// workspace), but each candidate is first split by fill_parts when its grid
-// leaves CUs idle, a candidate whose device workspace would pass the 2 GiB
-// limit is skipped, and its estimated time (microseconds) adds the
-// split's fp32 partial products, written once and read back once at about
-// 5 TB/s, and for the two-pass fused kernel (variant 13) its pack pass (x
-// read, x * gamma written: 4 bytes per x element at about 5 TB/s) and 3 us
-// for the second launch.  R0 is the fused kernel's 128 x 512 rate per CU at
-// 4096^3, in multiply-adds per second.
-// The fewest parts, from c.split_k up by powers of two, that leave every K
-// part within the gamma entries the fused instance stages in LDS and no part
-// empty; 0 when none up to kMaxSplit does (or the instance is not built).
-int gamma_fit_parts(const mi_tile_cfg& c, int K) {
-  const mi::MiEntry* e = find(MI_KERNEL_RMSNORM_MATMUL_BF16, c);
-  if (!e) return 0;
-  const long long kt = ((long long)K + c.block_k - 1) / c.block_k;
-  for (int p = c.split_k; p <= kMaxSplit; p *= 2) {
-    const long long kts = (kt + p - 1) / p;
-    if (p > 1 && (long long)(p - 1) * kts >= kt) return 0;
-    if (e->gamma_kmax <= 0 || kts * c.block_k <= e->gamma_kmax) return p;
-  }
-  return 0;
-}
-
-mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K, const mi_tile_cfg& fallback) {
-  constexpr double R0 = 2.28e12, kSplitBytesPerUs = 5e6, kPackBytesPerUs = 5e6, kLaunchUs = 3.0;
-  double best_t = 0.0;
-  mi_tile_cfg best_c = fallback;
-  bool found = false;
-  for (int i = 0; i < n; ++i) {
-    mi_tile_cfg c = cands[i].c;
-    const long long tiles = tiles_of(M, N, c.block_m, c.block_n);
-    c.split_k = tiles < kFillTiles ? fill_parts(tiles, K, c.block_k) : 1;
-    // Past the gamma entries an instance stages, K splits further; a
-    // candidate no split makes legal, or whose workspace the call could not
-    // allocate, is out.
-    c.split_k = gamma_fit_parts(c, K);
-    if (c.split_k == 0) continue;
-    if (mi::workspace_bytes(MI_KERNEL_RMSNORM_MATMUL_BF16, c, M, N, K) > kMaxWorkspace) continue;
-    const long long wgs = tiles * c.split_k, rounds = (wgs + kCUs - 1) / kCUs;
-    const double kp = (double)((K + c.split_k - 1) / c.split_k);
-    double t = (double)rounds * c.block_m * c.block_n * kp / (cands[i].rate * R0) * 1e6;
-    // The chip is power-limited under this load, so a single round that
-    // leaves CUs idle runs each busy CU faster (its clock rises): by up to
-    // 0.88 / (the busy fraction), at most 1.65 times (fitted to the fused
-    // candidates timed at 23 shapes).
-    if (rounds == 1) {
-      const double busy = (double)wgs / kCUs, speed = 0.88 / busy;
-      t /= speed > 1.65 ? 1.65 : speed < 1.0 ? 1.0 : speed;
-    }
-    if (c.split_k > 1) t += (double)c.split_k * M * N * 8.0 / kSplitBytesPerUs + kLaunchUs;
-    if (c.variant == 13) t += (double)M * K * 4.0 / kPackBytesPerUs + kLaunchUs;
-    if (!found || t < best_t) {
-      found = true;
-      best_t = t;
-      best_c = c;
-    }
-  }
-  return best_c;
-}
-
-// Skinny M (decode-like), either matmul: the weight is streamed once with
-// the non-temporal variants (lhsT.rhs 3, lhs.rhs 2).
-mi_tile_cfg skinny_matmul_default(bool lhs, int M, int N, int K) {
-  const int v_nt = lhs ? 2 : 3;
-  const mi_tile_cfg skinny = lhs ? mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt}
-                             : M <= 32 ? mi_tile_cfg{32, 128, 128, 4, 3, 1, 8, v_nt}
-                             : M <= 64 ? mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt}
-                                       : mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt};
-  // A grid of the skinny block that fills the chip runs unsplit.
-  if (tiles_of(M, N, skinny.block_m, skinny.block_n) >= kFillTiles) return skinny;
-  mi_tile_cfg c = skinny;
-  if (lhs) {
-    // lhs.rhs: the non-temporal block with the fewest wasted rows (64 x 128
-    // up to M = 64), split over K to up to one workgroup per CU.
-    if (M <= 64) c = {64, 128, 64, 4, 4, 1, 8, v_nt};
-    c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
-    return c;
-  }
-  // lhsT.rhs with a long K (8192 or more): 256-wide column blocks (512-byte
-  // weight row segments per workgroup) split over K, when that fills three
-  // quarters of the CUs or more with at least 16 K steps per part.
-  mi_tile_cfg wide = M <= 64 ? mi_tile_cfg{64, 256, 64, 4, 3, 1, 8, v_nt} : mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v_nt};
-  const long long wide_tiles = tiles_of(M, N, wide.block_m, wide.block_n);
-  wide.split_k = fill_parts(wide_tiles, K, wide.block_k);
-  if (K >= 8192 && wide_tiles * wide.split_k >= 3 * kCUs / 4 && (long long)K / wide.split_k >= 16LL * wide.block_k)
-    return wide;
-  // Otherwise the block with the most tiles up to one per CU (ties to the
-  // larger), split only when that grid still leaves CUs idle.
-  const mi_tile_cfg cands[] = {skinny, mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt},
-                               mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v_nt}};
-  long long most = 0;
-  for (const mi_tile_cfg& ci : cands) {
-    const long long t = tiles_of(M, N, ci.block_m, ci.block_n), capped = t < kCUs ? t : kCUs;
-    if (capped > most) {
-      most = capped;
-      c = ci;
-    }
-  }
-  if (most < kFillTiles) c.split_k = fill_parts(most, K, c.block_k);
-  return c;
-}
-
-// Either matmul past skinny M: the block whose rounds of tiles take the
-// least time (a block that leaves CUs idle can still beat a smaller one
-// whose grid needs a second, partial round), K split when the chosen grid
-// leaves CUs idle.  lhsT.rhs runs the pipelined variant 1; a 256-long block
-// lies with its long side along the shorter output side (128 x 256 when
-// M >= N), or along N at any shape when K <= 2048, and a 128-long one along
-// N unless N is at least four times M, as the winners do.  lhs.rhs runs
-// variant 0 and keeps block_m the short side (fewer rows of its
-// K-contiguous operand per tile); its 256-long blocks take the paired-load
-// variant 1 (block_k 32, the K-contiguous panel loaded as whole 128-byte
-// lines).
-mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
-  const int v = lhs ? 0 : 1;
-  const bool m_long = M >= N, n_much_longer = (long long)N >= 4LL * M;
-  const Cand cands[] = {
-      {lhs ? mi_tile_cfg{256, 256, 32, 8, 3, 1, 8, 1} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, v}, 1.0},
-      {lhs ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 1}
-           : (m_long || K <= 2048 ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v} : mi_tile_cfg{256, 128, 32, 4, 3, 1, 8, v}),
-       0.93},
-      {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v}, 0.62},
-      {n_much_longer && !lhs ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v}, 0.60},
-      {mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v}, 0.35}};
-  return fastest_estimate(cands, 5, M, N, K, kernel_id);
-}
-
-// rmsnorm_matmul.  The register-staged kernels keep gamma in LDS (8192
-// entries here).
-mi_tile_cfg fused_default(int M, int N, int K) {
-  if (M <= 128 && K > 8192) {
-    // Skinny M past K = 8192: the skinny variant 11 split into the fewest
-    // parts whose gamma fits (1..16 parts, none empty); past that the
-    // LDS-staged kernel (variant 0) takes any K.
-    const long long kt = (K + 63) / 64;
-    for (int p = 2; p <= 16; p *= 2) {
-      const long long kts = (kt + p - 1) / p;
-      const unsigned long long ws = (unsigned long long)p * ((unsigned long long)M * N + M) * 4ull;
-      if (kts * 64 <= 8192 && (long long)(p - 1) * kts < kt && ws <= kMaxWorkspace)
-        return {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, p, 8, 11};
-    }
-    return {64, 128, 64, 4, 2, 1, 8, 0};
-  }
-  if (M <= 128) {
-    // Weight streamed once (variant 11).  With a weight of 16 MiB or less
-    // (re-read from the caches), 32-row blocks (more tiles) win at any M
-    // (measured up to 16 MiB; at 32 MiB the 64-row block won); a larger one
-    // takes the block that covers M, with 64-row blocks before a split when
-    // 128-row ones leave CUs idle.  Below K = 4096 the summing launch of a
-    // split costs more than the idle CUs do.
-    const bool cached_w = (long long)K * N * 2 <= (16LL << 20);
-    mi_tile_cfg c = {cached_w || M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, 1, 8, 11};
-    if (c.block_m == 128 && tiles_of(M, N, 128, 128) < kFillTiles) c.block_m = 64;
-    if (K >= 4096) c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
-    return c;
-  }
-  // Each workgroup of the one-pass kernels scales its x rows once per column
-  // tile, so narrow blocks pay that work many times over: per CU, 128 x 256
-  // runs at 0.83 and 128 x 128 at 0.54 of the rate of 128 x 512.  The
-  // two-pass kernel scales x once, in a pass of its own, and its main pass
-  // runs the lhsT core (256 x 256 at 1.10 of that rate; past K = 8192 also
-  // 256 x 128, its long side along the shorter output side, at 0.95).
-  // Few-tile shapes split K, which the estimate charges for its fp32 partial
-  // products and the launch of the summing kernel; past K = 8192 the
-  // one-pass kernels split at least until each part's gamma fits.
-  const Cand cands[] = {{mi_tile_cfg{128, 512, 32, 8, 3, 1, 8, 4}, 1.0},
-                        {mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 5}, 0.83},
-                        {mi_tile_cfg{128, 128, 64, 4, 2, 1, 8, 4}, 0.54},
-                        {mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, 13}, 1.10},
-                        {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, 13}, 0.68},
-                        {mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, 13}, 0.57},
-                        {M <= N ? mi_tile_cfg{256, 128, 64, 4, 3, 1, 8, 13} : mi_tile_cfg{128, 256, 64, 4, 3, 1, 8, 13},
-                         0.95}};
-  return fastest_split_estimate(cands, K > 8192 ? 7 : 6, M, N, K, mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0});
-}
-
-// The library default, generalised from the autotune winners at the
-// benchmark shapes and studies of 83 other shapes and 30 seeded random ones.
-int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
-  const bool lhs = kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16;
-  switch (kernel_id) {
-    case MI_KERNEL_MATMUL_LHST_RHS_F32:
-      *cfg = {64, 64, 16, 4, 1, 1, 0, 0};
-      break;
-    case MI_KERNEL_MATMUL_LHST_RHS_BF16:
-    case MI_KERNEL_MATMUL_LHS_RHS_BF16:
-      *cfg = M <= 128 ? skinny_matmul_default(lhs, M, N, K) : matmul_default(kernel_id, lhs, M, N, K);
-      break;
-    case MI_KERNEL_RMSNORM_MATMUL_BF16:
-      *cfg = fused_default(M, N, K);
-      break;
-    default:
-      *cfg = {256, 256, 64, 8, 2, 1, 8, 0};
-      break;
-  }
-  return MI_OK;
 }
 
 // Device workspace (split-K partial products, the two-pass fused kernel's

@@ -8,9 +8,24 @@
 namespace mi {
 namespace capi {
 
+// Limits of a call: split-K parts, and bytes of device workspace.
+constexpr int kMaxSplit = 16;
+constexpr unsigned long long kMaxWorkspace = 1ull << 31;
+
 // Records the message of a failure for mi_last_error on this thread and
 // returns `code`.
 int fail(int code, const char* fmt, ...);
+
+// The prebuilt instance of `kernel_id` for cfg's tile parameters and
+// variant (split_k and group_m aside), or NULL.
+const MiEntry* find(int kernel_id, const mi_tile_cfg& cfg);
+
+// Whether `variant` of `kernel_id` takes split_k > 1.
+bool splittable(int kernel_id, int variant);
+
+// The library default config at a shape (mi_default_config without its
+// argument checks; mi_defaults.hip).
+int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
 
 // The body of mi_matmul_lhsT_rhs_bf16.  fixed_ws == NULL: a call that needs
 // device workspace takes it from the library's stream-ordered pool;
