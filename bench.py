@@ -106,6 +106,7 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--settle-s", type=float, default=2.0,
                     help="GPU idle time before the timed region's warm-up (see settle())")
     ap.add_argument("--m", type=int, default=16, choices=[16, 64, 128], help="M of the c5 / decode workloads")
+    ap.add_argument("--random-seed", type=int, default=2026, help="seed of the defaults-random shapes")
     return ap.parse_args()
 
 
@@ -506,7 +507,7 @@ def main() -> int:
             ("matmul_lhsT_rhs", DEFAULTS_MM + DEFAULTS_SKINNY), ("matmul_lhs_rhs", DEFAULTS_LHS),
             ("rmsnorm_matmul", DEFAULTS_RMS)) for sh in shapes], "defaults")
     if args.workload == "defaults-random":
-        return defaults_study(args, dev, random_default_shapes(), "defaults-random")
+        return defaults_study(args, dev, random_default_shapes(args.random_seed), f"defaults-random:{args.random_seed}")
     if args.workload in PLAIN_SHAPES:
         return shape_main(args, dev, *PLAIN_SHAPES[args.workload])
     fam, s = ("matmul_lhsT_rhs", M) if args.workload == "c2" else ("rmsnorm_matmul", 4096)

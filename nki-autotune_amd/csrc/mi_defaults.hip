@@ -141,41 +141,52 @@ mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K
 // the non-temporal variants (lhsT.rhs 3, lhs.rhs 2).
 mi_tile_cfg skinny_matmul_default(bool lhs, int M, int N, int K) {
   const int v_nt = lhs ? 2 : 3;
-  const mi_tile_cfg skinny = lhs ? mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt}
-                             : M <= 32 ? mi_tile_cfg{32, 128, 128, 4, 3, 1, 8, v_nt}
-                             : M <= 64 ? mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt}
-                                       : mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v_nt};
-  // A grid of the skinny block that fills the chip runs unsplit.
-  if (tiles_of(M, N, skinny.block_m, skinny.block_n) >= kFillTiles) return skinny;
-  mi_tile_cfg c = skinny;
   if (lhs) {
-    // lhs.rhs: the non-temporal block with the fewest wasted rows (64 x 128
-    // up to M = 64), split over K to up to one workgroup per CU.
-    if (M <= 64) c = {64, 128, 64, 4, 4, 1, 8, v_nt};
+    // lhs.rhs: the non-temporal 128 x 128 block when its grid fills the
+    // chip; otherwise the non-temporal block with the fewest wasted rows
+    // (64 x 128 up to M = 64), split over K to up to one workgroup per CU.
+    const mi_tile_cfg skinny = {128, 128, 64, 4, 3, 1, 8, v_nt};
+    if (tiles_of(M, N, skinny.block_m, skinny.block_n) >= kFillTiles) return skinny;
+    mi_tile_cfg c = M <= 64 ? mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt} : skinny;
     c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
     return c;
   }
-  // lhsT.rhs with a long K (8192 or more): 256-wide column blocks (512-byte
-  // weight row segments per workgroup) split over K, when that fills three
-  // quarters of the CUs or more with at least 16 K steps per part.
-  mi_tile_cfg wide = M <= 64 ? mi_tile_cfg{64, 256, 64, 4, 3, 1, 8, v_nt} : mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v_nt};
-  const long long wide_tiles = tiles_of(M, N, wide.block_m, wide.block_n);
-  wide.split_k = fill_parts(wide_tiles, K, wide.block_k);
-  if (K >= 8192 && wide_tiles * wide.split_k >= 3 * kCUs / 4 && (long long)K / wide.split_k >= 16LL * wide.block_k)
-    return wide;
-  // Otherwise the block with the most tiles up to one per CU (ties to the
-  // larger), split only when that grid still leaves CUs idle.
-  const mi_tile_cfg cands[] = {skinny, mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt},
-                               mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v_nt}};
-  long long most = 0;
+  // lhsT.rhs: a skinny launch is bound by each workgroup's own loads (its
+  // MFMA pipe is a quarter busy at most), so the estimate is the rounds of
+  // workgroups times one workgroup's panel bytes, (block_m + block_n) x its
+  // K range x 2, at 50 GB/s per CU plus 3 us, and a split pays its fp32
+  // partial products at 2 TB/s plus 8 us (the summing launch and the
+  // workspace).  Fitted to every block and split timed at 25 skinny shapes
+  // with the weight flushed (within 1.09 of the fastest at all of them).
+  // Equal estimates go to the earlier block (32 x 128 with block_k 64 and
+  // 4 stages measured faster than with block_k 128 and 3).
+  const mi_tile_cfg cands[] = {
+      {32, 128, 64, 4, 4, 1, 8, v_nt},  {32, 128, 128, 4, 3, 1, 8, v_nt}, {32, 256, 64, 4, 4, 1, 8, v_nt},
+      {64, 128, 64, 4, 4, 1, 8, v_nt},  {64, 64, 64, 4, 4, 1, 8, v_nt},   {64, 256, 64, 4, 3, 1, 8, v_nt},
+      {128, 128, 64, 4, 3, 1, 8, v_nt}, {128, 256, 32, 4, 3, 1, 8, v_nt}, {128, 256, 32, 4, 4, 1, 8, v_nt}};
+  // Blocks more than twice as tall as M are not considered; splits stop at
+  // 320 workgroups.
+  const int m_cap = 2 * (M > 32 ? M : 32);
+  mi_tile_cfg c = cands[0];
+  double best_t = 0.0;
+  bool found = false;
   for (const mi_tile_cfg& ci : cands) {
-    const long long t = tiles_of(M, N, ci.block_m, ci.block_n), capped = t < kCUs ? t : kCUs;
-    if (capped > most) {
-      most = capped;
-      c = ci;
+    if (ci.block_m > m_cap) continue;
+    const long long tiles = tiles_of(M, N, ci.block_m, ci.block_n), kt = ((long long)K + ci.block_k - 1) / ci.block_k;
+    for (int p = 1; p <= kMaxSplit; p *= 2) {
+      const long long kts = (kt + p - 1) / p, wgs = tiles * p;
+      if (p > 1 && (wgs > 320 || (long long)(p - 1) * kts >= kt)) break;
+      const double kp = (double)((K + p - 1) / p);
+      double t = (double)((wgs + kCUs - 1) / kCUs) * ((ci.block_m + ci.block_n) * kp * 2.0 / 50e3 + 3.0);
+      if (p > 1) t += (double)p * M * N * 8.0 / 2e6 + 8.0;
+      if (!found || t < best_t) {
+        found = true;
+        best_t = t;
+        c = ci;
+        c.split_k = p;
+      }
     }
   }
-  if (most < kFillTiles) c.split_k = fill_parts(most, K, c.block_k);
   return c;
 }
 
@@ -209,14 +220,25 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
 mi_tile_cfg fused_default(int M, int N, int K) {
   if (M <= 128 && K > 8192) {
     // Skinny M past K = 8192: the skinny variant 11 split into the fewest
-    // parts whose gamma fits (1..16 parts, none empty); past that the
+    // parts whose gamma fits (1..16 parts, none empty), or into more when
+    // that fills more CUs (up to one workgroup per CU); past 16 parts the
     // LDS-staged kernel (variant 0) takes any K.
+    const int bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
     const long long kt = (K + 63) / 64;
+    const int fill = fill_parts(tiles_of(M, N, bm, 128), K, 64);
     for (int p = 2; p <= 16; p *= 2) {
       const long long kts = (kt + p - 1) / p;
       const unsigned long long ws = (unsigned long long)p * ((unsigned long long)M * N + M) * 4ull;
-      if (kts * 64 <= 8192 && (long long)(p - 1) * kts < kt && ws <= kMaxWorkspace)
-        return {M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, p, 8, 11};
+      if (kts * 64 <= 8192 && (long long)(p - 1) * kts < kt && ws <= kMaxWorkspace) {
+        int parts = p;
+        // A larger split: still no empty part, and its workspace fits.
+        for (int q = p * 2; q <= fill; q *= 2) {
+          const long long qts = (kt + q - 1) / q;
+          const unsigned long long qws = (unsigned long long)q * ((unsigned long long)M * N + M) * 4ull;
+          if ((long long)(q - 1) * qts < kt && qws <= kMaxWorkspace) parts = q;
+        }
+        return {bm, 128, 64, 4, 3, parts, 8, 11};
+      }
     }
     return {64, 128, 64, 4, 2, 1, 8, 0};
   }

@@ -215,13 +215,15 @@ def test_library_default_is_legal_everywhere():
     ("matmul_lhsT_rhs", (2048, 1024, 8192), "bm64_bn128_bk64_w4_s4_v1"),
     ("matmul_lhsT_rhs", (512, 4096, 4096), "bm128_bn64_bk64_w4_s4_v1"),       # N >= 4M: 128 along M
     ("matmul_lhsT_rhs", (512, 512, 32768), "bm128_bn128_bk64_w4_s3_v1_k16"),  # few tiles, long K: the largest block a split fills the chip with
-    ("matmul_lhsT_rhs", (16, 28672, 8192), "bm32_bn128_bk128_w4_s3_v3"),      # skinny, weight streamed non-temporally
-    ("matmul_lhsT_rhs", (32, 14336, 4096), "bm64_bn64_bk64_w4_s4_v3"),        # skinny, short K: the most tiles
+    ("matmul_lhsT_rhs", (16, 28672, 8192), "bm32_bn128_bk64_w4_s4_v3"),       # skinny, weight streamed non-temporally
+    ("matmul_lhsT_rhs", (32, 14336, 4096), "bm64_bn64_bk64_w4_s4_v3"),        # skinny: least panel bytes per workgroup
     ("matmul_lhsT_rhs", (64, 4096, 4096), "bm64_bn64_bk64_w4_s4_v3_k4"),
-    ("matmul_lhsT_rhs", (16, 4096, 8192), "bm64_bn64_bk64_w4_s4_v3_k4"),     # long K, too few 256-wide K steps
-    ("matmul_lhsT_rhs", (32, 2048, 16384), "bm64_bn64_bk64_w4_s4_v3_k8"),    # long K, 256-wide grid too small
+    ("matmul_lhsT_rhs", (16, 4096, 8192), "bm32_bn128_bk64_w4_s4_v3_k8"),    # split to fill the CUs
+    ("matmul_lhsT_rhs", (32, 2048, 16384), "bm32_bn128_bk64_w4_s4_v3_k16"),
     ("matmul_lhsT_rhs", (64, 12288, 16384), "bm64_bn256_bk64_w4_s3_v3_k4"),
-    ("matmul_lhsT_rhs", (96, 8192, 8192), "bm128_bn256_bk32_w4_s3_v3_k8"),   # skinny, long K: 256-wide blocks split over K
+    ("matmul_lhsT_rhs", (96, 8192, 8192), "bm128_bn128_bk64_w4_s3_v3_k4"),
+    ("matmul_lhsT_rhs", (96, 4544, 16256), "bm128_bn256_bk32_w4_s3_v3_k8"),  # long K: 256-wide blocks split over K
+    ("matmul_lhsT_rhs", (16, 5440, 1216), "bm64_bn64_bk64_w4_s4_v3"),         # short K: no split
     ("rmsnorm_matmul", (4096, 4096, 4096), "bm128_bn512_bk32_w8_s3_v4"),
     ("rmsnorm_matmul", (4096, 2048, 4096), "bm128_bn256_bk32_w4_s3_v5"),
     ("rmsnorm_matmul", (512, 4096, 8192), "bm128_bn256_bk32_w4_s3_v5_k4"),
@@ -230,6 +232,7 @@ def test_library_default_is_legal_everywhere():
     ("rmsnorm_matmul", (128, 1024, 5248), "bm32_bn128_bk64_w4_s3_v11_k8"),
     ("rmsnorm_matmul", (768, 8064, 12992), "bm256_bn128_bk64_w4_s3_v13"),     # K > 8192: the estimate, 256 x 128 two-pass
     ("rmsnorm_matmul", (384, 4096, 16384), "bm128_bn512_bk32_w8_s3_v4_k8"),   # K > 8192: one-pass split until gamma fits
+    ("rmsnorm_matmul", (64, 4416, 14080), "bm64_bn128_bk64_w4_s3_v11_k4"),    # skinny past K = 8192: split to fill the CUs
     ("matmul_lhs_rhs", (48, 2880, 14912), "bm64_bn128_bk64_w4_s4_v2_k8"),     # skinny lhs: non-temporal 64 x 128, split
     ("rmsnorm_matmul", (2048, 2048, 2048), "bm128_bn128_bk64_w4_s2_v4"),
     ("rmsnorm_matmul", (256, 8192, 4096), "bm64_bn128_bk64_w4_s4_v13"),       # x scaled once, then the lhsT core
