@@ -46,6 +46,7 @@ def _rows(M: int) -> np.ndarray:
     ("matmul_lhsT_rhs", (16, 8192, 8192), "bm32_bn128_bk64_w4_s4_v3_k4"),
     ("matmul_lhsT_rhs", (32, 2048, 16384), "bm32_bn128_bk64_w4_s4_v3_k16"),
     ("matmul_lhsT_rhs", (640, 10240, 2048), "bm128_bn256_bk32_w4_s3_v1"),
+    ("matmul_lhsT_rhs", (8, 9344, 6336), "bm32_bn256_bk64_w4_s4_v3_k4"),
     ("matmul_lhs_rhs", (2048, 4096, 1024), "bm128_bn256_bk32_w4_s3_v1"),
     ("matmul_lhs_rhs", (512, 4096, 4096), "bm64_bn128_bk64_w4_s4"),
     ("matmul_lhs_rhs", (48, 2880, 14912), "bm64_bn128_bk64_w4_s4_v2_k8"),
