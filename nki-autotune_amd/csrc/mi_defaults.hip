@@ -219,11 +219,13 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
 // entries here).
 mi_tile_cfg fused_default(int M, int N, int K) {
   if (M <= 128 && K > 8192) {
-    // Skinny M past K = 8192: the skinny variant 11 split into the fewest
-    // parts whose gamma fits (1..16 parts, none empty), or into more when
-    // that fills more CUs (up to one workgroup per CU); past 16 parts the
-    // LDS-staged kernel (variant 0) takes any K.
-    const int bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
+    // Skinny M past K = 8192: the skinny variant 11 (64-row blocks when
+    // 128-row ones leave CUs idle) split into the fewest parts whose gamma
+    // fits (1..16 parts, none empty), or into more when that fills more CUs
+    // (up to one workgroup per CU); past 16 parts the LDS-staged kernel
+    // (variant 0) takes any K.
+    int bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
+    if (bm == 128 && tiles_of(M, N, 128, 128) < kFillTiles) bm = 64;
     const long long kt = (K + 63) / 64;
     const int fill = fill_parts(tiles_of(M, N, bm, 128), K, 64);
     for (int p = 2; p <= 16; p *= 2) {

@@ -233,6 +233,7 @@ def test_library_default_is_legal_everywhere():
     ("rmsnorm_matmul", (768, 8064, 12992), "bm256_bn128_bk64_w4_s3_v13"),     # K > 8192: the estimate, 256 x 128 two-pass
     ("rmsnorm_matmul", (384, 4096, 16384), "bm128_bn512_bk32_w8_s3_v4_k8"),   # K > 8192: one-pass split until gamma fits
     ("rmsnorm_matmul", (64, 4416, 14080), "bm64_bn128_bk64_w4_s3_v11_k4"),    # skinny past K = 8192: split to fill the CUs
+    ("rmsnorm_matmul", (128, 1792, 11008), "bm64_bn128_bk64_w4_s3_v11_k8"),   # and 64-row blocks before a split
     ("matmul_lhs_rhs", (48, 2880, 14912), "bm64_bn128_bk64_w4_s4_v2_k8"),     # skinny lhs: non-temporal 64 x 128, split
     ("rmsnorm_matmul", (2048, 2048, 2048), "bm128_bn128_bk64_w4_s2_v4"),
     ("rmsnorm_matmul", (256, 8192, 4096), "bm64_bn128_bk64_w4_s4_v13"),       # x scaled once, then the lhsT core
