@@ -753,8 +753,10 @@ DEFAULTS_RMS = [(4096, 4096, 4096), (2048, 8192, 2048), (8192, 4096, 4096), (102
 
 def random_default_shapes(seed: int = 2026, count: int = 30) -> list:
     """Shapes the default config was not fitted to: 14 lhsT.rhs, 6 lhs.rhs and 10 rmsnorm_matmul shapes,
-    drawn from a fixed seed.  A quarter are skinny (M from 8 to 128); the others have M of 256 to 8192, N of
-    512 to 14336 and K of 512 to 16384, in steps of 64, at most 5e11 FLOP each (so the sweep stays short)."""
+    drawn from a fixed seed.  Each draw is skinny (M from 8 to 128) with probability 1/4; the others have M of
+    256 to 8192, N of 512 to 14336 and K of 512 to 16384, in steps of 64.  A draw over 5e11 FLOP is redrawn (so
+    the sweep stays short), which leaves more skinny shapes than a quarter: 9, 9 and 17 of 30 for seeds 2026,
+    2027 and 2028."""
     import numpy as np
 
     rng = np.random.default_rng(seed)
