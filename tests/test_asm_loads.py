@@ -5,6 +5,7 @@ kernel code (no outlined calls, no scratch spills).  Needs hipcc, not a GPU."""
 
 from __future__ import annotations
 
+import os
 import shutil
 import subprocess
 import sys
@@ -26,24 +27,50 @@ def _hipcc():
     pytest.skip("hipcc not available")
 
 
+UNITS = ("mm_bf16_pipe.hip", "mm_bf16_kw.hip", "mm_bf16_lhs.hip", "mm_bf16_reg.hip", "rms_bf16_xreg.hip",
+         "rms_bf16_2pass.hip")
+
+
 @pytest.fixture(scope="module")
 def asm_of(tmp_path_factory):
-    """unit -> gfx950 assembly text, compiled once per module."""
+    """unit -> gfx950 assembly text, compiled once per module.
+
+    In a run without xdist workers every unit's compile starts at the first
+    request, all at once, so the module waits for the slowest unit rather
+    than for the sum of them; under xdist each worker compiles only what its
+    own tests ask for."""
     import build_lib
 
     cache: dict[str, str] = {}
+    running: dict[str, tuple[subprocess.Popen, object]] = {}
     tmp = tmp_path_factory.mktemp("asm")
+    flags = [f for f in build_lib.HIPCC_FLAGS if f != "-fPIC"]
+
+    def start(unit: str) -> None:
+        if unit in cache or unit in running:
+            return
+        out = tmp / (unit + ".s")
+        proc = subprocess.Popen([_hipcc(), *flags, f"-I{build_lib.INCLUDE}", "--cuda-device-only", "-S",
+                                 str(CSRC / unit), "-o", str(out)], stdout=subprocess.PIPE, stderr=subprocess.STDOUT)
+        running[unit] = (proc, out)
 
     def get(unit: str) -> str:
         if unit not in cache:
-            out = tmp / (unit + ".s")
-            flags = [f for f in build_lib.HIPCC_FLAGS if f != "-fPIC"]
-            subprocess.run([_hipcc(), *flags, f"-I{build_lib.INCLUDE}", "--cuda-device-only", "-S",
-                            str(CSRC / unit), "-o", str(out)], check=True, capture_output=True)
+            if not running and not os.environ.get("PYTEST_XDIST_WORKER"):
+                for u in UNITS:
+                    start(u)
+            start(unit)
+            proc, out = running.pop(unit)
+            log, _ = proc.communicate()
+            if proc.returncode != 0:
+                raise subprocess.CalledProcessError(proc.returncode, proc.args, log)
             cache[unit] = out.read_text()
         return cache[unit]
 
-    return get
+    yield get
+    for proc, _ in running.values():
+        proc.kill()
+        proc.wait()
 
 
 @pytest.mark.parametrize("unit", ["rms_bf16_xreg.hip"])
@@ -58,8 +85,7 @@ def test_async_register_loads_untouched_until_waited(unit, asm_of):
     assert total > 0
 
 
-@pytest.mark.parametrize("unit", ["mm_bf16_pipe.hip", "mm_bf16_kw.hip", "mm_bf16_lhs.hip", "mm_bf16_reg.hip",
-                                  "rms_bf16_xreg.hip", "rms_bf16_2pass.hip"])
+@pytest.mark.parametrize("unit", UNITS)
 def test_kernels_straight_line(unit, asm_of):
     """The unrolled tile lambdas are inlined: a device-function call would
     pass buffer descriptors in VGPRs and read captures through flat loads."""
