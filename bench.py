@@ -36,6 +36,12 @@ one launch of that kernel on inputs resident in HBM.
   kernel reading the engine-cycle and 100 MHz real-time counters around each
   workgroup: ``kernel_library._probe``), with the twin's launch time beside
   the product kernel's, and the share of the peak at that clock it reaches.
+  ``clock.settle`` records how the timed region's start was reached: the
+  kernel runs back to back until two successive twin readings agree within
+  1 % (settle()), so the short timed region measures the kernel at its
+  steady clock, not the clock's ramp after an idle gap.
+* ``sustained``: the same kernel over at least one second of back-to-back
+  launches after the timed region, with the twin's clock after it.
 * ``mfma_ceiling``: the rate of the MFMA work alone on the benchmark's data
   (operands from registers; then with the kernel's LDS operand reads), with
   no global traffic: what any kernel running those instructions reaches
@@ -250,19 +256,78 @@ def skinny_inputs(fam: str, m: int, dev):
     return upload(generate_tensors(specs, 0, dists), specs, dev)
 
 
-def settle(launch, idle_s: float) -> None:
-    """Idle ``idle_s`` seconds, then warm(launch): the state the timed region starts from.
+SETTLE_TOL = 0.01      # two successive clock readings this close: the clock has settled
+SETTLE_CAP_S = 6.0     # give up waiting for a steady clock after this much load
+SETTLE_STEP_S = 0.25   # back-to-back launches between two readings
+
+
+def settle(launch, idle_s: float, reading=None) -> dict:
+    """Bring the GPU to the steady clock of ``launch`` before a timed region; returns what it took.
 
     A long run of back-to-back GEMMs (the sweep before the timed region: ~10 s)
     drives the engine clock down under the power limit (the shipped config
-    timed 11 % slower right after the sweep than inside it); a GPU that has
-    been idle starts below its working clock.  The idle gap, then half a
-    second of the timed kernel itself, give the timed region the state a
-    short run of this kernel reaches -- the same state the profiling
-    commands (this script with --only-kernel, no sweep) measure."""
+    timed 11 % slower right after the sweep than inside it), and a GPU that
+    has been idle starts below its working clock and takes more than half a
+    second of load to reach it.  So: idle ``idle_s`` seconds, then run the
+    timed kernel back to back in steps of ``SETTLE_STEP_S`` seconds,
+    reading the engine clock after each step with ``reading`` (the kernel's
+    clocked twin, 10 launches), until two successive readings agree within
+    ``SETTLE_TOL`` -- or ``SETTLE_CAP_S`` seconds of load have passed.
+    Without a ``reading`` (no clocked twin for the kernel) it is half a
+    second of load."""
     if idle_s > 0:
         time.sleep(idle_s)
-    warm(launch)
+    t0 = time.perf_counter()
+    warm(launch, SETTLE_STEP_S)
+    readings: list[float] = []
+    steady = False
+    if reading is None:
+        warm(launch, 0.5 - SETTLE_STEP_S)
+    else:
+        while True:
+            r = reading()
+            if not r or "error" in r:
+                break
+            readings.append(r["clock_mhz"])
+            if len(readings) >= 2 and abs(readings[-1] - readings[-2]) <= SETTLE_TOL * readings[-1]:
+                steady = True
+                break
+            if time.perf_counter() - t0 >= SETTLE_CAP_S:
+                break
+            warm(launch, SETTLE_STEP_S)
+    return {"idle_s": idle_s, "load_s": round(time.perf_counter() - t0, 2), "readings_mhz": readings,
+            "steady": steady if reading is not None else None,
+            "rule": f"idle, then the timed kernel back to back; its clocked twin read every {SETTLE_STEP_S} s of "
+                    f"load until two successive readings agree within {100 * SETTLE_TOL:.0f} % "
+                    f"(at most {SETTLE_CAP_S} s)"}
+
+
+def sustained(launch, flop: float, reading=None, seconds: float = 1.0) -> dict:
+    """Throughput of at least ``seconds`` of back-to-back launches (HIP events around the whole run), then the
+    clock read by ``reading`` right after: the kernel under sustained load, beside the short timed region."""
+    import torch
+
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    n = 0
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(20):
+            launch()
+        n += 20
+        torch.cuda.synchronize()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    s = ev0.elapsed_time(ev1) * 1e-3
+    out = {"launches": n, "seconds": round(s, 3), "us_per_launch": round(s / n * 1e6, 1),
+           "tflops": round(flop * n / s / 1e12, 1), "pct_mfma_peak": round(100 * flop * n / s / 1e12 / PEAK_BF16_TFLOPS, 2)}
+    if reading is not None:
+        r = reading()
+        if r and "error" not in r:
+            out["clock_after_mhz"] = r["clock_mhz"]
+    return out
 
 
 def warm(launch, seconds: float = 0.5) -> None:
@@ -529,10 +594,12 @@ def main() -> int:
         def step():
             kl.rmsnorm_matmul(d["lhs"], d["rhs"], d["gamma"], cfg=cfg, out=out)
 
-    settle(step, args.settle_s)
+    clock_twin = fam == "matmul_lhsT_rhs" and not args.only_kernel
+    reading = (lambda: twin_clock(d, out, cfg)) if clock_twin else None
+    settled = settle(step, args.settle_s, reading)
+    log(f"settle: {settled}")
     for _ in range(args.warmup):
         step()
-    clock_twin = fam == "matmul_lhsT_rhs" and not args.only_kernel
     before = twin_clock(d, out, cfg) if clock_twin else None
     stream = torch.cuda.current_stream(dev)
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -587,7 +654,10 @@ def main() -> int:
     }
     if not args.only_kernel and fam == "matmul_lhsT_rhs":
         line["clock"] = clock_of(before, after, cfg, achieved)
+        line["clock"]["settle"] = settled
         log(f"clock: {line['clock']}")
+        line["sustained"] = sustained(step, flop, reading)
+        log(f"sustained: {line['sustained']}")
         line["mfma_ceiling"] = mfma_ceiling(d["lhs_T"])
         log(f"MFMA ceiling: {line['mfma_ceiling']}")
         line["vendor"] = vendor_matmul(d["lhs_T"], d["rhs"], kern_s)

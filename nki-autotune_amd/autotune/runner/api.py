@@ -128,6 +128,18 @@ def _trace_successes(cache_dir: str, kernels: dict[str, KernelJob], results, see
                                   job.input_specs, job.input_dists, seed, warmup, reps, flush_bytes)
         row = trace_kernel(variant_dir, replay)
         counters = collect_counters(variant_dir, replay)
-        results[i] = r._replace(profile_detailed={**(r.profile_detailed or {}), "rocprof": row, "counters": counters})
+        results[i] = r._replace(profile_detailed={**(r.profile_detailed or {}), "rocprof": row, "counters": counters},
+                                ntff_b64=trace_b64(row))
         logger.info("Traced %s: %s; counters %s", r.kernel_name, row.get("avg_ns", row.get("error")),
                     {k: counters.get(k) for k in ("mfma_busy_percent", "engine_clock_mhz", "hbm_gbps", "error")})
+
+
+def trace_b64(row: dict) -> str | None:
+    """Base64 of the replay's rocprofv3 kernel trace (one CSV row per dispatch), the NTFF's counterpart, or None."""
+    import base64
+
+    path = os.path.join(row.get("trace_dir") or "", "run_kernel_trace.csv")
+    if "error" in row or not row.get("trace_dir") or not os.path.exists(path):
+        return None
+    with open(path, "rb") as f:
+        return base64.b64encode(f.read()).decode("ascii")

@@ -168,13 +168,16 @@ def benchmark_one(kernel_name: str, library_path: str, func_name: str, cfg, inpu
 
     from kernel_library import _lib
 
-    summary = detailed = None
+    summary = detailed = neff_b64 = None
     dtype = out_spec.dtype
     hardware_output = f"{list(out_spec.shape)} {dtype}"
     try:
         library = _lib.load(library_path)
         dev = next(iter(inputs.values())).device
-        out = torch.empty(tuple(out_spec.shape), dtype=_torch_dtype(dtype), device=dev)
+        # NaN-filled, so that an output element the candidate never writes
+        # fails the numerics check instead of passing on a value an earlier
+        # candidate left in the same (recycled) allocation.
+        out = torch.full(tuple(out_spec.shape), float("nan"), dtype=_torch_dtype(dtype), device=dev)
         launch = Launcher(library, func_name, cfg, inputs, out, M, N, K)
         flush = None
         if flush_bytes:
@@ -207,10 +210,22 @@ def benchmark_one(kernel_name: str, library_path: str, func_name: str, cfg, inpu
             summary["numerics"] = numerics
         if collect_detailed_profile:
             detailed = {"times_s": times, "l2_flush_bytes": flush_bytes}
+            neff_b64 = code_object_b64(library_path, func_name, cfg)
     except Exception as exc:
         hardware_output = capture_error(exc)
-        summary = None
-    return ProfileResult(kernel_name, hardware_output, summary, detailed)
+        summary = detailed = neff_b64 = None
+    return ProfileResult(kernel_name, hardware_output, summary, detailed, neff_b64)
+
+
+def code_object_b64(library_path: str, func_name: str, cfg) -> str | None:
+    """Base64 of the gfx950 code object holding the instance (the NEFF's counterpart), or None."""
+    import base64
+
+    from autotune.runner.codeobj import code_object_of
+    from autotune.runner.compile import canonical_name
+
+    co = code_object_of(library_path, canonical_name(func_name), cfg)
+    return None if co is None else base64.b64encode(co).decode("ascii")
 
 
 def _torch_dtype(name: str):

@@ -42,6 +42,13 @@ FAILURE_CLASSES = (
     ("timeout", "timed out"),
     ("numerics_mismatch", "numerics check failed"),
 )
+# The reference's out-of-memory counters of results.json (output.py:225-239,
+# :265-266), kept under their names: SBUF is the on-chip scratchpad, whose
+# counterpart is LDS ("LDS over budget", the lds_over_budget class above);
+# PSUM holds the matmul accumulators, whose counterpart is a wave's
+# accumulator registers (the legality check's message for a wave tile whose
+# fp32 accumulators exceed its share of the SIMD's 512 registers).
+OOM_MARKS = (("sbuf_oom", "LDS over budget"), ("psum_oom", "exceed its share of the 512 registers"))
 
 
 class SuccessRow(NamedTuple):
@@ -235,6 +242,8 @@ class ResultsModel:
             "best_mbu": max(mbus, default=None),
             "worst_mbu": min(mbus, default=None),
             "success": len(self.ran),
+            **{key: sum(1 for k in self.records if not k.ok and mark in k.result.hardware_output)
+               for key, mark in OOM_MARKS},
             **counts,
         }
         doc = {"metadata": {"num_kernels": num_kernels, "wallclock_s": wallclock_s}, "metrics": metrics,

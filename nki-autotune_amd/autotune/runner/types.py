@@ -117,12 +117,25 @@ class ProfileResult(NamedTuple):
     ``hardware_output.startswith("[")``, as in the reference) or the error
     text.  ``profiler_summary`` holds the hipEvent timing summary;
     ``profile_detailed`` the optional per-rep timings and rocprofv3 kernel-trace row.
+
+    Filled only when the caller asks for a detailed profile, else None (as
+    in the reference):
+
+    * ``neff_b64``: the compiled artifact, base64 -- the gfx950 code object
+      (ELF) of the translation unit that defines the instance, read from
+      the library that holds it (:mod:`autotune.runner.codeobj`; the NEFF's
+      counterpart);
+    * ``ntff_b64``: the trace, base64 -- the rocprofv3 kernel trace
+      (``run_kernel_trace.csv``, one row per dispatch) of the instance's
+      replay, taken when the run has a cache dir (the NTFF's counterpart).
     """
 
     kernel_name: str
     hardware_output: str
     profiler_summary: dict | None = None
     profile_detailed: dict | None = None
+    neff_b64: str | None = None
+    ntff_b64: str | None = None
 
 
 class OutputSpec(NamedTuple):

@@ -124,6 +124,12 @@ def panel_stream(buf, region: int, waves: int, inflight: int, rounds: int, row_b
     """
     import torch
 
+    # The kernel's buffer descriptor spans `region` bytes from buf's start,
+    # so every load stays inside buf only if region fits in it.
+    if not buf.is_contiguous():
+        raise ValueError("panel_stream needs a contiguous buffer")
+    if region <= 0 or region > buf.numel() * buf.element_size():
+        raise ValueError(f"region of {region} bytes is outside the {buf.numel() * buf.element_size()}-byte buffer")
     clk = torch.zeros((launches + warmup, wgs, 2), dtype=torch.int64, device=buf.device)
     stream = torch.cuda.current_stream(buf.device)
     events = []

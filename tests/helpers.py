@@ -51,6 +51,46 @@ def rms_check(actual: np.ndarray, expected: np.ndarray) -> dict:
     return rep
 
 
+def rms_check_full(actual, expected) -> dict:
+    """``rms_check`` over a whole output on the GPU: ``actual`` a device
+    tensor, ``expected`` the float64 device tensor of the closed form on the
+    same bf16 inputs.  The figures are computed on the device in float64
+    with the definitions of ``oracle.metrics.report`` (max_abs, max_rel with
+    the atol floor, normwise, non-finite count, allclose), so every one of
+    the M*N outputs is compared without a host copy."""
+    import torch
+
+    a = actual.to(torch.float64)
+    e = expected.to(torch.float64)
+    if a.shape != e.shape:
+        raise ValueError(f"shape mismatch {tuple(a.shape)} vs {tuple(e.shape)}")
+    floor = RMS_ATOL_FRAC * (float(torch.sqrt(torch.mean(e * e))) if e.numel() else 1.0)
+    diff = (a - e).abs()
+    emax = float(e.abs().max()) if e.numel() else 0.0
+    finite = torch.isfinite(a)
+    rep = {
+        "elements": int(a.numel()),
+        "max_abs": float(diff.max()) if diff.numel() else 0.0,
+        "max_rel": float((diff / (e.abs() + floor)).max()) if diff.numel() else 0.0,
+        "normwise": float(diff.max() / emax) if diff.numel() and emax > 0 else 0.0,
+        "nonfinite": int((~finite).sum()),
+        "allclose": bool(finite.all() and (diff <= floor + RMS_RTOL * e.abs()).all()),
+        "atol_floor": floor,
+    }
+    rep["ok"] = rep["allclose"] and rep["nonfinite"] == 0
+    return rep
+
+
+def rms_closed_form_gpu(x, w, gamma=None, eps: float = 1e-6):
+    """float64 closed form (x * rsqrt(mean x^2 + eps) * gamma) @ W of bf16 device tensors, on the device
+    (reference kernel_library/rmsnorm_matmul/kernel_hand_online.py:5-8; eps :195, 1/K :213)."""
+    xd, wd = x.double(), w.double()
+    y = xd * (xd * xd).mean(dim=1, keepdim=True).add(eps).rsqrt()
+    if gamma is not None:
+        y = y * gamma.double()[None, :]
+    return y @ wd
+
+
 def mm_inputs(K: int, M: int, N: int, seed: int = 0, dist="uniform", dtype="bfloat16") -> dict:
     return oinputs.generate({"lhs_T": ((K, M), dtype), "rhs": ((K, N), dtype)}, seed,
                             {"lhs_T": dist, "rhs": dist})

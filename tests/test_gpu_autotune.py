@@ -76,6 +76,14 @@ def test_profile_sweep_selection_failures_and_traces(gpu, tmp_path):
         assert 0.5 * compulsory < c["hbm_bytes"] < 64 * compulsory, (c["hbm_bytes"], compulsory)
         assert times[r.kernel_name]["hbm_gbps_measured"] == pytest.approx(c["hbm_gbps"])
         assert "engine_clock_mhz" not in c and "note" in c     # 512^3 calls are too short to clock
+        # the compiled artifact and the trace, base64 (the reference's neff_b64 / ntff_b64)
+        import base64
+
+        co = base64.b64decode(r.neff_b64)
+        assert co[:4] == b"\x7fELF", stem
+        trace = base64.b64decode(r.ntff_b64).decode()
+        assert trace.splitlines()[0].count(",") > 3 and "mi::" in trace, trace[:300]
+    assert by[f"{illegal.name}.hip"].neff_b64 is None and by[f"{illegal.name}.hip"].ntff_b64 is None
 
     # the JIT-built library computes the same product
     specs = input_specs("matmul_lhsT_rhs", M, N, K)

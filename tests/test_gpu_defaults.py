@@ -78,6 +78,8 @@ def test_matmul_without_config(gpu, fam, shape, expect):
 @pytest.mark.parametrize("shape,expect", [
     ((256, 8192, 4096), "bm64_bn128_bk64_w4_s4_v13"),
     ((128, 4096, 4096), "bm64_bn128_bk64_w4_s3_v11_k4"),
+    ((256, 4096, 4096), "bm64_bn128_bk64_w4_s4_v13_k2"),
+    ((256, 2048, 2048), "bm64_bn128_bk64_w4_s4_v13_k4"),
     ((512, 4096, 8192), "bm128_bn256_bk32_w4_s3_v5_k4"),
     ((1024, 4096, 4096), "bm128_bn128_bk64_w4_s3_v13"),
     ((48, 5504, 704), "bm32_bn128_bk64_w4_s3_v11"),

@@ -11,7 +11,7 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-from helpers import rms_check, rms_inputs
+from helpers import rms_check, rms_check_full, rms_closed_form_gpu, rms_inputs
 from oracle import rmsnorm as orms
 
 pytestmark = pytest.mark.gpu
@@ -116,12 +116,18 @@ def test_scale_invariance_and_identity_weight(gpu):
 
 def test_baseline_c3_full_size(gpu):
     """Benchmark config C3 (M=K=N=4096, gamma, eps=1e-6), every variant family
-    and the configs the C3 sweep ships: sampled rows vs the closed form."""
+    and the configs the C3 sweep ships (the one-pass bm128_bn512_bk32_w8_s3_v4,
+    the two-pass v13 blocks, the library default): all 16.7 M outputs against
+    a float64 evaluation of the closed form on the GPU, and sampled rows
+    against the CPU oracle."""
+    import torch
+
     import kernel_library as kl
 
     print("C3 4096^3 rmsnorm_matmul", flush=True)
     d = rms_inputs(4096, 4096, 4096, seed=0)
     x, g, w = _dev(d["lhs"], gpu), _dev(d["gamma"], gpu), _dev(d["rhs"], gpu)
+    exp_full = rms_closed_form_gpu(x, w, g)
     rng = np.random.default_rng(7)
     rows = np.unique(np.concatenate([[0, 4095], rng.integers(0, 4096, size=24)]))
     expected = orms.closed_form(d["lhs"][rows], d["rhs"], d["gamma"])
@@ -133,9 +139,13 @@ def test_baseline_c3_full_size(gpu):
             kl.TileConfig(128, 512, 32, 8, 3, variant=13), kl.TileConfig(256, 256, 32, 8, 3, variant=13),
             kl.default_config("rmsnorm_matmul", 4096, 4096, 4096)]
     for cfg in cfgs:
-        out = _host(kl.rmsnorm_matmul(x, w, g, cfg=cfg))
-        rep = rms_check(out[rows], expected)
-        print(cfg.name, rep, flush=True)
+        out_dev = torch.full((4096, 4096), float("nan"), dtype=torch.bfloat16, device=gpu)
+        kl.rmsnorm_matmul(x, w, g, cfg=cfg, out=out_dev)
+        full = rms_check_full(out_dev, exp_full)
+        print(cfg.name, "all outputs vs float64 on the GPU:", full, flush=True)
+        assert full["ok"], (cfg, full)
+        rep = rms_check(_host(out_dev)[rows], expected)
+        print(cfg.name, "sampled rows vs oracle:", rep, flush=True)
         assert _ok(rep), (cfg, rep)
 
 
@@ -167,8 +177,13 @@ def test_error_within_reference_bf16_semantics(gpu, shape, with_gamma):
     cfgs = shipped + [kl.TileConfig(256, 256, 32, 4, 3, variant=13)]
     if with_gamma:
         cfgs.append(kl.default_config("rmsnorm_matmul", M, N, K))
+    exp_full = rms_closed_form_gpu(x, w, g)
     for cfg in cfgs:
-        out = _host(kl.rmsnorm_matmul(x, w, g, cfg=cfg))[rows]
+        out_dev = kl.rmsnorm_matmul(x, w, g, cfg=cfg)
+        full = rms_check_full(out_dev, exp_full)
+        print(cfg.name, "all outputs vs float64 on the GPU:", full, flush=True)
+        assert full["ok"], (cfg, full)
+        out = _host(out_dev)[rows]
         rep = rms_check(out, closed)
         err = float(np.max(np.abs(out.astype(np.float64) - closed)))
         print(cfg.name, f"max|hip-closed| {err:.4g}  max|reference bf16 - closed| {ref_err:.4g}  "

@@ -79,6 +79,63 @@ def test_selection_metrics_and_failure_classes(tmp_path):
     assert (m["success"], m["lds_over_budget"], m["illegal_config"], m["compile_error"], m["timeout"]) == (2, 1, 1, 1, 1)
 
 
+def test_reference_result_fields_and_oom_metric_keys(tmp_path):
+    """A caller of the reference builds ProfileResult with all six of its
+    keyword arguments (reference types.py:70-98) and reads results.json's
+    out-of-memory counters (output.py:225-239, :265-266): here LDS over
+    budget (SBUF) and accumulator registers over budget (PSUM)."""
+    full = ProfileResult(kernel_name="a.hip", hardware_output="[8, 8] bfloat16",
+                         profiler_summary={"total_time": 1e-3, "mfu_estimated_percent": 0.5},
+                         profile_detailed={"times_s": [1e-3]}, neff_b64="AAAA", ntff_b64="QkJC")
+    assert (full.neff_b64, full.ntff_b64) == ("AAAA", "QkJC")
+    bare = ProfileResult("b.hip", "[8, 8] bfloat16")
+    assert bare.profiler_summary is None and bare.neff_b64 is None and bare.ntff_b64 is None
+    results = [full,
+               ProfileResult("c.hip", "illegal config x at M=8 N=8 K=8: [LDS over budget] LDS 262144 bytes"),
+               ProfileResult("d.hip", "illegal config y at M=8 N=8 K=8: [wave tile smaller than one MFMA tile] "
+                                      "each wave's accumulators exceed its share of the 512 registers"),
+               ProfileResult("e.hip", "Traceback ...\nRuntimeError: boom")]
+    write_results_json(str(tmp_path), len(results), results, 1.0)
+    m = json.loads((tmp_path / "results.json").read_text())["metrics"]
+    assert (m["success"], m["sbuf_oom"], m["psum_oom"]) == (1, 1, 1)
+    for key in ("best_total_time_s", "worst_total_time_s", "best_kernel", "worst_kernel", "best_mfu", "worst_mfu",
+                "best_mbu", "worst_mbu"):
+        assert key in m
+    # The real legality message of an over-budget wave tile carries the PSUM mark.
+    import ctypes
+
+    c = TileConfig(256, 256, 32, 1, 2, variant=1).to_c()
+    rc = _lib.lib().mi_cfg_check(0, ctypes.byref(c), 512, 512, 512)
+    msg = _lib.last_error()
+    assert rc == _lib.MI_E_WAVE_TILE and "exceed its share of the 512 registers" in msg, (rc, msg)
+
+
+def test_code_object_of_prebuilt_instances():
+    """neff_b64's artifact: the gfx950 code object (an ELF) of the library's
+    offload bundle that defines the instance's kernel, found by its mangled
+    template name and tile parameters; None for a config the library lacks."""
+    import base64
+
+    from autotune.runner import codeobj
+    from autotune.runner.benchmark import code_object_b64
+
+    lib = str(_lib.LIB_PATH)
+    seen = set()
+    for fam, name in (("matmul_lhsT_rhs", "bm256_bn256_bk32_w4_s3_v1"), ("matmul_lhsT_rhs", "bm32_bn128_bk128_w4_s3_v3"),
+                      ("rmsnorm_matmul", "bm128_bn512_bk32_w8_s3_v4"), ("rmsnorm_matmul", "bm256_bn256_bk32_w4_s3_v13"),
+                      ("matmul_lhs_rhs", "bm128_bn128_bk64_w4_s3"), ("matmul_lhsT_rhs_f32", "bm64_bn64_bk16_w4_s1")):
+        cfg = TileConfig.from_name(name)
+        co = codeobj.code_object_of(lib, fam, cfg)
+        assert co is not None and co[:4] == b"\x7fELF", (fam, name)
+        assert codeobj.mangled_stem(fam, cfg) in co
+        seen.add(hash(co))
+        assert base64.b64decode(code_object_b64(lib, fam, cfg)) == co
+    assert len(seen) >= 4                      # different translation units, different code objects
+    assert codeobj.code_object_of(lib, "matmul_lhsT_rhs", TileConfig(512, 512, 32, 4, 3, variant=1)) is None
+    assert codeobj.mangled_stem("matmul_lhsT_rhs", TileConfig(256, 256, 32, 4, 3, variant=1)) == \
+        b"28mm_lhsT_rhs_bf16_pipe_kernelILi256ELi256ELi32ELi4ELi3E"
+
+
 def test_profiler_percent_contract():
     assert profiler_percent({"x": 0.5}, "x") == 50.0
     assert profiler_percent({"x": -1.0}, "x") is None       # negative sentinel
