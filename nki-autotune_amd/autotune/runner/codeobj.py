@@ -32,6 +32,8 @@ _TEMPLATES = {
     ("matmul_lhsT_rhs", 2): ("mm_lhsT_rhs_bf16_reg_kernel", 5),
     ("matmul_lhsT_rhs", 3): ("mm_lhsT_rhs_bf16_pipe_kernel", 5),
     ("matmul_lhsT_rhs", 4): ("mm_lhsT_rhs_bf16_kw_kernel", 5),
+    ("matmul_lhsT_rhs", 5): ("mm_lhsT_rhs_bf16_sk_kernel", 5),
+    ("matmul_lhsT_rhs", 6): ("mm_lhsT_rhs_bf16_sk_kernel", 5),
     ("matmul_lhs_rhs", 0): ("mm_lhs_rhs_bf16_pipe_kernel", 5),
     ("matmul_lhs_rhs", 1): ("mm_lhs_rhs_bf16_pair_kernel", 5),
     ("matmul_lhs_rhs", 2): ("mm_lhs_rhs_bf16_pipe_kernel", 5),

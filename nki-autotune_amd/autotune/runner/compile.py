@@ -53,7 +53,7 @@ def _instance(fam: str, cfg) -> tuple[str, str, str] | None:
     bm, bn, bk, w, s, v = cfg.block_m, cfg.block_n, cfg.block_k, cfg.waves, cfg.lds_stages, int(cfg.variant)
     base = f"{bm}, {bn}, {bk}, {w}"
     if fam == "matmul_lhsT_rhs":
-        macro = {0: "MI_MM", 1: "MI_MMP", 2: "MI_MMR", 3: "MI_MMPN", 4: "MI_MMW"}.get(v)
+        macro = {0: "MI_MM", 1: "MI_MMP", 2: "MI_MMR", 3: "MI_MMPN", 4: "MI_MMW", 5: "MI_MMS", 6: "MI_MMSN"}.get(v)
         return (f"{macro}_INST", f"{macro}_ROW", f"{base}, {s}") if macro else None
     if fam == "matmul_lhs_rhs":
         macro = {0: "MI_MMK", 1: "MI_MMKP", 2: "MI_MMKN"}.get(v)

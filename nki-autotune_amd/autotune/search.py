@@ -52,7 +52,7 @@ class Atom(NamedTuple):
 
 # Variants of each family that compute the same function (include/mi_kernels.h).
 FAMILY_VARIANTS = {
-    "matmul_lhsT_rhs": (0, 1, 2, 3, 4),
+    "matmul_lhsT_rhs": (0, 1, 2, 3, 4, 5, 6),
     "matmul_lhs_rhs": (0, 1, 2),
     "rmsnorm_matmul": (0, 1, 4, 5, 11, 12, 13),
     "matmul_lhsT_rhs_f32": (0,),

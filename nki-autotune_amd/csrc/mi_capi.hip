@@ -75,6 +75,27 @@ const MiEntry* find(int kernel_id, const mi_tile_cfg& cfg) {
   return nullptr;
 }
 
+int device_cus() {
+  static std::mutex mu;
+  static std::map<int, int> cus;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();  // no device (a CPU-only host): leave no error behind for a later launch check
+    return kDefaultCus;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cus.find(dev);
+  if (it == cus.end()) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+      (void)hipGetLastError();
+      n = kDefaultCus;
+    }
+    it = cus.emplace(dev, n).first;
+  }
+  return it->second;
+}
+
 bool splittable(int kernel_id, int variant) {
   return (kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (variant == 1 || variant == 3 || variant == 4)) ||
          (kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16 && (variant == 0 || variant == 2)) ||
@@ -105,6 +126,7 @@ mi::Legal template_legal(int kernel_id, const mi_tile_cfg& c) {
       if (c.variant == 1 || c.variant == 3) return mi::legal_mm_pipe(bm, bn, bk, w, s, false);
       if (c.variant == 2) return mi::legal_mm_reg(bm, bn, bk, w, s);
       if (c.variant == 4) return mi::legal_mm_kw(bm, bn, bk, w, s);
+      if (c.variant == 5 || c.variant == 6) return mi::legal_mm_pipe(bm, bn, bk, w, s, false);
       break;
     case MI_KERNEL_MATMUL_LHS_RHS_BF16:
       if (c.variant == 0 || c.variant == 2) return mi::legal_mm_pipe(bm, bn, bk, w, s, true);
@@ -156,7 +178,10 @@ int check(int kernel_id, const mi_tile_cfg* cfg, int M, int N, int K, const mi::
   if (lg.code != MI_OK)
     return fail(lg.code, "kernel %d variant %d bm=%d bn=%d bk=%d waves=%d stages=%d: %s", kernel_id, c.variant,
                 c.block_m, c.block_n, c.block_k, c.waves, c.lds_stages, lg.why);
-  const size_t ws = mi::workspace_bytes(kernel_id, c, M, N, K);
+  if (mi::is_streamk(kernel_id, c.variant) && mi::grid_tiles(M, N, c.block_m, c.block_n) > mi::kSkMaxTiles)
+    return fail(MI_E_RANGE, "stream-K takes at most %d output tiles (%d x %d blocks at M=%d N=%d)", mi::kSkMaxTiles,
+                c.block_m, c.block_n, M, N);
+  const size_t ws = mi::workspace_bytes(kernel_id, c, M, N, K, mi::capi::device_cus());
   if (ws > kMaxWorkspace) return fail(MI_E_RANGE, "device workspace of %zu bytes exceeds %llu", ws, kMaxWorkspace);
   const mi::MiEntry* e = find(kernel_id, c);
   if (!e)
@@ -220,17 +245,16 @@ int zero_output(void* out, size_t n, void* stream) {
 }
 
 // Device workspace (split-K partial products, the two-pass fused kernel's
-// packed operand): allocated per call, stream-ordered (hipMallocFromPoolAsync
-// / hipFreeAsync), from a memory pool the library keeps per device.  The
-// runtime hands a call's freed workspace back to the pool at the pool's
-// next allocation (measured: not at a synchronisation), and the pool's
-// release threshold, kPoolKeepBytes, then returns what it holds beyond that
-// to the device.  So between calls the library holds up to the last
-// workspace call's buffer plus kPoolKeepBytes; mi_release_workspace returns
-// all of it.
-// Each call has its own buffer (calls on different streams do not share
-// one), and a call under HIP graph capture becomes allocation and free
-// nodes of the graph.
+// packed operand, stream-K partial tiles): from a memory pool the library
+// keeps per device, stream-ordered (hipMallocFromPoolAsync / hipFreeAsync).
+// Outside graph capture a workspace of at most kKeepBytes is a buffer kept
+// per stream (run_kept below); otherwise each call allocates its own and
+// frees it after its launches, and under HIP graph capture those become
+// allocation and free nodes of the graph.  The runtime hands a freed
+// buffer back to the pool at the pool's next allocation (measured: not at
+// a synchronisation), and the pool's release threshold, kPoolKeepBytes,
+// then returns what it holds beyond that to the device.
+// mi_release_workspace returns all of it.
 constexpr uint64_t kPoolKeepBytes = 256ull << 20;
 std::mutex g_pool_mu;
 std::map<int, hipMemPool_t> g_pools;
@@ -266,42 +290,143 @@ int resolve(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& a, mi_ti
   return check(kernel_id, cfg, a.M, a.N, a.K, e);
 }
 
-int launch(const mi::MiEntry* e, const mi_tile_cfg& cfg, const mi::MiArgs& args_in, char* ws, void* stream) {
+int launch(const mi::MiEntry* e, const mi_tile_cfg& cfg, const mi::MiArgs& args_in, char* ws, bool ws_zeroed,
+           void* stream) {
   mi::MiArgs a = args_in;
   a.group_m = cfg.group_m > 0 ? cfg.group_m : 8;
   a.parts = cfg.split_k;
   a.ws = ws;
+  a.ws_zeroed = ws_zeroed;
   const hipError_t err = e->launch(a, (hipStream_t)stream);
   return err == hipSuccess ? MI_OK : hip_fail(err, "kernel launch");
 }
 
-// fixed_ws != NULL: the caller's device buffer of fixed_cap bytes serves as
-// the workspace (nothing is allocated; a larger need is rejected).
-int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, void* stream, char* fixed_ws = nullptr,
-        size_t fixed_cap = 0) {
-  mi_tile_cfg cfg;
-  const mi::MiEntry* e = nullptr;
-  const int rc = resolve(kernel_id, cfg_in, args_in, &cfg, &e);
-  if (rc != MI_OK) return rc;
-  const size_t ws_bytes = mi::workspace_bytes(kernel_id, cfg, args_in.M, args_in.N, args_in.K);
-  if (ws_bytes == 0) return launch(e, cfg, args_in, nullptr, stream);
-  if (fixed_ws) {
-    if (ws_bytes > fixed_cap)
-      return fail(MI_E_RANGE, "the config needs %zu bytes of workspace, over the %zu-byte static scratch", ws_bytes,
-                  fixed_cap);
-    return launch(e, cfg, args_in, fixed_ws, stream);
-  }
-  hipMemPool_t pool = nullptr;
-  const int prc = workspace_pool(&pool);
-  if (prc != MI_OK) return prc;
+// A workspace of its own for one call, allocated and freed stream-ordered
+// from the pool (under HIP graph capture these become allocation and free
+// nodes of the graph).
+int run_pooled(const mi::MiEntry* e, const mi_tile_cfg& cfg, const mi::MiArgs& a, size_t ws_bytes, hipMemPool_t pool,
+               void* stream) {
   char* ws = nullptr;
   const hipError_t ae = hipMallocFromPoolAsync((void**)&ws, ws_bytes, pool, (hipStream_t)stream);
   if (ae != hipSuccess) return hip_fail(ae, "workspace alloc");
-  const int lrc = launch(e, cfg, args_in, ws, stream);
+  const int lrc = launch(e, cfg, a, ws, false, stream);
   const hipError_t fe = hipFreeAsync(ws, (hipStream_t)stream);
   if (lrc != MI_OK) return lrc;
   if (fe != hipSuccess) return hip_fail(fe, "workspace free");
   return MI_OK;
+}
+
+// Kept workspaces: outside HIP graph capture, a call that needs at most
+// kKeepBytes of workspace reuses a buffer the library keeps for its
+// (device, stream), at most kKeepStreams streams per device; other
+// streams' calls take a buffer of their own from the pool.  Calls on one
+// stream run in stream order, so the buffer is free for the next call once
+// the last one's kernels end, and a call that needs more frees it and
+// allocates a larger one, both stream-ordered.  A stream that can be
+// destroyed (any but the null and per-thread default streams) could leave
+// kernels running on its buffer while a new stream gets the same handle,
+// so its buffer carries an event recorded after each use, which the next
+// call's stream waits for before touching the buffer (a wait costs nothing
+// measurable; recording the event costs the GPU about 2.5 us per call).
+// The default streams skip both.  This saves the pool allocation and free
+// of every call (about 7 us of host time).  A kept buffer's stream-K
+// counters (its first kSkCounterBytes) are zeroed by its first stream-K
+// launch, and every stream-K launch leaves them 0, so later ones skip the
+// zeroing.  Buffers stay with their stream until mi_release_workspace
+// returns them all.
+constexpr size_t kKeepBytes = 64ull << 20;
+constexpr int kKeepStreams = 4;
+
+struct KeptWs {
+  int dev;
+  hipStream_t stream;
+  char* ptr;
+  size_t bytes;
+  hipEvent_t done;  // null for a default stream
+  bool zeroed;
+};
+std::vector<KeptWs> g_kept;  // guarded by g_pool_mu
+
+int run_kept(const mi::MiEntry* e, const mi_tile_cfg& cfg, const mi::MiArgs& a, size_t ws_bytes, int kernel_id,
+             hipMemPool_t pool, int dev, void* stream_v) {
+  hipStream_t stream = (hipStream_t)stream_v;
+  std::unique_lock<std::mutex> lock(g_pool_mu);
+  KeptWs* k = nullptr;
+  int held = 0;
+  for (KeptWs& x : g_kept) {
+    if (x.dev != dev) continue;
+    ++held;
+    if (x.stream == stream) k = &x;
+  }
+  hipError_t err;
+  if (!k) {
+    if (held >= kKeepStreams) {
+      lock.unlock();
+      return run_pooled(e, cfg, a, ws_bytes, pool, stream);
+    }
+    hipEvent_t ev = nullptr;
+    const bool permanent = stream == nullptr || stream == hipStreamPerThread;
+    if (!permanent && (err = hipEventCreateWithFlags(&ev, hipEventDisableTiming)) != hipSuccess)
+      return hip_fail(err, "workspace event");
+    g_kept.push_back(KeptWs{dev, stream, nullptr, 0, ev, false});
+    k = &g_kept.back();
+  } else if (k->done && (err = hipStreamWaitEvent(stream, k->done, 0)) != hipSuccess) {
+    return hip_fail(err, "workspace wait");
+  }
+  if (k->bytes < ws_bytes) {
+    if (k->ptr && (err = hipFreeAsync(k->ptr, stream)) != hipSuccess) return hip_fail(err, "workspace free");
+    k->ptr = nullptr;
+    k->bytes = 0;
+    // Round up (to 1 MiB, at least 1/4 more) so that growing shapes reallocate rarely.
+    size_t want = ws_bytes + ws_bytes / 4;
+    want = (want + (1u << 20) - 1) / (1u << 20) * (1u << 20);
+    if (want > kKeepBytes) want = kKeepBytes;
+    if ((err = hipMallocFromPoolAsync((void**)&k->ptr, want, pool, stream)) != hipSuccess) {
+      k->ptr = nullptr;
+      return hip_fail(err, "workspace alloc");
+    }
+    k->bytes = want;
+    k->zeroed = false;
+  }
+  const int lrc = launch(e, cfg, a, k->ptr, k->zeroed, stream);
+  if (lrc == MI_OK && mi::is_streamk(kernel_id, cfg.variant)) k->zeroed = true;
+  if (k->done && (err = hipEventRecord(k->done, stream)) != hipSuccess && lrc == MI_OK)
+    return hip_fail(err, "workspace event");
+  return lrc;
+}
+
+// fixed_ws != NULL: the caller's device buffer of fixed_cap bytes serves as
+// the workspace (nothing is allocated; a larger need is rejected); its
+// stream-K counters must be 0 (a static array, zero when loaded; every
+// stream-K launch leaves them 0).
+int run(int kernel_id, const mi_tile_cfg* cfg_in, const mi::MiArgs& args_in, void* stream, char* fixed_ws = nullptr,
+        size_t fixed_cap = 0) {
+  mi_tile_cfg cfg;
+  const mi::MiEntry* e = nullptr;
+  int rc = resolve(kernel_id, cfg_in, args_in, &cfg, &e);
+  if (rc != MI_OK) return rc;
+  mi::MiArgs a = args_in;
+  a.cus = mi::capi::device_cus();
+  const size_t ws_bytes = mi::workspace_bytes(kernel_id, cfg, a.M, a.N, a.K, a.cus);
+  if (ws_bytes == 0) return launch(e, cfg, a, nullptr, false, stream);
+  if (fixed_ws) {
+    if (ws_bytes > fixed_cap)
+      return fail(MI_E_RANGE, "the config needs %zu bytes of workspace, over the %zu-byte static scratch", ws_bytes,
+                  fixed_cap);
+    return launch(e, cfg, a, fixed_ws, true, stream);
+  }
+  hipMemPool_t pool = nullptr;
+  if ((rc = workspace_pool(&pool)) != MI_OK) return rc;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t err = hipStreamIsCapturing((hipStream_t)stream, &cap);
+  if (err != hipSuccess) return hip_fail(err, "hipStreamIsCapturing");
+  if (cap == hipStreamCaptureStatusNone && ws_bytes <= kKeepBytes) {
+    int dev = 0;
+    if ((err = hipGetDevice(&dev)) != hipSuccess) return hip_fail(err, "hipGetDevice");
+    return run_kept(e, cfg, a, ws_bytes, kernel_id, pool, dev, stream);
+  }
+  // Under capture, or a large workspace: a buffer of its own.
+  return run_pooled(e, cfg, a, ws_bytes, pool, stream);
 }
 
 // Device pointers are read and written in 16-byte vectors (bf16 kernels)
@@ -456,6 +581,21 @@ int mi_release_workspace(void) {
   hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
   int rc = MI_OK;
+  // The kept buffers first, once every stream's work on the device is done.
+  for (KeptWs& k : g_kept) {
+    if ((e = hipSetDevice(k.dev)) != hipSuccess || (e = hipDeviceSynchronize()) != hipSuccess ||
+        (k.ptr && (e = hipFreeAsync(k.ptr, nullptr)) != hipSuccess) ||
+        (k.done && (e = hipEventDestroy(k.done)) != hipSuccess)) {
+      rc = hip_fail(e, "releasing a kept workspace");
+      break;
+    }
+    k.ptr = nullptr;
+  }
+  if (rc != MI_OK) {
+    (void)hipSetDevice(cur);
+    return rc;
+  }
+  g_kept.clear();
   for (const auto& kv : g_pools) {
     // The runtime hands memory freed by hipFreeAsync back to its pool at the
     // pool's next allocation, not at a synchronisation: one small

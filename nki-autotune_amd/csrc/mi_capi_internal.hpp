@@ -20,6 +20,11 @@ int fail(int code, const char* fmt, ...);
 // variant (split_k and group_m aside), or NULL.
 const MiEntry* find(int kernel_id, const mi_tile_cfg& cfg);
 
+// Compute units of the current device (the stream-K grid); kDefaultCus,
+// MI355X's count, when no device is visible.
+constexpr int kDefaultCus = 256;
+int device_cus();
+
 // Whether `variant` of `kernel_id` takes split_k > 1.
 bool splittable(int kernel_id, int variant);
 

@@ -114,7 +114,7 @@ mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K
     // allocate, is out.
     c.split_k = gamma_fit_parts(c, K);
     if (c.split_k == 0) continue;
-    if (mi::workspace_bytes(MI_KERNEL_RMSNORM_MATMUL_BF16, c, M, N, K) > kMaxWorkspace) continue;
+    if (mi::workspace_bytes(MI_KERNEL_RMSNORM_MATMUL_BF16, c, M, N, K, kDefaultCus) > kMaxWorkspace) continue;
     const long long wgs = tiles * c.split_k, rounds = (wgs + kCUs - 1) / kCUs;
     const double kp = (double)((K + c.split_k - 1) / c.split_k);
     double t = (double)rounds * c.block_m * c.block_n * kp / (cands[i].rate * R0) * 1e6;

@@ -29,6 +29,7 @@
 #include <utility>
 
 #include "mi_legal.hpp"
+#include "mi_streamk.hpp"
 
 namespace mi {
 
@@ -159,6 +160,12 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int group_
 struct SplitK {
   int parts;          // 1: no split
   float* ws;          // fp32 partial products, [parts][M][N]
+};
+
+// One segment of a stream-K workgroup (mi_streamk.hpp): K tiles
+// [kt0, kt0 + kts) of output tile (tm, tn).
+struct SegK {
+  int tm, tn, kt0, kts;
 };
 
 // Epilogue row scale of the two-pass fused kernel: output row m is
@@ -671,12 +678,19 @@ __global__ __launch_bounds__(256) void splitk_sum_kernel(const float* __restrict
   }
 }
 
+struct NoEpi {};
+
+// SK (stream-K): the tile and its K range come from `seg`, and instead of an
+// epilogue of its own the body hands its accumulators to
+// epi(acc, row0, col0) (row0, col0: this wave's first output row and
+// column), after the main loop's final barrier.
 template <int BM, int BN, int BK, int WAVES, int STAGES, bool AK, bool NTB = false, bool SPLIT = false,
-          bool RS = false, bool KW = false>
+          bool RS = false, bool KW = false, bool SK = false, class Epi = NoEpi>
 __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, const uint16_t* __restrict__ rhs,
                                              uint16_t* __restrict__ out, int M, int N, int K, int group_m,
                                              char* smem, const SplitK sk = SplitK{1, nullptr},
-                                             const RowScale rsc = RowScale{nullptr, 0, 0.0f, 0.0f}) {
+                                             const RowScale rsc = RowScale{nullptr, 0, 0.0f, 0.0f},
+                                             const SegK seg = SegK{0, 0, 0, 0}, Epi&& epi = Epi{}) {
   using C = PipeCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
   static_assert(KW ? legal_mm_kw(BM, BN, BK, WAVES, STAGES).code == MI_OK
@@ -685,6 +699,7 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   static_assert(C::LDS_BYTES == lds_mm_pipe(BM, BN, BK, WAVES, STAGES), "host LDS budget out of step");
   static_assert(KW || G::ok, "illegal wave grid");
   static_assert(!KW || (!AK && !RS), "K split over the waves: lhsT operand, no row scale");
+  static_assert(!SK || (!KW && !RS && !SPLIT), "stream-K: the plain wave-grid core");
   static_assert(BK % 32 == 0, "BK must be a multiple of 32 (even number of MFMA K steps)");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
   // KW: every wave covers the whole block (TM x TN MFMA tiles) over its own
@@ -704,8 +719,14 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
   int tmi, tni, part = 0;
-  if constexpr (SPLIT) tile_coords_split(tiles_m, tiles_n, group_m, sk.parts, tmi, tni, part);
-  else tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
+  if constexpr (SK) {
+    tmi = seg.tm;
+    tni = seg.tn;
+  } else if constexpr (SPLIT) {
+    tile_coords_split(tiles_m, tiles_n, group_m, sk.parts, tmi, tni, part);
+  } else {
+    tile_coords(tiles_m, tiles_n, group_m, tmi, tni);
+  }
   const int m0 = tmi * BM, n0 = tni * BN;
   const int wm0 = KW ? 0 : (wave / G::WN) * G::WTM;
   const int wn0 = KW ? 0 : (wave % G::WN) * G::WTN;
@@ -720,6 +741,12 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
     a += AK ? (size_t)k0 : (size_t)k0 * (size_t)M;
     rhs += (size_t)k0 * (size_t)N;
     K = K - k0 < kts * BK ? K - k0 : kts * BK;
+  } else if constexpr (SK) {
+    // The segment's K tiles (the host grid keeps every segment non-empty).
+    k0 = seg.kt0 * BK;
+    a += AK ? (size_t)k0 : (size_t)k0 * (size_t)M;
+    rhs += (size_t)k0 * (size_t)N;
+    K = K - k0 < seg.kts * BK ? K - k0 : seg.kts * BK;
   }
 
   // Bytes from the (part's) base to the end of the A buffer.
@@ -938,6 +965,10 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
     store_partial<TM, TN>(acc, sk.ws + (size_t)part * (size_t)M * (size_t)N, lane, M, N, m0 + wm0, n0 + wn0);
     return;
   }
+  if constexpr (SK) {
+    epi(acc, m0 + wm0, n0 + wn0);
+    return;
+  }
   float scale[TM];
 #pragma unroll
   for (int i = 0; i < TM; ++i) scale[i] = RS ? rs_lds[wm0 + i * 32 + (lane & 31)] : 1.0f;
@@ -958,6 +989,203 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_pipe_kernel(const
   __shared__ __attribute__((aligned(1024))) char smem[PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
   mm_pipe_body<BM, BN, BK, WAVES, STAGES, false, NTB, SPLIT>(lhsT, rhs, out, M, N, K, group_m, smem,
                                                              SplitK{parts, ws});
+}
+
+// ---------------------------------------------------------------------------
+// Stream-K lhsT.rhs (matmul variants 5 and 6): the pipelined core over a
+// grid of one workgroup per CU, each taking an equal share of all tiles' K
+// tiles (mi_streamk.hpp has the split and the combine protocol).
+// ---------------------------------------------------------------------------
+
+// Cache policy of the buffer intrinsics on gfx950: SC0 = 1, NT = 2, SC1 = 16.
+// sc0 sc1 is system scope: a store is written through to memory before it
+// is acknowledged, and a load misses every cache on the way, so a partial
+// sum stored by one workgroup and loaded by another after the tile
+// counter's atomic shows the stored values whichever CU or XCD each ran on.
+constexpr int kCpolSystem = 1 | 16;
+
+// Workspace of a stream-K launch: the tile counters at its start
+// (kSkCounterBytes), then `grid` later slots (one per workgroup, for its one
+// segment that is not a tile's p_0) and `tiles` first slots (p_0 of each
+// tile), BM*BN fp32 each.
+struct StreamKWs {
+  int* ctr;
+  float* later;
+  float* first;
+};
+
+// A slot holds one workgroup's accumulators in its own register order:
+// wave v, fragment (i, j), quad q of the 16 fp32 values, lane l at byte
+// ((((v * TM + i) * TN + j) * 4 + q) * 64 + l) * 16, so each wave store is
+// one contiguous 1 KiB.
+template <int TM, int TN>
+__device__ __forceinline__ uint32_t sk_slot_off(int wave, int i, int j, int q, int lane) {
+  return (uint32_t)((((wave * TM + i) * TN + j) * 4 + q) * 64 + lane) * 16u;
+}
+
+template <int BM, int BN, int TM, int TN>
+__device__ __forceinline__ void sk_store_slot(const f32x16_t (&acc)[TM][TN], float* slot, int wave, int lane) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(slot, (uint32_t)BM * BN * 4u);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4_t v = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, v), r,
+                                               sk_slot_off<TM, TN>(wave, i, j, q, lane), 0, kCpolSystem);
+      }
+}
+
+__device__ __forceinline__ f32x4_t sk_load4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolSystem));
+}
+
+// s[i][j] (+)= slot.
+template <int TM, int TN, bool ADD>
+__device__ __forceinline__ void sk_take_slot(f32x16_t (&s)[TM][TN], const float* slot, size_t slot_floats, int wave,
+                                             int lane) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(slot, (uint32_t)slot_floats * 4u);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x4_t v = sk_load4(r, sk_slot_off<TM, TN>(wave, i, j, q, lane));
+#pragma unroll
+        for (int x = 0; x < 4; ++x) s[i][j][4 * q + x] = ADD ? s[i][j][4 * q + x] + v[x] : v[x];
+      }
+}
+
+// The combine of tile t: acc = ((p_0 + p_1) + ...) + p_n.  The checker
+// (last_in_regs) holds p_n in acc and the storers' parts come from their
+// slots; a storer that combines takes every part from the slots, its own
+// included (stored, and drained, before its counter update).  Both add in
+// the same order, so the bits are the same.
+template <int BM, int BN, int TM, int TN>
+__device__ __forceinline__ void sk_combine(f32x16_t (&acc)[TM][TN], const StreamKWs& ws, int t, int fw, int n,
+                                           bool last_in_regs, int wave, int lane) {
+  const size_t slot = (size_t)BM * BN;
+  f32x16_t s[TM][TN];
+  sk_take_slot<TM, TN, false>(s, ws.first + (size_t)t * slot, slot, wave, lane);
+  for (int e = 1; e < n; ++e) sk_take_slot<TM, TN, true>(s, ws.later + (size_t)(fw + e) * slot, slot, wave, lane);
+  if (!last_in_regs) sk_take_slot<TM, TN, false>(acc, ws.later + (size_t)(fw + n) * slot, slot, wave, lane);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = s[i][j] + acc[i][j];
+}
+
+// s_waitcnt vmcnt(0) that the compiler may not move memory operations across.
+__device__ __forceinline__ void sk_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Epilogue of one stream-K segment: K tiles [kb, ke) of tile t, computed by
+// workgroup w.  A whole tile is stored; a part runs the protocol of
+// mi_streamk.hpp and, if it is the one that combines, stores the tile.
+// `bcast` is an LDS word for thread 0's atomic results.
+template <int BM, int BN, int WAVES, int TM, int TN>
+__device__ __forceinline__ void sk_epilogue(f32x16_t (&acc)[TM][TN], const StreamKPlan& plan, const StreamKWs& ws,
+                                            int w, int t, int kb, int ke, char* smem, int* bcast, int wave,
+                                            int lane, uint16_t* __restrict__ out, int M, int N, int row0,
+                                            int col0) {
+  float one[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) one[i] = 1.0f;
+  if (kb == 0 && ke == plan.kt) {
+    store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, row0, col0);
+    return;
+  }
+  const int tid = wave * 64 + lane;
+  const int fw = (int)plan.first_wg(t);
+  const int n = (int)plan.later_parts(t);
+  const size_t slot = (size_t)BM * BN;
+  float* mine = kb == 0 ? ws.first + (size_t)t * slot : ws.later + (size_t)w * slot;
+  bool combine, last_in_regs;
+  if (ke < plan.kt) {
+    // A storer.
+    sk_store_slot<BM, BN, TM, TN>(acc, mine, wave, lane);
+    sk_drain();
+    __syncthreads();
+    if (tid == 0) *bcast = __hip_atomic_fetch_add(ws.ctr + t, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+    const int old = *bcast;
+    combine = (old & kSkLastReady) != 0 && (old & kSkStoredMask) == n - 1;
+    last_in_regs = false;
+  } else {
+    // The checker.
+    if (tid == 0)
+      *bcast = __hip_atomic_fetch_add(ws.ctr + t, kSkLastArrived, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+    int old = *bcast;
+    combine = (old & kSkStoredMask) == n;
+    if (!combine) {
+      __syncthreads();  // every thread has read bcast before thread 0 writes it again
+      sk_store_slot<BM, BN, TM, TN>(acc, mine, wave, lane);
+      sk_drain();
+      __syncthreads();
+      if (tid == 0)
+        *bcast = __hip_atomic_fetch_add(ws.ctr + t, kSkLastReady, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __syncthreads();
+      old = *bcast;
+      combine = (old & kSkStoredMask) == n;
+    }
+    last_in_regs = true;
+  }
+  if (!combine) return;
+  // Every part has arrived: reset the counter for the next launch.
+  if (tid == 0) __hip_atomic_store(ws.ctr + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  sk_combine<BM, BN, TM, TN>(acc, ws, t, fw, n, last_in_regs, wave, lane);
+  store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, row0, col0);
+}
+
+// The stream-K kernel: gridDim.x workgroups (the host launches
+// streamk_grid(CUs, tiles, K tiles)); `ws` is the workspace, its counters
+// zero.  NTB: rhs read non-temporally (variant 6, skinny M).
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool NTB>
+__global__ __launch_bounds__(WAVES * 64) void mm_lhsT_rhs_bf16_sk_kernel(const uint16_t* __restrict__ lhsT,
+                                                                        const uint16_t* __restrict__ rhs,
+                                                                        uint16_t* __restrict__ out, int M, int N,
+                                                                        int K, int group_m, char* __restrict__ ws) {
+  using C = PipeCfg<BM, BN, BK, WAVES, STAGES>;
+  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+  __shared__ int bcast;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+  const int KT = (K + BK - 1) / BK;
+  const int grid = (int)gridDim.x;
+  const StreamKPlan plan((long long)tiles_m * tiles_n, KT, grid);
+  const StreamKWs sw{(int*)ws, (float*)(ws + kSkCounterBytes),
+                     (float*)(ws + kSkCounterBytes) + (size_t)grid * BM * BN};
+  // Logical workgroup id: the dispatcher deals workgroups round-robin to the
+  // 8 XCDs, so renumbering gives each XCD a run of consecutive ranges (the
+  // workgroups that share a tile mostly run on one XCD).  The protocol
+  // itself does not depend on where they run.
+  int w = (int)blockIdx.x;
+  {
+    const int per = grid >> 3, rem = grid & 7, xcd = w & 7;
+    w = xcd * per + (xcd < rem ? xcd : rem) + (w >> 3);
+  }
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Segments in reverse unit order: the head of the last tile first, the
+  // tail of the first tile last (mi_streamk.hpp).
+  const long long ubeg = plan.begin(w);
+  long long u = plan.begin(w + 1);
+  while (u > ubeg) {
+    const int t = (int)((u - 1) / KT);
+    const long long tstart = (long long)t * KT;
+    const int kb = (int)((tstart > ubeg ? tstart : ubeg) - tstart);
+    const int ke = (int)(u - tstart);
+    const int tm = t % tiles_m, tn = t / tiles_m;
+    mm_pipe_body<BM, BN, BK, WAVES, STAGES, false, NTB, false, false, false, true>(
+        lhsT, rhs, out, M, N, K, group_m, smem, SplitK{1, nullptr}, RowScale{nullptr, 0, 0.0f, 0.0f},
+        SegK{tm, tn, kb, ke - kb}, [&](auto& acc, int row0, int col0) __attribute__((always_inline)) {
+          sk_epilogue<BM, BN, WAVES>(acc, plan, sw, w, t, kb, ke, smem, &bcast, wave, lane, out, M, N, row0, col0);
+        });
+    u = tstart + kb;
+  }
 }
 
 // lhsT.rhs matmul variant 4: the pipelined core with each K tile's

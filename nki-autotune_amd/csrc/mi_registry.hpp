@@ -28,7 +28,19 @@ struct MiArgs {
   int group_m;
   int parts = 1;          // split-K parts
   char* ws = nullptr;     // workspace of workspace_bytes() bytes (256-byte aligned), or null if none is needed
+  int cus = 256;          // compute units of the device (the stream-K grid)
+  bool ws_zeroed = false; // the workspace's stream-K counters are known to be 0 (a reused workspace)
 };
+
+// Every workspace starts with the stream-K tile counters (kSkCounterBytes,
+// mi_streamk.hpp), which only the stream-K kernels touch and which each of
+// their launches leaves at 0; the data of the other kernels follows.
+inline char* ws_data(const MiArgs& a) { return a.ws + kSkCounterBytes; }
+
+// Stream-K variants (lhsT.rhs 5 and 6).
+inline bool is_streamk(int kernel_id, int variant) {
+  return kernel_id == MI_KERNEL_MATMUL_LHST_RHS_BF16 && (variant == 5 || variant == 6);
+}
 
 typedef hipError_t (*LaunchFn)(const MiArgs&, hipStream_t);
 
@@ -44,18 +56,33 @@ inline int grid_tiles(int M, int N, int BM, int BN) { return ((M + BM - 1) / BM)
 
 inline size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
-// Device workspace a launch needs, in bytes (0: none).
+// Device workspace a launch needs, in bytes (0: none): the stream-K
+// counters (kSkCounterBytes), then
 //   split-K matmul:                 fp32 products [parts][M][N]
 //   split-K fused (variants 4..12): products, then row sums of squares [parts][M]
 //   two-pass fused (variant 13):    xt [K][M] bf16, ssq [ceil(K/512)][M] fp32,
 //                                   then (split) products [parts][M][N]
-inline size_t workspace_bytes(int kernel_id, const mi_tile_cfg& c, int M, int N, int K) {
+//   stream-K (lhsT.rhs 5, 6):       fp32 partial tiles: one early slot per
+//                                   workgroup of the grid, one owner slot per
+//                                   output tile, BM*BN each (the counters
+//                                   themselves are the reserved region)
+inline size_t workspace_bytes(int kernel_id, const mi_tile_cfg& c, int M, int N, int K, int cus) {
   const size_t m = (size_t)M, n = (size_t)N, k = (size_t)K, p = (size_t)(c.split_k > 1 ? c.split_k : 0);
+  size_t data = 0;
   if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 && c.variant == 13)
-    return align256(k * m * 2) + align256((size_t)rms2_parts(K) * m * 4) + p * m * n * 4;
-  if (p == 0) return 0;
-  if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16) return p * (m * n + m) * 4;
-  return p * m * n * 4;
+    data = align256(k * m * 2) + align256((size_t)rms2_parts(K) * m * 4) + p * m * n * 4;
+  else if (is_streamk(kernel_id, c.variant)) {
+    const long long tiles = grid_tiles(M, N, c.block_m, c.block_n);
+    const long long kt = (K + c.block_k - 1) / c.block_k;
+    const size_t grid = (size_t)streamk_grid(cus, tiles, kt);
+    data = (grid + (size_t)tiles) * (size_t)c.block_m * (size_t)c.block_n * 4;
+  } else if (p == 0)
+    return 0;
+  else if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16)
+    data = p * (m * n + m) * 4;
+  else
+    data = p * m * n * 4;
+  return (size_t)kSkCounterBytes + data;
 }
 
 template <int BM, int BN, int BK, int W, int S>
@@ -87,15 +114,39 @@ hipError_t launch_mm_pipe(const MiArgs& a, hipStream_t s) {
     // Split-K: the parts' fp32 products into ws, then their sum into out.
     hipLaunchKernelGGL((mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, true>),
                        dim3(grid_tiles(a.M, a.N, BM, BN) * a.parts), dim3(W * 64), 0, s, (const uint16_t*)a.a,
-                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, (float*)a.ws);
+                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, (float*)ws_data(a));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_splitk_sum((const float*)a.ws, (uint16_t*)a.out, (size_t)a.M * (size_t)a.N, a.parts, s);
+    launch_splitk_sum((const float*)ws_data(a), (uint16_t*)a.out, (size_t)a.M * (size_t)a.N, a.parts, s);
   } else {
     hipLaunchKernelGGL((mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, false>),
                        dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
                        (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, 1, nullptr);
   }
+  return hipGetLastError();
+}
+
+// Zeroes the stream-K tile counters of a fresh workspace (a small kernel,
+// not hipMemsetAsync, so that a caller may capture the call in a HIP graph).
+template <int UNUSED = 0>
+__global__ __launch_bounds__(256) void sk_zero_kernel(int* __restrict__ p, int n) {
+  for (int i = (int)(blockIdx.x * 256 + threadIdx.x); i < n; i += (int)(gridDim.x * 256)) p[i] = 0;
+}
+
+// Stream-K (variants 5 and 6): one workgroup per CU; the counters are
+// zeroed first unless the workspace is known to hold zeros.
+template <int BM, int BN, int BK, int W, int S, bool NTB>
+hipError_t launch_mm_sk(const MiArgs& a, hipStream_t s) {
+  const int tiles = grid_tiles(a.M, a.N, BM, BN);
+  const int kt = (a.K + BK - 1) / BK;
+  const long long grid = streamk_grid(a.cus, tiles, kt);
+  if (!a.ws_zeroed) {
+    hipLaunchKernelGGL(sk_zero_kernel<0>, dim3((unsigned)((tiles + 255) / 256)), dim3(256), 0, s, (int*)a.ws, tiles);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((mm_lhsT_rhs_bf16_sk_kernel<BM, BN, BK, W, S, NTB>), dim3((unsigned)grid), dim3(W * 64), 0, s,
+                     (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.ws);
   return hipGetLastError();
 }
 
@@ -105,10 +156,10 @@ hipError_t launch_mm_kw(const MiArgs& a, hipStream_t s) {
   if (a.parts > 1) {
     hipLaunchKernelGGL((mm_lhsT_rhs_bf16_kw_kernel<BM, BN, BK, W, S, true>),
                        dim3(grid_tiles(a.M, a.N, BM, BN) * a.parts), dim3(W * 64), 0, s, (const uint16_t*)a.a,
-                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, (float*)a.ws);
+                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, (float*)ws_data(a));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_splitk_sum((const float*)a.ws, (uint16_t*)a.out, (size_t)a.M * (size_t)a.N, a.parts, s);
+    launch_splitk_sum((const float*)ws_data(a), (uint16_t*)a.out, (size_t)a.M * (size_t)a.N, a.parts, s);
   } else {
     hipLaunchKernelGGL((mm_lhsT_rhs_bf16_kw_kernel<BM, BN, BK, W, S, false>), dim3(grid_tiles(a.M, a.N, BM, BN)),
                        dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N,
@@ -122,10 +173,10 @@ hipError_t launch_mm_lhs(const MiArgs& a, hipStream_t s) {
   if (a.parts > 1) {
     hipLaunchKernelGGL((mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, true>),
                        dim3(grid_tiles(a.M, a.N, BM, BN) * a.parts), dim3(W * 64), 0, s, (const uint16_t*)a.a,
-                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, (float*)a.ws);
+                       (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, a.parts, (float*)ws_data(a));
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    launch_splitk_sum((const float*)a.ws, (uint16_t*)a.out, (size_t)a.M * (size_t)a.N, a.parts, s);
+    launch_splitk_sum((const float*)ws_data(a), (uint16_t*)a.out, (size_t)a.M * (size_t)a.N, a.parts, s);
   } else {
     hipLaunchKernelGGL((mm_lhs_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, NTB, false>),
                        dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64), 0, s, (const uint16_t*)a.a,
@@ -163,7 +214,7 @@ void launch_rms_xreg_one(const MiArgs& a, hipStream_t s) {
   hipLaunchKernelGGL((rmsnorm_mm_bf16_xreg_kernel<BM, BN, BK, W, S, XS, HG, NTW, SPLIT>),
                      dim3(grid_tiles(a.M, a.N, BM, BN) * (SPLIT ? a.parts : 1)), dim3(W * 64), 0, s,
                      (const uint16_t*)a.a, (const uint16_t*)a.g, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N,
-                     a.K, a.inv_k, a.eps, a.group_m, SPLIT ? a.parts : 1, SPLIT ? (float*)a.ws : nullptr);
+                     a.K, a.inv_k, a.eps, a.group_m, SPLIT ? a.parts : 1, SPLIT ? (float*)ws_data(a) : nullptr);
 }
 
 template <int BM, int BN, int BK, int W, int S, int XS, bool NTW = false>
@@ -174,7 +225,7 @@ hipError_t launch_rms_xreg(const MiArgs& a, hipStream_t s) {
     else launch_rms_xreg_one<BM, BN, BK, W, S, XS, false, NTW, true>(a, s);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const float* prod = (const float*)a.ws;
+    const float* prod = (const float*)ws_data(a);
     launch_splitk_rms_sum(prod, a.parts, prod + (size_t)a.parts * (size_t)a.M * (size_t)a.N, a.parts, a, s);
   } else if (a.g) {
     launch_rms_xreg_one<BM, BN, BK, W, S, XS, true, NTW, false>(a, s);
@@ -192,9 +243,10 @@ template <int BM, int BN, int BK, int W, int S>
 hipError_t launch_rms_2pass(const MiArgs& a, hipStream_t s) {
   const size_t m = (size_t)a.M, k = (size_t)a.K;
   const int sparts = rms2_parts(a.K);
-  uint16_t* xt = (uint16_t*)a.ws;
-  float* ssq = (float*)(a.ws + align256(k * m * 2));
-  float* prod = (float*)(a.ws + align256(k * m * 2) + align256((size_t)sparts * m * 4));
+  char* data = ws_data(a);
+  uint16_t* xt = (uint16_t*)data;
+  float* ssq = (float*)(data + align256(k * m * 2));
+  float* prod = (float*)(data + align256(k * m * 2) + align256((size_t)sparts * m * 4));
   hipLaunchKernelGGL(rms_pack_kernel<0>, dim3((unsigned)((a.M + RP_ROWS - 1) / RP_ROWS), (unsigned)sparts),
                      dim3(RP_WAVES * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, xt, ssq, a.M, a.K);
   hipError_t e = hipGetLastError();
@@ -231,6 +283,13 @@ hipError_t launch_rms_2pass(const MiArgs& a, hipStream_t s) {
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);    \
   template __global__ void mm_lhsT_rhs_bf16_pipe_kernel<BM, BN, BK, W, S, true, true>(  \
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*);
+// Stream-K lhsT matmul (variant 5; MI_MMSN: variant 6, rhs non-temporal).
+#define MI_MMS_INST(BM, BN, BK, W, S)                                                 \
+  template __global__ void mm_lhsT_rhs_bf16_sk_kernel<BM, BN, BK, W, S, false>(      \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, char*);
+#define MI_MMSN_INST(BM, BN, BK, W, S)                                                \
+  template __global__ void mm_lhsT_rhs_bf16_sk_kernel<BM, BN, BK, W, S, true>(       \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, char*);
 // K split over the waves (variant 4), unsplit and split-K instances.
 #define MI_MMW_INST(BM, BN, BK, W, S)                                                  \
   template __global__ void mm_lhsT_rhs_bf16_kw_kernel<BM, BN, BK, W, S, false>(       \
@@ -296,6 +355,13 @@ hipError_t launch_rms_2pass(const MiArgs& a, hipStream_t s) {
 #define MI_MMPN_ROW(BM, BN, BK, W, S)                                                              \
   {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 3}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
    &launch_mm_pipe<BM, BN, BK, W, S, true>},
+// Stream-K pipelined matmul: variant 5 (rhs cached), variant 6 (rhs non-temporal).
+#define MI_MMS_ROW(BM, BN, BK, W, S)                                                               \
+  {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 5}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_mm_sk<BM, BN, BK, W, S, false>},
+#define MI_MMSN_ROW(BM, BN, BK, W, S)                                                              \
+  {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 6}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_mm_sk<BM, BN, BK, W, S, true>},
 // Pipelined matmul with each K tile's sub-steps split over the waves: variant 4.
 #define MI_MMW_ROW(BM, BN, BK, W, S)                                                               \
   {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 4}, lds_mm_kw(BM, BN, BK, W, S), \
@@ -365,6 +431,7 @@ const MiEntry* table_mm_bm64(int* n);
 const MiEntry* table_mm_bm128(int* n);
 const MiEntry* table_mm_bm256(int* n);
 const MiEntry* table_mm_pipe(int* n);
+const MiEntry* table_mm_sk(int* n);
 const MiEntry* table_mm_kw(int* n);
 const MiEntry* table_mm_reg(int* n);
 const MiEntry* table_mm_lhs(int* n);

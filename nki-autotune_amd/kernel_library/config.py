@@ -158,8 +158,20 @@ def legal_configs(func_name: str, M: int, N: int, K: int, grid: list[TileConfig]
     """
     if grid is None:
         grid = compiled_configs(func_name)
+        # Stream-K configs only where split-K copies are offered too: shapes
+        # whose output tiles fill fewer than two waves of workgroups.
+        grid = [c for c in grid if not (is_streamk(func_name, c) and -(-M // c.block_m) * -(-N // c.block_n) >= 512)]
         grid = grid + split_k_variants(func_name, grid, M, N)
     return [c for c in grid if check(func_name, c, M, N, K)[0] == 0]
+
+
+# Stream-K variants (mi_streamk.hpp): lhsT.rhs 5 (rhs cached) and 6 (rhs non-temporal).
+STREAMK_VARIANTS = {"matmul_lhsT_rhs": (5, 6), "matmul_lhsT_rhs_nkigym": (5, 6)}
+
+
+def is_streamk(func_name: str, cfg: TileConfig) -> bool:
+    """Whether ``cfg`` is a stream-K config of ``func_name`` (one workgroup per CU over all tiles' K loops)."""
+    return cfg.variant in STREAMK_VARIANTS.get(func_name, ())
 
 
 SPLIT_K_PARTS = (2, 4, 8, 16)
@@ -245,6 +257,7 @@ __all__ = [
     "check",
     "compiled_configs",
     "default_config",
+    "is_streamk",
     "legal_configs",
     "record_tuned",
     "tuned_table",

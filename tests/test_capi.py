@@ -408,3 +408,21 @@ def test_output_aliasing_an_input_is_rejected():
         _no_overlap(buf[1500:2524].view(32, 32), lhs=a, rhs=b)
     with pytest.raises(ValueError, match="overlaps lhs"):
         _no_overlap(a, lhs=a, rhs=b)
+
+
+def test_library_needs_no_hip_symbol_newer_than_torchs_runtime():
+    """torch loads its own libamdhip64 (ROCm 7.0) first, and the library's
+    HIP calls bind to it, so every HIP symbol the library imports must carry
+    a version that runtime has: hip_7.0 or older."""
+    import re
+    import shutil
+    import subprocess
+
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--undefined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    versions = {tuple(int(x) for x in m.group(1).split(".")) for m in re.finditer(r"@hip_(\d+\.\d+)", out)}
+    assert versions, "no versioned HIP imports found"
+    assert max(versions) <= (7, 0), sorted(versions)

@@ -171,7 +171,7 @@ def test_render_parse_roundtrip_and_aliases():
     assert rcompile.problem_shape("matmul_lhs_rhs", input_specs("matmul_lhs_rhs", 64, 96, 128)) == (64, 96, 128)
 
 
-@pytest.mark.parametrize("fam,variants", [("matmul_lhsT_rhs", (0, 1, 2, 3)), ("matmul_lhs_rhs", (0, 1, 2)),
+@pytest.mark.parametrize("fam,variants", [("matmul_lhsT_rhs", (0, 1, 2, 3, 4, 5, 6)), ("matmul_lhs_rhs", (0, 1, 2)),
                                           ("rmsnorm_matmul", (0, 1, 4, 5, 11, 12, 13))])
 def test_jit_units_instantiate_every_variant(fam, variants, tmp_path):
     """The generated single-config unit of every variant names a real template
