@@ -101,14 +101,15 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--sweep-reps", type=int, default=20)
     ap.add_argument("--config", default="", help="tile config name (e.g. bm256_bn256_bk32_w4_s3_v1) instead of the sweep")
     ap.add_argument("--workload", choices=["c2", "c2-clock", "c3", "c3-matmul", "c4a", "c4b", "c4c", "c5", "decode",
-                                           "panel-stream", "defaults", "defaults-random"], default="c2",
+                                           "panel-stream", "defaults", "defaults-random", "split-host"], default="c2",
                     help="c2: lhsT.rhs matmul 8192^3 (the metric); c3: rmsnorm_matmul 4096^3; c3-matmul: the plain "
                          "lhsT.rhs matmul at 4096^3; c4a/b/c: the C4 "
                          "lhsT.rhs shapes; c5: skinny lhsT.rhs (--m) x 28672 x 8192; decode: rmsnorm_matmul at the "
                          "c5 shape; panel-stream: the K-panel loads alone from L2, MALL and HBM; defaults: the "
                          "library's default config against the autotune sweep's best at 83 shapes; "
-                         "defaults-random: the same at 30 seeded random shapes the default was not fitted to (all "
-                         "but c2: profiling workloads)")
+                         "defaults-random: the same at 30 seeded random shapes the default was not fitted to; "
+                         "split-host: back-to-back calls of workspace configs through the allocating entry point "
+                         "and the no-alloc one (all but c2: profiling workloads)")
     ap.add_argument("--settle-s", type=float, default=2.0,
                     help="GPU idle time before the timed region's warm-up (see settle())")
     ap.add_argument("--m", type=int, default=16, choices=[16, 64, 128], help="M of the c5 / decode workloads")
@@ -573,6 +574,8 @@ def main() -> int:
             ("rmsnorm_matmul", DEFAULTS_RMS)) for sh in shapes], "defaults")
     if args.workload == "defaults-random":
         return defaults_study(args, dev, random_default_shapes(args.random_seed), f"defaults-random:{args.random_seed}")
+    if args.workload == "split-host":
+        return split_host_study(args, dev)
     if args.workload in PLAIN_SHAPES:
         return shape_main(args, dev, *PLAIN_SHAPES[args.workload])
     fam, s = ("matmul_lhsT_rhs", M) if args.workload == "c2" else ("rmsnorm_matmul", 4096)
@@ -819,6 +822,72 @@ DEFAULTS_RMS = [(4096, 4096, 4096), (2048, 8192, 2048), (8192, 4096, 4096), (102
                 (2048, 2048, 2048), (1024, 4096, 4096), (3072, 3072, 3072), (256, 8192, 4096), (1024, 1024, 4096),
                 (1536, 6144, 2048), (640, 8192, 4096), (4096, 2048, 4096), (128, 4096, 4096), (768, 6144, 4096),
                 (2560, 4096, 2048), (384, 8192, 8192), (1024, 8192, 1024)]
+
+
+SPLIT_HOST_CASES = [((2048, 2048, 1024), "bm128_bn128_bk64_w4_s3_v1_k2"), ((2048, 2048, 1024), "bm64_bn64_bk64_w4_s4_v1_k2"),
+                    ((2048, 2048, 1024), "bm128_bn128_bk64_w4_s3_v1"), ((2048, 2048, 1024), "bm64_bn128_bk64_w4_s4_v5"),
+                    ((2048, 1024, 8192), "bm128_bn128_bk64_w4_s3_v1_k2"),
+                    ((2048, 1024, 8192), "bm256_bn128_bk64_w8_s3_v1_k4"),
+                    ((2048, 1024, 8192), "bm64_bn128_bk64_w4_s4_v1")]
+
+
+def split_host_study(args, dev) -> int:
+    """--workload split-host: what does a workspace config cost per call beyond its kernels?
+
+    Each (M, N, K), config of ``SPLIT_HOST_CASES`` (split-K, stream-K, and an
+    unsplit control) is called back to back on torch's current stream through
+    ``mi_matmul_lhsT_rhs_bf16`` (which keeps a workspace per stream) and
+    through ``mi_matmul_lhsT_rhs_bf16_noalloc`` (a static device array: no
+    allocation of any kind), the two in alternating rounds.  Per entry point:
+    the wall time per call of 400 back-to-back calls with one synchronisation
+    (best of 5 rounds), and the host time to issue 200 calls without waiting.
+    Equal back-to-back times mean the allocating entry point adds nothing the
+    GPU waits for."""
+    import ctypes
+
+    import torch
+
+    import kernel_library as kl
+    from kernel_library import _lib
+
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rows = []
+    for (m, n, k), name in SPLIT_HOST_CASES:
+        a = torch.empty((k, m), dtype=torch.bfloat16, device=dev).uniform_(-1, 1)
+        b = torch.empty((k, n), dtype=torch.bfloat16, device=dev).uniform_(-1, 1)
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
+        c = kl.TileConfig.from_name(name).to_c()
+        fns = {e: getattr(lib, e) for e in ("mi_matmul_lhsT_rhs_bf16", "mi_matmul_lhsT_rhs_bf16_noalloc")}
+        call_args = (a.data_ptr(), b.data_ptr(), out.data_ptr(), m, n, k, ctypes.byref(c), stream)
+        for e, fn in fns.items():
+            for _ in range(50):
+                rc = fn(*call_args)
+                if rc != 0:
+                    raise RuntimeError(f"{e} {name}: {_lib.last_error()}")
+        torch.cuda.synchronize()
+        b2b = {e: float("inf") for e in fns}
+        issue = {e: float("inf") for e in fns}
+        for _ in range(5):
+            for e, fn in fns.items():
+                t0 = time.perf_counter()
+                for _ in range(400):
+                    fn(*call_args)
+                torch.cuda.synchronize()
+                b2b[e] = min(b2b[e], (time.perf_counter() - t0) / 400)
+                t0 = time.perf_counter()
+                for _ in range(200):
+                    fn(*call_args)
+                issue[e] = min(issue[e], (time.perf_counter() - t0) / 200)
+                torch.cuda.synchronize()
+        r = {"shape": [m, n, k], "config": name}
+        for e in fns:
+            r[e] = {"back_to_back_us": round(b2b[e] * 1e6, 2), "host_issue_us": round(issue[e] * 1e6, 2)}
+        log(json.dumps(r))
+        rows.append(r)
+        del a, b, out
+    print(json.dumps({"workload": "split-host", "rows": rows}), flush=True)
+    return 0
 
 
 def random_default_shapes(seed: int = 2026, count: int = 30) -> list:

@@ -76,13 +76,20 @@ enum {
  *                               library-owned memory pool and frees after the
  *                               launch; a second kernel sums them in part
  *                               order into out (and applies 1/rms, fused).
- *                               A call's workspace is at most 2 GiB; the pool
+ *                               Every workspace also starts with 16 KiB of
+ *                               stream-K tile counters.  A call's workspace
+ *                               is at most 2 GiB.  Outside graph capture a
+ *                               workspace of at most 64 MiB is a buffer the
+ *                               library keeps per stream (up to 4 streams
+ *                               per device; it grows when a call needs
+ *                               more), so back-to-back calls allocate
+ *                               nothing; a larger one, or any under HIP
+ *                               graph capture, is allocated and freed
+ *                               around the call (under capture: allocation
+ *                               and free nodes of the graph).  The pool
  *                               keeps at most 256 MiB of freed workspace
- *                               cached per device and returns the rest to
- *                               the device at a synchronisation that
- *                               begins after the call's launches finished.
- *                               Under HIP graph capture the workspace becomes
- *                               allocation and free nodes of the graph.
+ *                               cached per device; mi_release_workspace
+ *                               returns all of it.
  *   group_m                   : L2 raster group height in tiles (0 = default 8)
  *   variant                   : kernel-specific pipeline (every variant computes
  *                               the same function):
@@ -94,7 +101,14 @@ enum {
  *                    most 128x128) and the epilogue adding the waves' sums
  *                    in wave order (few output tiles, long K).  Variant 4
  *                    adds in another fp32 order than 0..3, so its result
- *                    may differ from theirs in the last bit
+ *                    may differ from theirs in the last bit; 5 stream-K: a
+ *                    grid of one workgroup per CU (at most 4096 output
+ *                    tiles), each taking an equal share of all tiles' K
+ *                    loops on the pipelined core; a tile computed in parts
+ *                    is summed by the part that finishes it, in K order,
+ *                    from fp32 partials in the workspace ((CUs + tiles) *
+ *                    block_m * block_n * 4 bytes after the counters); 6 as
+ *                    5 with rhs read non-temporally (skinny M)
  *     matmul_lhs_rhs 0 the software-pipelined core (block_k >= 32, 2..4 stages);
  *                    1 the same with the K-contiguous A panel loaded two K
  *                    tiles per load (block_k 32 or 64); 2 as 0 with rhs read
@@ -170,8 +184,9 @@ int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void
  * the reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
  * hipMalloc).  Same arguments, result and errors as mi_matmul_lhsT_rhs_bf16;
- * the workspace of a split-K config (split_k * M * N * 4 bytes of fp32
- * partial products) is a static device array of MI_NOALLOC_SCRATCH_BYTES
+ * the workspace of a split-K or stream-K config (16 KiB of stream-K
+ * counters, then split_k * M * N * 4 bytes of fp32 partial products, or the
+ * stream-K partial tiles) is a static device array of MI_NOALLOC_SCRATCH_BYTES
  * that each GPU holds from the first call there until the process ends, and
  * a config needing more returns MI_E_RANGE (cfg == NULL never does: the
  * default splits at most 256 blocks of 256 x 256).  Calls on one GPU share that
@@ -187,16 +202,17 @@ int mi_matmul_lhsT_rhs_bf16_noalloc(const void* lhsT, const void* rhs, void* out
  * (reference autotune/src/autotune/runner/detect.py:7-20). */
 int mi_device_info(int* num_devices, char* arch, int arch_len, int* num_cus);
 
-/* Returns the device memory the library holds for split-K and two-pass
- * workspace freed by earlier calls to the device, on every device the
- * library has used; synchronises the null stream of each.  Memory behind a
- * call whose launches have not finished is kept.  Without it, the runtime
+/* Returns the device memory the library holds for split-K, stream-K and
+ * two-pass workspace to the device, on every device the library has used:
+ * the buffers kept per stream (after a device synchronisation) and what
+ * earlier calls freed into the library's pool.  Without it, the runtime
  * hands a call's freed workspace back to the library's pool only at the
  * pool's next allocation (the next call that needs workspace), which then
- * keeps at most 256 MiB cached: between calls the library holds up to the
- * last such call's workspace plus 256 MiB.  Not under graph capture.  No
- * counterpart in the reference (its kernels allocate nothing beyond their
- * output).  Returns 0 or -error. */
+ * keeps at most 256 MiB cached: between calls the library holds its kept
+ * buffers (at most 64 MiB for each of up to 4 streams per device) plus up
+ * to the last larger call's workspace and 256 MiB.  Not under graph
+ * capture.  No counterpart in the reference (its kernels allocate nothing
+ * beyond their output).  Returns 0 or -error. */
 int mi_release_workspace(void);
 
 /* Message of the last failure on the calling thread ("" if none). */

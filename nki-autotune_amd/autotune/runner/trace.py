@@ -264,3 +264,70 @@ def collect_counters(variant_dir: str, replay_path: str, reps: int = 5, timeout_
         return derive(passes)
     except Exception as exc:  # per-kernel failures are data, never raised
         return {"error": f"{type(exc).__name__}: {exc}"}
+
+
+def read_kernel_trace(path: str) -> list[dict]:
+    """Dispatches of a rocprofv3 kernel_trace.csv in start order: name and duration (ns)."""
+    rows = []
+    with open(path) as f:
+        for row in csv.DictReader(f):
+            start, end = float(row["Start_Timestamp"]), float(row["End_Timestamp"])
+            rows.append({"name": row["Kernel_Name"], "start": start, "ns": end - start})
+    rows.sort(key=lambda r: r["start"])
+    return rows
+
+
+def timed_region(dispatches: list[dict], steps: int, product: str = "mm_lhsT_rhs_bf16_pipe_kernel",
+                 bracket: str = "clocked_lhsT_rhs_kernel") -> dict:
+    """The dispatches of a bench.py timed region in a kernel trace of the whole run.
+
+    bench.py reads the engine clock with the kernel's clocked twin right
+    before and right after its ``steps`` timed launches, so the timed region
+    is the one run of exactly ``steps`` consecutive dispatches of the
+    product kernel with a twin dispatch on each side (the warm-up run before
+    the first twin reading has ``--warmup`` dispatches, the settle runs
+    more).  Dispatches of other libraries (torch's buffer fills around a
+    twin reading) are skipped.  Returns their kernel name and duration
+    statistics (us)."""
+    ours = [d for d in dispatches if "mi::" in d["name"]]
+    runs, i = [], 0
+    while i < len(ours):
+        if product in ours[i]["name"]:
+            j = i
+            while j < len(ours) and ours[j]["name"] == ours[i]["name"]:
+                j += 1
+            before = i > 0 and bracket in ours[i - 1]["name"]
+            after = j < len(ours) and bracket in ours[j]["name"]
+            if j - i == steps and before and after:
+                runs.append(ours[i:j])
+            i = j
+        else:
+            i += 1
+    if len(runs) != 1:
+        raise ValueError(f"{len(runs)} runs of {steps} {product} dispatches between clocked-twin dispatches")
+    ns = sorted(d["ns"] for d in runs[0])
+    return {"kernel": runs[0][0]["name"].split("(")[0], "dispatches": len(ns),
+            "avg_us": round(sum(ns) / len(ns) / 1e3, 2), "median_us": round(ns[len(ns) // 2] / 1e3, 2),
+            "min_us": round(ns[0] / 1e3, 2), "max_us": round(ns[-1] / 1e3, 2)}
+
+
+def _main() -> int:
+    import argparse
+
+    ap = argparse.ArgumentParser(description="rocprofv3 trace summaries")
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    tr = sub.add_parser("timed-region", help="the bench.py timed region in a kernel_trace.csv of the whole run")
+    tr.add_argument("--csv", required=True)
+    tr.add_argument("--steps", type=int, required=True)
+    tr.add_argument("--flop", type=float, default=2.0 * 8192 ** 3, help="algorithmic FLOP per launch")
+    tr.add_argument("--peak-tflops", type=float, default=2500.0)
+    args = ap.parse_args()
+    res = timed_region(read_kernel_trace(args.csv), args.steps)
+    res["tflops_from_avg"] = round(args.flop / (res["avg_us"] * 1e-6) / 1e12, 1)
+    res["frac_from_avg"] = round(res["tflops_from_avg"] / args.peak_tflops, 4)
+    print(json.dumps(res))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(_main())
