@@ -19,6 +19,8 @@ one launch of that kernel on inputs resident in HBM.
   the plain matmul at the same shape, each with its autotuned config; the
   matmul both on its own U(-1,1) inputs and on the fused kernel's operands
   (normalised x, W).
+* ``fused_reference_contract``: the same pair at the reference kernel's own
+  shape and contract (2048^3, no gamma: rmsnorm_matmul_online).
 * ``data_sensitivity``: the C2 kernel on all-zero and all-one inputs
   (diagnostic: the chip's clock under MFMA load depends on operand data).
 * ``other_configs``: C4's three shapes (TFLOP/s) and C5's three, plus the
@@ -101,7 +103,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--sweep-reps", type=int, default=20)
     ap.add_argument("--config", default="", help="tile config name (e.g. bm256_bn256_bk32_w4_s3_v1) instead of the sweep")
     ap.add_argument("--workload", choices=["c2", "c2-clock", "c3", "c3-matmul", "c4a", "c4b", "c4c", "c5", "decode",
-                                           "panel-stream", "defaults", "defaults-random", "split-host"], default="c2",
+                                           "panel-stream", "defaults", "defaults-random", "split-host", "online-pair"],
+                    default="c2",
                     help="c2: lhsT.rhs matmul 8192^3 (the metric); c3: rmsnorm_matmul 4096^3; c3-matmul: the plain "
                          "lhsT.rhs matmul at 4096^3; c4a/b/c: the C4 "
                          "lhsT.rhs shapes; c5: skinny lhsT.rhs (--m) x 28672 x 8192; decode: rmsnorm_matmul at the "
@@ -109,7 +112,8 @@ def parse() -> argparse.Namespace:
                          "library's default config against the autotune sweep's best at 83 shapes; "
                          "defaults-random: the same at 30 seeded random shapes the default was not fitted to; "
                          "split-host: back-to-back calls of workspace configs through the allocating entry point "
-                         "and the no-alloc one (all but c2: profiling workloads)")
+                         "and the no-alloc one; online-pair: the fused kernel without gamma beside the matmul at "
+                         "2048^3, the reference kernel's shape and contract (all but c2: profiling workloads)")
     ap.add_argument("--settle-s", type=float, default=2.0,
                     help="GPU idle time before the timed region's warm-up (see settle())")
     ap.add_argument("--m", type=int, default=16, choices=[16, 64, 128], help="M of the c5 / decode workloads")
@@ -117,14 +121,14 @@ def parse() -> argparse.Namespace:
     return ap.parse_args()
 
 
-def sweep(func_name: str, m: int, n: int, k: int, reps: int, no_tune: bool):
+def sweep(func_name: str, m: int, n: int, k: int, reps: int, no_tune: bool, with_gamma: bool = True):
     """Autotuned config of ``func_name`` at (m, n, k) (or the table/default one with ``no_tune``)."""
     import kernel_library as kl
     from autotune.tune import tune
 
     if no_tune:
         return kl.default_config(func_name, m, n, k), None
-    res = tune(func_name, m, n, k, check=True, warmup=max(3, reps // 4), reps=reps)
+    res = tune(func_name, m, n, k, check=True, warmup=max(3, reps // 4), reps=reps, with_gamma=with_gamma)
     if res.best is None:
         raise RuntimeError(f"autotune sweep found no working config for {func_name} {m}x{n}x{k}:\n{res.output}")
     if res.check is not None and not res.check["pass"]:
@@ -134,64 +138,104 @@ def sweep(func_name: str, m: int, n: int, k: int, reps: int, no_tune: bool):
     return res.best, res
 
 
-def time_pair(a, b, cfg, launch_fn, reps: int = 50) -> float:
+def time_calls(launch, reps: int = 50) -> float:
+    """Median per-launch seconds (HIP events around each launch) of ``launch``."""
     import torch
 
     from autotune.runner.benchmark import time_launches
 
-    times = time_launches(lambda: launch_fn(a, b, cfg), 5, reps)
+    times = time_launches(launch, 5, reps)
     torch.cuda.synchronize()
     return sorted(times)[len(times) // 2]
 
 
-def fused_pair(reps: int, no_tune: bool) -> dict:
-    """rmsnorm_matmul vs plain matmul at 4096^3, each autotuned."""
+def c_launchers(dev):
+    """Launch closures that call the C ABI with arguments built once: the
+    Python wrappers' ~10 us of host work per call would otherwise leave the
+    GPU idle between 20 us kernels and be timed with them."""
+    import ctypes
+
     import torch
 
-    import kernel_library as kl
+    from kernel_library import _lib
+
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    held = []
+
+    def mm(lhs_t, rhs, out, cfg):
+        c = cfg.to_c()
+        held.append(c)
+        k, m = lhs_t.shape
+        args = (lhs_t.data_ptr(), rhs.data_ptr(), out.data_ptr(), m, rhs.shape[1], k, ctypes.byref(c), stream)
+        _lib.check_rc(lib.mi_matmul_lhsT_rhs_bf16(*args), "matmul_lhsT_rhs")
+        return lambda: lib.mi_matmul_lhsT_rhs_bf16(*args)
+
+    def rms(x, w, g, out, cfg, eps=1e-6):
+        c = cfg.to_c()
+        held.append(c)
+        m, k = x.shape
+        args = (x.data_ptr(), g.data_ptr() if g is not None else None, w.data_ptr(), out.data_ptr(), m, w.shape[1], k,
+                ctypes.c_float(eps), ctypes.byref(c), stream)
+        _lib.check_rc(lib.mi_rmsnorm_matmul_bf16(*args), "rmsnorm_matmul")
+        return lambda: lib.mi_rmsnorm_matmul_bf16(*args)
+
+    return mm, rms
+
+
+def fused_pair(reps: int, no_tune: bool, s: int = 4096, gamma: bool = True) -> dict:
+    """rmsnorm_matmul vs plain matmul at s^3, each autotuned: C3 (4096^3 with
+    gamma), or without gamma the reference kernel's own contract
+    (rmsnorm_matmul_online, tuned under that name)."""
+    import torch
+
     from autotune.runner.benchmark import generate_tensors, upload
     from autotune.tune import default_dists, input_specs
 
-    s = 4096
     dev = torch.device("cuda:0")
-    cfg_r, _ = sweep("rmsnorm_matmul", s, s, s, reps, no_tune)
+    fam_r = "rmsnorm_matmul" if gamma else "rmsnorm_matmul_online"
+    cfg_r, _ = sweep(fam_r, s, s, s, reps, no_tune, with_gamma=gamma)
     cfg_m, _ = sweep("matmul_lhsT_rhs", s, s, s, reps, no_tune)
-    spec_r = input_specs("rmsnorm_matmul", s, s, s)
+    spec_r = input_specs("rmsnorm_matmul", s, s, s, with_gamma=gamma)
     r = upload(generate_tensors(spec_r, 0, default_dists("rmsnorm_matmul", s)), spec_r, dev)
+    g = r.get("gamma")
     spec_m = input_specs("matmul_lhsT_rhs", s, s, s)
     mm = upload(generate_tensors(spec_m, 0, default_dists("matmul_lhsT_rhs", s)), spec_m, dev)
     out_r = torch.empty((s, s), dtype=torch.bfloat16, device=dev)
     out_m = torch.empty((s, s), dtype=torch.bfloat16, device=dev)
+    c_mm, c_rms = c_launchers(dev)
+    fused = c_rms(r["lhs"], r["rhs"], g, out_r, cfg_r)
+    plain = c_mm(mm["lhs_T"], mm["rhs"], out_m, cfg_m)
     # Interleaved rounds: both kernels see the same clock and power states.
     tr, tm = [], []
     for _ in range(5):
-        tr.append(time_pair(r, None, cfg_r, lambda d, _b, c: kl.rmsnorm_matmul(d["lhs"], d["rhs"], d["gamma"], cfg=c,
-                                                                                  out=out_r), 40))
-        tm.append(time_pair(mm, None, cfg_m, lambda d, _b, c: kl.matmul_lhsT_rhs(d["lhs_T"], d["rhs"], cfg=c,
-                                                                                  out=out_m), 40))
+        tr.append(time_calls(fused, 40))
+        tm.append(time_calls(plain, 40))
     # The same matmul on the fused kernel's own operands: lhsT = the
     # normalised, gamma-scaled x (bf16), rhs = W.  MI355X's clock under MFMA
     # load depends on the operand data, so this is the like-for-like pair.
     xf = r["lhs"].float()
-    xhat = (xf * torch.rsqrt(xf.pow(2).mean(1, keepdim=True) + 1e-6) * r["gamma"].float()).bfloat16()
+    xhat = xf * torch.rsqrt(xf.pow(2).mean(1, keepdim=True) + 1e-6)
+    xhat = (xhat * g.float() if gamma else xhat).bfloat16()
     same = {"lhs_T": xhat.t().contiguous(), "rhs": r["rhs"]}
     del xf, xhat
+    same_launch = c_mm(same["lhs_T"], same["rhs"], out_m, cfg_m)
     ts = []
     for _ in range(5):
-        ts.append(time_pair(same, None, cfg_m, lambda d, _b, c: kl.matmul_lhsT_rhs(d["lhs_T"], d["rhs"], cfg=c,
-                                                                                    out=out_m), 40))
+        ts.append(time_calls(same_launch, 40))
     t_r, t_m, t_s = sorted(tr)[2], sorted(tm)[2], sorted(ts)[2]
     fl = 2.0 * s ** 3
-    x, w, g = r["lhs"], r["rhs"], r["gamma"]
+    x, w = r["lhs"], r["rhs"]
 
     def unfused():
         xf = x.float()
-        torch.matmul((xf * torch.rsqrt(xf.pow(2).mean(1, keepdim=True) + 1e-6) * g.float()).to(torch.bfloat16), w,
-                     out=out_r)
+        xn = xf * torch.rsqrt(xf.pow(2).mean(1, keepdim=True) + 1e-6)
+        torch.matmul((xn * g.float() if gamma else xn).to(torch.bfloat16), w, out=out_r)
 
     t_v = vendor_time(unfused)
     return {
         "shape": [s, s, s],
+        "gamma": gamma,
         "rmsnorm_matmul_tflops": round(fl / t_r / 1e12, 1),
         "rmsnorm_matmul_config": cfg_r.name,
         "matmul_tflops": round(fl / t_m / 1e12, 1),
@@ -576,6 +620,10 @@ def main() -> int:
         return defaults_study(args, dev, random_default_shapes(args.random_seed), f"defaults-random:{args.random_seed}")
     if args.workload == "split-host":
         return split_host_study(args, dev)
+    if args.workload == "online-pair":
+        print(json.dumps({"workload": "online-pair", **fused_pair(args.sweep_reps, args.no_tune, s=2048, gamma=False)}),
+              flush=True)
+        return 0
     if args.workload in PLAIN_SHAPES:
         return shape_main(args, dev, *PLAIN_SHAPES[args.workload])
     fam, s = ("matmul_lhsT_rhs", M) if args.workload == "c2" else ("rmsnorm_matmul", 4096)
@@ -669,6 +717,8 @@ def main() -> int:
         log(f"data sensitivity: {line['data_sensitivity']}")
         line["fused"] = fused_pair(args.sweep_reps, args.no_tune)
         log(f"fused pair: {line['fused']}")
+        line["fused_reference_contract"] = fused_pair(args.sweep_reps, args.no_tune, s=2048, gamma=False)
+        log(f"fused pair, 2048^3 without gamma: {line['fused_reference_contract']}")
         line["other_configs"] = other_configs()
         log(f"other configs: {line['other_configs']}")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)

@@ -121,7 +121,11 @@ enum {
  *                    kernel writes bf16(x * gamma) in the lhsT layout and
  *                    the rows' sums of squares to the workspace (K * M * 2 +
  *                    ceil(K / 512) * M * 4 bytes), then the pipelined lhsT
- *                    core applies 1/rms to its fp32 accumulators.  Variants
+ *                    core applies 1/rms to its fp32 accumulators; 14
+ *                    without gamma only (gamma != NULL: MI_E_TILE): the
+ *                    matmul_lhs_rhs core reads x once, LDS-direct, sums its
+ *                    rows' squares from the MFMA A fragments (bf16 dot2)
+ *                    and applies 1/rms to its fp32 accumulators.  Variants
  *                    2, 3 and 6..10 do not exist (MI_E_TILE).
  */
 typedef struct {

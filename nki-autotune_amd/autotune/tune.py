@@ -176,7 +176,7 @@ def tune(func_name: str, M: int, N: int, K: int, configs=None, seed: int = 0, ca
 
     fam = canonical_name(func_name)
     if configs is None:
-        configs = kl.legal_configs(fam, M, N, K)
+        configs = kl.legal_configs(fam, M, N, K, with_gamma=with_gamma)
     jobs = make_jobs(fam, M, N, K, configs, dists, with_gamma)
     output = profile(jobs, cache_dir, seed, "gfx950", detailed, warmup=warmup, reps=reps, flush_bytes=flush_bytes,
                      allow_jit=allow_jit, check_numerics=check)

@@ -317,10 +317,11 @@ struct KPanelLoader {
   }
   __device__ __forceinline__ void issue_at(int j, __amdgpu_buffer_rsrc_t rs_kt, char* smem, int base,
                                            bool tail) const {
-    if (EVEN || active[j]) {
-      if (tail) lds_dma16(rs_kt, smem + base + lds_off[j], voff_tail[j]);
-      else lds_dma16(rs_kt, smem + base + lds_off[j], voff[j]);
-    }
+    // One load either way, its offset selected without a branch: a branch
+    // per load splits the main loop into blocks, and code the compiler
+    // moves between blocks (sinking a chain of VALU work into the last
+    // block of the loop body) escapes the scheduling hints of its sub-step.
+    if (EVEN || active[j]) lds_dma16(rs_kt, smem + base + lds_off[j], tail ? voff_tail[j] : voff[j]);
   }
   static constexpr int LOADS_PER_TILE = PER_WAVE;
 };
@@ -684,8 +685,19 @@ struct NoEpi {};
 // epilogue of its own the body hands its accumulators to
 // epi(acc, row0, col0) (row0, col0: this wave's first output row and
 // column), after the main loop's final barrier.
+// SQ (the fused kernel without gamma, rmsnorm_matmul variant 14): the
+// K-contiguous A operand is x itself, so every x value of the block passes
+// through the A fragments the MFMAs consume, each sub-step once.  Lane l
+// holds row l%32 of each 32-row fragment and K chunk 2*kk + l/32 of
+// sub-step kk; it sums the squares of its chunks' 8 values with bf16 dot2
+// (v_dot2c_f32_bf16: exact bf16 products, fp32 sums), four per fragment,
+// in K order.  The waves that share rows (one wave row of the grid) take
+// the sub-steps in turns, the two half-waves' sums are added, the wave
+// row's parts are added through LDS in a fixed order, and the epilogue
+// scales output row m by 1/sqrt(ssq[m] * inv_k + eps) (rsc.inv_k,
+// rsc.eps).  K chunks past K read zeros and add nothing.
 template <int BM, int BN, int BK, int WAVES, int STAGES, bool AK, bool NTB = false, bool SPLIT = false,
-          bool RS = false, bool KW = false, bool SK = false, class Epi = NoEpi>
+          bool RS = false, bool KW = false, bool SK = false, class Epi = NoEpi, bool SQ = false>
 __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, const uint16_t* __restrict__ rhs,
                                              uint16_t* __restrict__ out, int M, int N, int K, int group_m,
                                              char* smem, const SplitK sk = SplitK{1, nullptr},
@@ -700,6 +712,8 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   static_assert(KW || G::ok, "illegal wave grid");
   static_assert(!KW || (!AK && !RS), "K split over the waves: lhsT operand, no row scale");
   static_assert(!SK || (!KW && !RS && !SPLIT), "stream-K: the plain wave-grid core");
+  static_assert(!SQ || (AK && !KW && !RS && !SPLIT && !SK), "row sums of squares: the K-contiguous unsplit core");
+  static_assert(!SQ || G::WN * BM * 4 <= C::LDS_BYTES, "row sums of squares exchanged through LDS");
   static_assert(BK % 32 == 0, "BK must be a multiple of 32 (even number of MFMA K steps)");
   static_assert(STAGES >= 2 && STAGES <= 4, "2..4 LDS stages");
   // KW: every wave covers the whole block (TM x TN MFMA tiles) over its own
@@ -812,12 +826,39 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
 #pragma unroll
     for (int f = 0; f < NF; ++f) read_frag(stage, kk, buf, f);
   };
-  auto mfmas = [&](int buf) {
+  float sq[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) sq[i] = 0.0f;
+  // SQ: the G::WN waves that share rows take turns, sub-step kk going to
+  // the wave in column kk % WN, and add their sums at the end.
+  const int wcol = KW ? 0 : wave % G::WN;
+  auto mfmas = [&](int buf, int kk, auto wc_c) {
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[buf][j], af[buf][i], acc[i][j], 0, 0, 0);
+    if constexpr (SQ) {
+      if (G::WN > 1 && kk % G::WN != decltype(wc_c)::value) return;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        // Pair d of the fragment as a shuffle with constant indices.  (A
+        // bf16x2 bit-cast from dword d of the fragment viewed as u32x4 is
+        // compiled as dword 0 for every d by this hipcc; the shuffle and an
+        // element-wise build are not.)
+        static_for<4>([&](auto d_c) __attribute__((always_inline)) {
+          constexpr int d = decltype(d_c)::value;
+          const bf16x2_t v = __builtin_shufflevector(af[buf][i], af[buf][i], 2 * d, 2 * d + 1);
+          sq[i] = __builtin_amdgcn_fdot2_f32_bf16(v, v, sq[i], false);
+        });
+      }
+    }
+  };
+  // Scheduling of one sub-step: its MFMAs with the LDS reads (and, SQ, the
+  // dot2 VALU work) spread between them.
+  auto sched = [&]() __attribute__((always_inline)) {
+    if constexpr (SQ) interleave_mfma_mix<TM * TN, 2 * NF, 4 * TM, 0>();
+    else interleave_mfma_ds<TM * TN, 2 * NF>();
   };
   // Load q (< LPT) of K tile kt into `stage`: the A loads, then the B loads.
   auto issue_one = [&](int q, int kt, int stage) {
@@ -900,14 +941,16 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
   // even, so the ring's wrap keeps the alternation.
   static_assert((STAGES * KSW) % 2 == 0, "operand buffers need an even sub-step count per ring turn");
   auto bufof = [](int stage, int kk) { return (stage * KSW + kk) & 1; };
-  auto tile = [&](int t, auto cur_c) __attribute__((always_inline)) {
+  // wc_c: the wave column as a compile-time constant (SQ, below), so that
+  // each sub-step's share of the sums of squares is decided at compile time.
+  auto tile = [&](int t, auto cur_c, auto wc_c) __attribute__((always_inline)) {
     constexpr int cur = decltype(cur_c)::value;
     constexpr int nxt = cur + 1 == STAGES ? 0 : cur + 1;
 #pragma unroll
     for (int kk = 0; kk + 1 < KSW; ++kk) {
       read_frags(cur, kk + 1, bufof(cur, kk + 1));
-      mfmas(bufof(cur, kk));
-      interleave_mfma_ds<TM * TN, 2 * NF>();
+      mfmas(bufof(cur, kk), kk, wc_c);
+      sched();
     }
     vm_wait<(STAGES - 2) * LPT>();
     __syncthreads();
@@ -918,39 +961,49 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
 #pragma unroll
       for (int q = f * LPT / NF; q < (f + 1) * LPT / NF; ++q) issue_one(q, kt_new, cur);
     }
-    mfmas(bufof(cur, KSW - 1));
-    interleave_mfma_ds<TM * TN, 2 * NF>();
+    mfmas(bufof(cur, KSW - 1), KSW - 1, wc_c);
+    sched();
   };
   // Last tile: no further loads.
-  auto last_tile = [&](int cur) __attribute__((always_inline)) {
+  auto last_tile = [&](int cur, auto wc_c) __attribute__((always_inline)) {
 #pragma unroll
     for (int kk = 0; kk < KSW; ++kk) {
       if (kk + 1 < KSW) read_frags(cur, kk + 1, (kk + 1) & 1);
-      mfmas(kk & 1);
-      interleave_mfma_ds<TM * TN, 2 * NF>();
+      mfmas(kk & 1, kk, wc_c);
+      sched();
     }
   };
-  int t0 = 0;
-  for (; t0 + STAGES < KT; t0 += STAGES)
-    static_for<STAGES>([&](auto s_c) __attribute__((always_inline)) { tile(t0 + s_c(), s_c); });
-  if constexpr (KSW % 2 == 1) {
-    // The buffer parity depends on the stage, which is a compile-time
-    // constant only inside tile(): the last tile runs through tile() too.
-    // Its extra barrier reads the next stage (a clamped re-read of the last
-    // K tile) into the unused buffer and issues one more clamped load group,
-    // which the drain below retires.
-    static_while<STAGES>([&](auto s_c) __attribute__((always_inline)) {
-      if (t0 + s_c() >= KT) return false;
-      tile(t0 + s_c(), s_c);
-      return true;
+  auto k_loop = [&](auto wc_c) __attribute__((always_inline)) {
+    int t0 = 0;
+    for (; t0 + STAGES < KT; t0 += STAGES)
+      static_for<STAGES>([&](auto s_c) __attribute__((always_inline)) { tile(t0 + s_c(), s_c, wc_c); });
+    if constexpr (KSW % 2 == 1) {
+      // The buffer parity depends on the stage, which is a compile-time
+      // constant only inside tile(): the last tile runs through tile() too.
+      // Its extra barrier reads the next stage (a clamped re-read of the
+      // last K tile) into the unused buffer and issues one more clamped
+      // load group, which the drain below retires.
+      static_while<STAGES>([&](auto s_c) __attribute__((always_inline)) {
+        if (t0 + s_c() >= KT) return false;
+        tile(t0 + s_c(), s_c, wc_c);
+        return true;
+      });
+    } else {
+      static_while<STAGES>([&](auto s_c) __attribute__((always_inline)) {
+        if (t0 + s_c() + 1 >= KT) return false;
+        tile(t0 + s_c(), s_c, wc_c);
+        return true;
+      });
+      last_tile((KT - 1) % STAGES, wc_c);
+    }
+  };
+  if constexpr (SQ && G::WN > 1) {
+    // One copy of the K loop per wave column; each wave runs its own.
+    static_for<G::WN>([&](auto wc_c) __attribute__((always_inline)) {
+      if (wcol == decltype(wc_c)::value) k_loop(wc_c);
     });
   } else {
-    static_while<STAGES>([&](auto s_c) __attribute__((always_inline)) {
-      if (t0 + s_c() + 1 >= KT) return false;
-      tile(t0 + s_c(), s_c);
-      return true;
-    });
-    last_tile((KT - 1) % STAGES);
+    k_loop(std::integral_constant<int, 0>{});
   }
   wait_vmem();
   __syncthreads();  // the epilogue reuses the panel buffers
@@ -970,8 +1023,30 @@ __device__ __forceinline__ void mm_pipe_body(const uint16_t* __restrict__ a, con
     return;
   }
   float scale[TM];
+  if constexpr (SQ) {
+    // Lanes l and l^32 hold the two K halves of one row (a + b == b + a,
+    // so both get the same bits); the WN waves of a wave row then add
+    // their sums through LDS [WN][BM], in wave-column order.
+    float* xs = (float*)smem;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) scale[i] = RS ? rs_lds[wm0 + i * 32 + (lane & 31)] : 1.0f;
+    for (int i = 0; i < TM; ++i) {
+      const float t = sq[i] + __shfl_xor(sq[i], 32);
+      if (lane < 32) xs[wcol * BM + wm0 + i * 32 + lane] = t;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm0 + i * 32 + (lane & 31);
+      float t = xs[r];
+#pragma unroll
+      for (int c = 1; c < G::WN; ++c) t += xs[c * BM + r];
+      scale[i] = 1.0f / __builtin_sqrtf(t * rsc.inv_k + rsc.eps);
+    }
+    __syncthreads();  // store_tile reuses the same LDS
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) scale[i] = RS ? rs_lds[wm0 + i * 32 + (lane & 31)] : 1.0f;
+  }
   store_tile<TM, TN, WAVES>(acc, scale, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
 }
 
@@ -1216,6 +1291,21 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pipe_kernel(const 
   __shared__ __attribute__((aligned(1024))) char smem[PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
   mm_pipe_body<BM, BN, BK, WAVES, STAGES, true, NTB, SPLIT>(lhs, rhs, out, M, N, K, group_m, smem,
                                                             SplitK{parts, ws});
+}
+
+// Fused out[M,N] = (x[M,K] * rsqrt(mean_k x^2 + eps)) . W[K,N] without gamma
+// (rmsnorm_matmul variant 14): the pipelined K-contiguous core with the
+// rows' sums of squares taken from its A fragments (SQ above), so x is read
+// once, by LDS-direct loads, and never scaled: 1/rms scales the fp32
+// accumulators in the epilogue.
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+__global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_sq_kernel(const uint16_t* __restrict__ x,
+                                                                       const uint16_t* __restrict__ w,
+                                                                       uint16_t* __restrict__ out, int M, int N,
+                                                                       int K, int group_m, float eps, float inv_k) {
+  __shared__ __attribute__((aligned(1024))) char smem[PipeCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
+  mm_pipe_body<BM, BN, BK, WAVES, STAGES, true, false, false, false, false, false, NoEpi, true>(
+      x, w, out, M, N, K, group_m, smem, SplitK{1, nullptr}, RowScale{nullptr, 0, inv_k, eps});
 }
 
 // ---------------------------------------------------------------------------

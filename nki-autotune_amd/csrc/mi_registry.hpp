@@ -265,6 +265,17 @@ hipError_t launch_rms_2pass(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Fused kernel without gamma (variant 14): one launch of the K-contiguous
+// pipelined core that takes the rows' sums of squares from its A operand.
+// The C ABI rejects it with gamma.
+template <int BM, int BN, int BK, int W, int S>
+hipError_t launch_rms_sq(const MiArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((rmsnorm_mm_bf16_sq_kernel<BM, BN, BK, W, S>), dim3(grid_tiles(a.M, a.N, BM, BN)), dim3(W * 64),
+                     0, s, (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m,
+                     a.eps, a.inv_k);
+  return hipGetLastError();
+}
+
 // Explicit instantiation of one config's kernel (namespace scope); every
 // table row needs its kernel instantiated in the same translation unit so
 // the host launch stub is emitted there.
@@ -344,6 +355,11 @@ hipError_t launch_rms_2pass(const MiArgs& a, hipStream_t s) {
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*, const float*, int, float, \
       float);
 
+// Variant 14: the fused kernel without gamma.
+#define MI_RMSQ_INST(BM, BN, BK, W, S)                                                                     \
+  template __global__ void rmsnorm_mm_bf16_sq_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*, \
+                                                                       uint16_t*, int, int, int, int, float, float);
+
 // Table rows.
 #define MI_MM_ROW(BM, BN, BK, W, S)                                                                  \
   {MI_KERNEL_MATMUL_LHST_RHS_BF16, {BM, BN, BK, W, S, 1, 0, 0}, MatmulCfg<BM, BN, BK, W, S>::LDS_BYTES, \
@@ -396,6 +412,10 @@ hipError_t launch_rms_2pass(const MiArgs& a, hipStream_t s) {
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 9 + XS}, XregCfg<BM, BN, BK, W, S>::LDS_BYTES, \
    &launch_rms_xreg<BM, BN, BK, W, S, XS, true>, XregCfg<BM, BN, BK, W, S>::GK_MAX},
 
+#define MI_RMSQ_ROW(BM, BN, BK, W, S)                                                                  \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 14}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_rms_sq<BM, BN, BK, W, S>},
+
 #define MI_RMS2_ROW(BM, BN, BK, W, S)                                                               \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 13}, lds_rms2(BM, BN, BK, W, S),         \
    &launch_rms_2pass<BM, BN, BK, W, S>},
@@ -437,6 +457,7 @@ const MiEntry* table_mm_reg(int* n);
 const MiEntry* table_mm_lhs(int* n);
 const MiEntry* table_rms_xreg(int* n);
 const MiEntry* table_rms_2pass(int* n);
+const MiEntry* table_rms_sq(int* n);
 const MiEntry* table_rms_bm64(int* n);
 const MiEntry* table_rms_bm128(int* n);
 const MiEntry* table_rms_bm256(int* n);

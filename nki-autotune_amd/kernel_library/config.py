@@ -149,12 +149,15 @@ def baseline_grid(variants: tuple[int, ...] = (0,)) -> list[TileConfig]:
     ]
 
 
-def legal_configs(func_name: str, M: int, N: int, K: int, grid: list[TileConfig] | None = None) -> list[TileConfig]:
+def legal_configs(func_name: str, M: int, N: int, K: int, grid: list[TileConfig] | None = None,
+                  with_gamma: bool = True) -> list[TileConfig]:
     """Configs of ``grid`` (default: all compiled ones) that pass static legality at (M, N, K).
 
     This plays the role of ``KernelMDP.legal_actions`` (reference
     nkigym/src/nkigym/environment/mdp.py:44-54): the action space of the
-    search is the set of legal tile configs.
+    search is the set of legal tile configs.  ``with_gamma`` (the fused
+    kernel called with a gamma) drops the variants that compute the
+    product without gamma only.
     """
     if grid is None:
         grid = compiled_configs(func_name)
@@ -162,7 +165,14 @@ def legal_configs(func_name: str, M: int, N: int, K: int, grid: list[TileConfig]
         # whose output tiles fill fewer than two waves of workgroups.
         grid = [c for c in grid if not (is_streamk(func_name, c) and -(-M // c.block_m) * -(-N // c.block_n) >= 512)]
         grid = grid + split_k_variants(func_name, grid, M, N)
+    if with_gamma:
+        grid = [c for c in grid if c.variant not in GAMMA_FREE_VARIANTS.get(func_name, ())]
     return [c for c in grid if check(func_name, c, M, N, K)[0] == 0]
+
+
+# Fused variants that compute the product without gamma only (the C ABI
+# rejects them with a gamma): rmsnorm_matmul 14.
+GAMMA_FREE_VARIANTS = {"rmsnorm_matmul": (14,), "rmsnorm_matmul_online": (14,)}
 
 
 # Stream-K variants (mi_streamk.hpp): lhsT.rhs 5 (rhs cached) and 6 (rhs non-temporal).

@@ -28,7 +28,7 @@ def _hipcc():
 
 
 UNITS = ("mm_bf16_pipe.hip", "mm_bf16_kw.hip", "mm_bf16_lhs.hip", "mm_bf16_reg.hip", "rms_bf16_xreg.hip",
-         "rms_bf16_2pass.hip")
+         "rms_bf16_2pass.hip", "rms_bf16_sq.hip")
 
 
 @pytest.fixture(scope="module")
@@ -94,3 +94,30 @@ def test_kernels_straight_line(unit, asm_of):
     for name, lines in ks.items():
         bad = [ln for ln in lines if ln.strip().startswith(("s_swappc", "s_setpc", "flat_load", "scratch_"))]
         assert not bad, (name, bad[:3])
+
+
+def test_row_square_sums_read_every_pair_of_the_fragment(asm_of):
+    """The fused kernel without gamma (rmsnorm_matmul variant 14) sums the
+    squares of each A fragment's four bf16 pairs with four dependent
+    v_dot2c_f32_bf16 into one accumulator.  Each such chain must read four
+    different registers (the fragment's dwords): a bit-cast of the
+    fragment's dword d to bf16x2 was compiled as dword 0 for every d."""
+    import re
+
+    ks = kernels(asm_of("rms_bf16_sq.hip"))
+    assert ks
+    dot2 = re.compile(r"^\s*v_dot2c_f32_bf16(?:_e32)?\s+v(\d+),\s*v(\d+),\s*v(\d+)")
+    ks = {name: lines for name, lines in ks.items() if "rmsnorm_mm_bf16_sq_kernel" in name}
+    assert ks
+    for name, lines in ks.items():
+        per_acc: dict[int, list[int]] = {}
+        for ln in lines:
+            m = dot2.match(ln)
+            if m:
+                assert m.group(2) == m.group(3), (name, ln)   # a square: the pair with itself
+                per_acc.setdefault(int(m.group(1)), []).append(int(m.group(2)))
+        assert per_acc, name
+        for acc, srcs in per_acc.items():
+            assert len(srcs) % 4 == 0, (name, acc, len(srcs))
+            for i in range(0, len(srcs), 4):
+                assert len(set(srcs[i:i + 4])) == 4, (name, acc, srcs[i:i + 4])

@@ -142,6 +142,10 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (LHS, TileConfig(64, 128, 128, 4, 3, variant=1), (1024, 1024, 1024), _lib.MI_E_TILE),    # pairs: bk <= 64
         (MM, TileConfig(256, 256, 32, 8, 1, variant=1), (1024, 1024, 1024), _lib.MI_E_TILE),     # pipelined: >= 2 stages
         (MM, TileConfig(256, 256, 16, 8, 2, variant=3), (1024, 1024, 1024), _lib.MI_E_TILE),     # pipelined: bk >= 32
+        (RMS, TileConfig(128, 128, 64, 4, 3, variant=14), (2048, 2048, 2048), _lib.MI_OK),
+        (RMS, TileConfig(128, 128, 64, 4, 3, variant=14), (2048, 2048, 2044), _lib.MI_E_ALIGN),   # K % 8
+        (RMS, TileConfig(128, 128, 64, 4, 1, variant=14), (2048, 2048, 2048), _lib.MI_E_TILE),    # pipelined core
+        (RMS, TileConfig(128, 128, 64, 4, 3, split_k=2, variant=14), (512, 512, 8192), _lib.MI_E_SPLIT),
     ],
 )
 def test_cfg_check_codes(kid, cfg, shape, code):
@@ -331,6 +335,24 @@ def test_entry_points_reject_bad_arguments_before_any_gpu_call():
     bad = TileConfig(256, 256, 128, 8, 2).to_c()
     a, b, o = (ctypes.c_void_p(0x10000000 + i * (1 << 28)) for i in range(3))
     assert L.mi_matmul_lhsT_rhs_bf16(a, b, o, 8192, 8192, 8192, ctypes.byref(bad), None) == _lib.MI_E_LDS
+
+
+def test_gamma_free_variant_rejects_gamma_before_any_gpu_call():
+    """rmsnorm_matmul variant 14 computes the product without gamma: a call
+    with gamma is refused with MI_E_TILE on the host, and the sweep of a
+    call with gamma never offers it."""
+    L = _lib.lib()
+    c = TileConfig(128, 128, 64, 4, 3, variant=14).to_c()
+    x, g, w, o = (ctypes.c_void_p(0x10000000 + i * (1 << 28)) for i in range(4))
+    assert L.mi_rmsnorm_matmul_bf16(x, g, w, o, 2048, 2048, 2048, 1e-6, ctypes.byref(c), None) == _lib.MI_E_TILE
+    assert "without gamma" in _lib.last_error()
+    from kernel_library.config import legal_configs
+
+    with_g = legal_configs("rmsnorm_matmul", 2048, 2048, 2048)
+    without = legal_configs("rmsnorm_matmul", 2048, 2048, 2048, with_gamma=False)
+    assert not [cfg for cfg in with_g if cfg.variant == 14]
+    assert [cfg for cfg in without if cfg.variant == 14]
+    assert {cfg.name for cfg in with_g} < {cfg.name for cfg in without}
 
 
 def test_entry_points_reject_misaligned_pointers():

@@ -60,6 +60,22 @@ def test_128cube_fp32_reference_procedure(gpu):
     np.testing.assert_allclose(_host(out), lhs_T.T @ rhs, atol=1e-4, rtol=1e-4)
 
 
+def _streamk_key(cfg, M, N, K, cus):
+    """K offsets at which the stream-K plan cuts every output tile (mi_streamk.hpp: unit u = t*KT + kt,
+    workgroup w takes units [w*total//grid, (w+1)*total//grid)), as the split-K key; a config whose
+    tiles are cut differently gets a key of its own."""
+    kt = -(-K // cfg.block_k)
+    tiles = -(-M // cfg.block_m) * -(-N // cfg.block_n)
+    total = tiles * kt
+    grid = min(cus, total)
+    starts = {w * total // grid for w in range(grid)}
+    cuts = {tuple(u - t * kt for u in range(t * kt, t * kt + kt) if u in starts) for t in range(tiles)}
+    if len(cuts) != 1:
+        return ("streamk", cfg.name)
+    offs = tuple(c * cfg.block_k for c in sorted(cuts.pop()))
+    return () if offs == (0,) else offs
+
+
 def test_bf16_every_config_small_fixture(gpu):
     """The reference's small fixture shape (K=256, M=256, N=512), every compiled config."""
     import torch
@@ -81,10 +97,15 @@ def test_bf16_every_config_small_fixture(gpu):
         # equal when they split K at the same boundaries.  Variant 4 sums
         # each wave's K sub-steps, then the waves: equal when its split of
         # every K tile into waves' sub-steps is the same.
+        # Stream-K (variants 5, 6) sums its parts in K order as split-K does,
+        # so it joins the split configs with the same boundaries when every
+        # tile is cut at the same K offsets (else it stands alone).
         kts = -(-(-(-K // cfg.block_k)) // cfg.split_k) * cfg.block_k
         key = tuple(range(0, K, kts)) if cfg.split_k > 1 else ()
         if cfg.variant == 4:
             key += ("kw", cfg.block_k // 16 // cfg.waves, cfg.waves)
+        if cfg.variant in (5, 6):
+            key = _streamk_key(cfg, 256, 512, K, torch.cuda.get_device_properties(gpu).multi_processor_count)
         if key not in first:
             first[key] = (cfg, bits)
         else:

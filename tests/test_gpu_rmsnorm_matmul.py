@@ -173,7 +173,9 @@ def test_error_within_reference_bf16_semantics(gpu, shape, with_gamma):
     if with_gamma:
         shipped = [kl.TileConfig.from_name("bm128_bn512_bk32_w8_s3_v4")]
     else:
-        shipped = [kl.TileConfig.from_name("bm128_bn128_bk64_w4_s2_v4")]
+        shipped = [kl.TileConfig.from_name("bm128_bn128_bk64_w4_s2_v4"),
+                   kl.TileConfig.from_name("bm128_bn128_bk64_w4_s3_v14"),
+                   kl.TileConfig.from_name("bm256_bn256_bk32_w8_s3_v14")]
     cfgs = shipped + [kl.TileConfig(256, 256, 32, 4, 3, variant=13)]
     if with_gamma:
         cfgs.append(kl.default_config("rmsnorm_matmul", M, N, K))
@@ -190,6 +192,50 @@ def test_error_within_reference_bf16_semantics(gpu, shape, with_gamma):
               f"ratio {err / ref_err:.3f}", rep, flush=True)
         assert _ok(rep), (cfg, rep)
         assert err <= ref_err, (cfg, err, ref_err)
+
+
+def test_no_gamma_variant14_every_config_ragged(gpu):
+    """Variant 14 (no gamma; the rows' sums of squares taken from the MFMA A
+    fragments): every prebuilt config at ragged M, N, K (K not a multiple of
+    block_k, so the last K tile's zero-filled chunks must add nothing), with
+    a zero row (exactly 0), a constant row and a row of large values, every
+    output against the closed form."""
+    import kernel_library as kl
+
+    M, K, N = 200, 264, 136
+    d = rms_inputs(M, K, N, seed=12, with_gamma=False)
+    x = d["lhs"].copy()
+    x[7] = 0.0
+    x[11] = 0.25
+    x[13] *= 64.0
+    expected = orms.closed_form(x, d["rhs"])
+    xd, wd = _dev(x, gpu), _dev(d["rhs"], gpu)
+    cfgs = [c for c in kl.legal_configs("rmsnorm_matmul", M, N, K, with_gamma=False) if c.variant == 14]
+    assert len(cfgs) >= 8
+    for cfg in cfgs:
+        print("v14 ragged", cfg.name, flush=True)
+        host = _host(kl.rmsnorm_matmul(xd, wd, None, cfg=cfg))
+        rep = rms_check(host, expected)
+        assert _ok(rep), (cfg, rep)
+        assert np.all(host[7] == 0.0)
+
+
+def test_no_gamma_variant14_identity_weight(gpu):
+    """W = I isolates the row statistics: out = bf16(x / rms(x)) for every
+    row, at K = 1024 (16 K tiles of the 128x128 block, both halves of every
+    A fragment used)."""
+    import kernel_library as kl
+
+    M, K = 256, 1024
+    d = rms_inputs(M, K, K, seed=13, with_gamma=False)
+    x = d["lhs"]
+    eye = _dev(np.eye(K, dtype=np.float32), gpu)
+    ref = x * orms.inv_rms(x)[:, None]
+    for name in ("bm128_bn128_bk64_w4_s3_v14", "bm64_bn64_bk64_w4_s4_v14", "bm256_bn128_bk64_w8_s3_v14"):
+        y = _host(kl.rmsnorm_matmul(_dev(x, gpu), eye, None, cfg=kl.TileConfig.from_name(name)))
+        rep = rms_check(y, ref)
+        print("v14 identity", name, rep, flush=True)
+        assert _ok(rep), (name, rep)
 
 
 def test_skinny_decode_shape(gpu):
