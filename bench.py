@@ -23,8 +23,10 @@ one launch of that kernel on inputs resident in HBM.
   shape and contract (2048^3, no gamma: rmsnorm_matmul_online).
 * ``data_sensitivity``: the C2 kernel on all-zero and all-one inputs
   (diagnostic: the chip's clock under MFMA load depends on operand data).
-* ``other_configs``: C4's three shapes (TFLOP/s) and C5's three, plus the
-  fused kernel at C5's shapes (HBM GB/s), each with its tuned config.
+* ``other_configs``: C4's three shapes (TFLOP/s), each autotuned by a sweep
+  in this run (its winner, configs timed and numerics under ``sweep``), and
+  C5's three plus the fused kernel at C5's shapes (HBM GB/s) with their
+  tuned configs.
 * ``cpu_baseline``: the CPU oracle's tile-faithful emulation of the
   reference kernel's loop nest (fp32, numpy/BLAS) on a bounded column slice
   of the same workload, rank 0 only.
@@ -389,13 +391,18 @@ def warm(launch, seconds: float = 0.5) -> None:
         torch.cuda.synchronize()
 
 
-def other_configs(reps: int = 30) -> dict:
-    """C4 (TFLOP/s) and C5 plus the fused kernel at C5's shapes (HBM GB/s), each with its tuned config.
+def other_configs(reps: int = 30, sweep_reps: int = 20, no_tune: bool = False) -> dict:
+    """C4 (TFLOP/s) and C5 plus the fused kernel at C5's shapes (HBM GB/s).
 
-    Each shape is timed after half a second of back-to-back launches of the
-    same kernel.  C5 and the fused decode shapes are timed with a 512 MiB
-    buffer overwritten before every launch, so W streams from HBM, not from
-    the 256 MB MALL."""
+    C4 is the autotune sweep BASELINE's config 4 asks for: each shape is
+    swept in this run (every legal prebuilt config with its numerics gate,
+    then the finalists re-timed in interleaved rounds; ``no_tune`` takes the
+    tuned-table config instead), and the winner is timed through the C ABI
+    with arguments built once.  C5 and the fused decode shapes take their
+    tuned configs.  Each shape is timed after half a second of back-to-back
+    launches of the same kernel.  C5 and the fused decode shapes are timed
+    with a 512 MiB buffer overwritten before every launch, so W streams from
+    HBM, not from the 256 MB MALL."""
     import torch
 
     import kernel_library as kl
@@ -403,21 +410,27 @@ def other_configs(reps: int = 30) -> dict:
     from autotune.tune import default_dists, input_specs
 
     dev = torch.device("cuda:0")
+    c_mm, _ = c_launchers(dev)
     res = {}
     for m, k, n in ((2048, 8192, 1024), (4096, 1024, 14336), (1024, 14336, 4096)):
+        cfg, tuned = sweep("matmul_lhsT_rhs", m, n, k, sweep_reps, no_tune)
         specs = input_specs("matmul_lhsT_rhs", m, n, k)
         d = upload(generate_tensors(specs, 0, default_dists("matmul_lhsT_rhs", k)), specs, dev)
-        cfg = kl.default_config("matmul_lhsT_rhs", m, n, k)
         out = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
-        launch = lambda: kl.matmul_lhsT_rhs(d["lhs_T"], d["rhs"], cfg=cfg, out=out)  # noqa: E731
+        launch = c_mm(d["lhs_T"], d["rhs"], out, cfg)
         warm(launch)
         t = sorted(time_launches(launch, 5, reps))
         tf = 2.0 * m * n * k / t[len(t) // 2] / 1e12
         a_t = d["lhs_T"].t()
         tv = vendor_time(lambda: torch.matmul(a_t, d["rhs"], out=out))  # noqa: B023
-        res[f"C4 (M,K,N)=({m},{k},{n})"] = {"config": cfg.name, "tflops": round(tf, 1),
-                                            "pct_mfma_peak": round(100 * tf / PEAK_BF16_TFLOPS, 1),
-                                            "hipblaslt_tflops": round(2.0 * m * n * k / tv / 1e12, 1)}
+        row = {"config": cfg.name, "tflops": round(tf, 1), "pct_mfma_peak": round(100 * tf / PEAK_BF16_TFLOPS, 1),
+               "hipblaslt_tflops": round(2.0 * m * n * k / tv / 1e12, 1)}
+        if tuned is not None:
+            row["sweep"] = {"configs_timed": len(tuned.output.successes), "failures": len(tuned.output.failures),
+                            "winner_sweep_us": round(tuned.best_time_s * 1e6, 2),
+                            "numerics_pass": bool(tuned.check and tuned.check["pass"]),
+                            "tuned_table_config": kl.default_config("matmul_lhsT_rhs", m, n, k).name}
+        res[f"C4 (M,K,N)=({m},{k},{n})"] = row
         del d, out
     scratch = torch.empty((512 << 20) // 4, dtype=torch.float32, device=dev)
     for fam, label in (("matmul_lhsT_rhs", "C5"), ("rmsnorm_matmul", "fused decode")):
@@ -719,7 +732,7 @@ def main() -> int:
         log(f"fused pair: {line['fused']}")
         line["fused_reference_contract"] = fused_pair(args.sweep_reps, args.no_tune, s=2048, gamma=False)
         log(f"fused pair, 2048^3 without gamma: {line['fused_reference_contract']}")
-        line["other_configs"] = other_configs()
+        line["other_configs"] = other_configs(sweep_reps=args.sweep_reps, no_tune=args.no_tune)
         log(f"other configs: {line['other_configs']}")
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line, ensure_ascii=False), flush=True)

@@ -140,6 +140,39 @@ def test_tune_picks_a_passing_winner(gpu):
     assert res.best_time_s > 0
 
 
+@pytest.mark.parametrize("M,N,K", [(2048, 1024, 8192), (1024, 4096, 14336)])
+def test_tune_at_c4_shapes(gpu, M, N, K):
+    """The autotune sweep BASELINE's config 4 asks for, at two of its shapes:
+    every legal prebuilt config (split-K and stream-K copies included at
+    C4a) through the numerics gate, the winner re-checked, and the winner no
+    slower than the shipped tuned-table config timed in the same way."""
+    import statistics
+
+    import torch
+
+    import kernel_library as kl
+    from autotune.runner.benchmark import Launcher, generate_tensors, time_launches, upload
+    from autotune.tune import default_dists, input_specs, tune
+    from kernel_library import _lib
+
+    print(f"tune matmul_lhsT_rhs {M}x{N}x{K}", flush=True)
+    res = tune("matmul_lhsT_rhs", M, N, K, reps=10, warmup=3, finalists=4, rounds=3)
+    assert res.best is not None and res.check["pass"], res.check
+    assert len(res.output.successes) >= 40
+    shipped = kl.default_config("matmul_lhsT_rhs", M, N, K)
+    specs = input_specs("matmul_lhsT_rhs", M, N, K)
+    d = upload(generate_tensors(specs, 0, default_dists("matmul_lhsT_rhs", K)), specs, torch.device(gpu))
+    out = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
+    t = {}
+    for cfg in (res.best, shipped):
+        launch = Launcher(_lib.lib(), "matmul_lhsT_rhs", cfg, d, out, M, N, K)
+        t[cfg.name] = statistics.median(statistics.median(time_launches(launch, 5, 20)) for _ in range(3))
+    print(f"winner {res.best.name} {t[res.best.name] * 1e6:.1f} us, tuned table {shipped.name} "
+          f"{t[shipped.name] * 1e6:.1f} us", flush=True)
+    # One box's timing noise between two near-equal configs, not a ranking.
+    assert t[res.best.name] <= 1.10 * t[shipped.name]
+
+
 def test_vendor_baseline_matches_oracle(gpu):
     """The vendor rows (hipBLASLt for the matmuls; torch's unfused rmsnorm then
     hipBLASLt for the fused kernel) compute the same function as the kernels:
