@@ -53,6 +53,10 @@ def test_mdp_moves_and_legality():
     assert Atom("split_k", "x2") in atoms_for("rmsnorm_matmul")
     assert Atom("split_k", "x2") not in atoms_for("matmul_lhsT_rhs_f32")
     assert not mdp.is_terminal(s)
+    # Variant moves reach every variant of the family, 0 and those above 8 included.
+    assert mdp.step(TileConfig(256, 256, 32, 4, 2, variant=1), Atom("variant", "=0")).variant == 0
+    rms = TileMDP("rmsnorm_matmul", 4096, 4096, 4096, prebuilt_only=True)
+    assert rms.step(TileConfig(256, 256, 32, 4, 2, variant=0), Atom("variant", "=13")).variant == 13
 
 
 @pytest.mark.parametrize("fam", ["matmul_lhsT_rhs", "matmul_lhs_rhs", "rmsnorm_matmul"])
