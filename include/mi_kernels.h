@@ -172,7 +172,11 @@ int mi_matmul_lhs_rhs_bf16(const void* lhs, const void* rhs, void* out, int M, i
                            const mi_tile_cfg* cfg, void* stream);
 
 /* fp32 variant of the lhsT product (the fp32 CPU-simulation semantics of
- * reference nkigym/src/nkigym/synthesis/simulate_nki.py:24-48). */
+ * reference nkigym/src/nkigym/synthesis/simulate_nki.py:24-48).  Variant 0:
+ * LDS-tiled FMAs, K summed in sequential order (64x64 blocks, block_k 16 or
+ * 32); variant 1: the fp32 MFMA (v_mfma_f32_32x32x2_f32), K summed two at a
+ * time (64x64 or 128x128 blocks, block_k 16).  Any M, N, K; 4-byte aligned
+ * pointers; cfg == NULL selects mi_default_config. */
 int mi_matmul_lhsT_rhs_f32(const float* lhsT, const float* rhs, float* out, int M, int N, int K,
                            const mi_tile_cfg* cfg, void* stream);
 

@@ -56,7 +56,7 @@ FAMILY_VARIANTS = {
     "matmul_lhsT_rhs": (0, 1, 2, 3, 4, 5, 6),
     "matmul_lhs_rhs": (0, 1, 2),
     "rmsnorm_matmul": (0, 1, 4, 5, 11, 12, 13),
-    "matmul_lhsT_rhs_f32": (0,),
+    "matmul_lhsT_rhs_f32": (0, 1),
 }
 
 _POW2_KNOBS = {"block_m": (32, 512), "block_n": (32, 512), "block_k": (16, 128), "group_m": (1, 64),

@@ -146,6 +146,11 @@ mi::Legal template_legal(int kernel_id, const mi_tile_cfg& c) {
           return mi::bad(MI_E_TILE, "the fp32 kernel takes 64x64 blocks, block_k 16 or 32, 4 waves, 1 stage");
         return mi::ok();
       }
+      if (c.variant == 1) {
+        if ((bm != 64 && bm != 128) || bn != bm || bk != 16 || w != 4 || s != 1)
+          return mi::bad(MI_E_TILE, "the fp32 MFMA kernel takes 64x64 or 128x128 blocks, block_k 16, 4 waves, 1 stage");
+        return mi::ok();
+      }
       break;
     default:
       break;

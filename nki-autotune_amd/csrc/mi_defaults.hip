@@ -285,7 +285,8 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
   const bool lhs = kernel_id == MI_KERNEL_MATMUL_LHS_RHS_BF16;
   switch (kernel_id) {
     case MI_KERNEL_MATMUL_LHST_RHS_F32:
-      *cfg = {64, 64, 16, 4, 1, 1, 0, 0};
+      // The fp32 MFMA kernel; variant 0 (sequential K order) stays selectable.
+      *cfg = {64, 64, 16, 4, 1, 1, 0, 1};
       break;
     case MI_KERNEL_MATMUL_LHST_RHS_BF16:
     case MI_KERNEL_MATMUL_LHS_RHS_BF16:

@@ -142,6 +142,11 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (LHS, TileConfig(64, 128, 128, 4, 3, variant=1), (1024, 1024, 1024), _lib.MI_E_TILE),    # pairs: bk <= 64
         (MM, TileConfig(256, 256, 32, 8, 1, variant=1), (1024, 1024, 1024), _lib.MI_E_TILE),     # pipelined: >= 2 stages
         (MM, TileConfig(256, 256, 16, 8, 2, variant=3), (1024, 1024, 1024), _lib.MI_E_TILE),     # pipelined: bk >= 32
+        (F32, TileConfig(64, 64, 16, 4, 1, variant=1), (256, 512, 512), _lib.MI_OK),
+        (F32, TileConfig(128, 128, 16, 4, 1, variant=1), (37, 53, 129), _lib.MI_OK),     # any M, N, K
+        (F32, TileConfig(128, 64, 16, 4, 1, variant=1), (256, 512, 512), _lib.MI_E_TILE),  # square blocks only
+        (F32, TileConfig(64, 64, 32, 4, 1, variant=1), (256, 512, 512), _lib.MI_E_TILE),   # block_k 16
+        (F32, TileConfig(64, 64, 16, 4, 1, variant=2), (256, 512, 512), _lib.MI_E_TILE),   # no variant 2
         (RMS, TileConfig(128, 128, 64, 4, 3, variant=14), (2048, 2048, 2048), _lib.MI_OK),
         (RMS, TileConfig(128, 128, 64, 4, 3, variant=14), (2048, 2048, 2044), _lib.MI_E_ALIGN),   # K % 8
         (RMS, TileConfig(128, 128, 64, 4, 1, variant=14), (2048, 2048, 2048), _lib.MI_E_TILE),    # pipelined core

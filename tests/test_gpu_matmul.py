@@ -49,6 +49,37 @@ def test_c1_fp32_matches_closed_form(gpu):
     np.testing.assert_allclose(_host(out), expected, atol=F32_ATOL, rtol=F32_RTOL)
 
 
+@pytest.mark.parametrize("name", ["bm64_bn64_bk16_w4_s1", "bm64_bn64_bk32_w4_s1", "bm64_bn64_bk16_w4_s1_v1",
+                                  "bm128_bn128_bk16_w4_s1_v1"])
+@pytest.mark.parametrize("M,N,K", [(256, 512, 512), (37, 53, 129), (200, 136, 1000), (1, 1, 1), (130, 70, 2)])
+def test_fp32_variants_match_closed_form(gpu, name, M, N, K):
+    """Both fp32 kernels (0: sequential FMAs; 1: the fp32 MFMA, two K values
+    per step) at C1 and at ragged shapes (odd K, edges in M and N, a single
+    element), against the float64 product within C1's tolerance."""
+    import torch
+
+    kl = _kl()
+    d = mm_inputs(K, M, N, seed=3, dist="normal", dtype="float32")
+    out = kl.matmul_lhsT_rhs(_dev(d["lhs_T"], torch.float32, gpu), _dev(d["rhs"], torch.float32, gpu),
+                             cfg=kl.TileConfig.from_name(name))
+    expected = d["lhs_T"].astype(np.float64).T @ d["rhs"].astype(np.float64)
+    np.testing.assert_allclose(_host(out), expected, atol=F32_ATOL, rtol=F32_RTOL)
+
+
+def test_fp32_mfma_128cube_within_1e4(gpu):
+    """The fp32 MFMA kernel on the reference's own 128^3 check (atol=rtol=1e-4)."""
+    import torch
+
+    kl = _kl()
+    rng = np.random.default_rng(0)
+    lhs_T = rng.standard_normal((128, 128)).astype(np.float32)
+    rhs = rng.standard_normal((128, 128)).astype(np.float32)
+    for name in ("bm64_bn64_bk16_w4_s1_v1", "bm128_bn128_bk16_w4_s1_v1"):
+        out = kl.matmul_lhsT_rhs(_dev(lhs_T, torch.float32, gpu), _dev(rhs, torch.float32, gpu),
+                                 cfg=kl.TileConfig.from_name(name))
+        np.testing.assert_allclose(_host(out), lhs_T.T @ rhs, atol=1e-4, rtol=1e-4)
+
+
 def test_128cube_fp32_reference_procedure(gpu):
     """test/ops/test_direct_numpy_call.py:32-38: seed 0, 128^3, atol=rtol=1e-4."""
     import torch
