@@ -154,6 +154,15 @@ int mi_get_config(int kernel_id, int idx, mi_tile_cfg* cfg);
  * A negative size is MI_E_ARGS. */
 int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
 
+/* The default of rmsnorm_matmul for a call without gamma (what
+ * mi_rmsnorm_matmul_bf16 takes when cfg and gamma are both NULL):
+ * mi_default_config's pick, except that its 128x128, 64x128 and 64x64
+ * blocks go to the gamma-free variant 14 with the same block, unsplit.
+ * No counterpart in the reference, whose kernel has no gamma at all; for
+ * callers of its contract (rmsnorm_matmul_online).  A negative size is
+ * MI_E_ARGS. */
+int mi_default_config_no_gamma(int M, int N, int K, mi_tile_cfg* cfg);
+
 /* out[M,N] = lhsT[K,M]^T . rhs[K,N]; bf16 storage, fp32 accumulation over
  * the whole K (over each K part, then across parts in part order, when
  * cfg->split_k > 1), one round-to-nearest-even store.
@@ -184,7 +193,9 @@ int mi_matmul_lhsT_rhs_f32(const float* lhsT, const float* rhs, float* out, int 
  * bf16 storage, fp32 accumulation and fp32 row statistics.
  * gamma == NULL means gamma = 1, which is exactly the reference kernel
  * rmsnorm_matmul_online(lhs, rhs) with EPS = 1e-6
- * (reference kernel_library/rmsnorm_matmul/kernel_hand_online.py:195-353). */
+ * (reference kernel_library/rmsnorm_matmul/kernel_hand_online.py:195-353).
+ * cfg == NULL selects mi_default_config, or mi_default_config_no_gamma
+ * when gamma is NULL too; variant 14 with gamma is MI_E_TILE. */
 int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void* out, int M, int N,
                            int K, float eps, const mi_tile_cfg* cfg, void* stream);
 

@@ -505,6 +505,12 @@ int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
   return pick_default(kernel_id, M, N, K, cfg);
 }
 
+int mi_default_config_no_gamma(int M, int N, int K, mi_tile_cfg* cfg) {
+  if (!cfg) return fail(MI_E_ARGS, "null config");
+  if (M < 0 || N < 0 || K < 0) return fail(MI_E_ARGS, "negative size M=%d N=%d K=%d", M, N, K);
+  return mi::capi::pick_default_no_gamma(M, N, K, cfg);
+}
+
 int mi_matmul_lhsT_rhs_bf16(const void* lhsT, const void* rhs, void* out, int M, int N, int K,
                             const mi_tile_cfg* cfg, void* stream) {
   return mi::capi::matmul_lhsT_rhs_bf16(lhsT, rhs, out, M, N, K, cfg, stream, nullptr, 0);
@@ -561,6 +567,11 @@ int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void
   if (gamma && cfg && cfg->variant == 14)
     return fail(MI_E_TILE, "rmsnorm_matmul variant 14 computes the fused product without gamma; with gamma use "
                            "variant 0, 1, 4, 5, 11, 12 or 13");
+  mi_tile_cfg no_gamma_default;
+  if (!cfg && !gamma) {
+    mi::capi::pick_default_no_gamma(M, N, K, &no_gamma_default);
+    cfg = &no_gamma_default;
+  }
   mi::MiArgs a = {x, W, gamma, out, M, N, K, eps, 1.0f / (float)K, 8};
   return run(MI_KERNEL_RMSNORM_MATMUL_BF16, cfg, a, stream);
 }

@@ -31,6 +31,8 @@ bool splittable(int kernel_id, int variant);
 // The library default config at a shape (mi_default_config without its
 // argument checks; mi_defaults.hip).
 int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
+// The fused kernel's default for a call without gamma (mi_defaults.hip).
+int pick_default_no_gamma(int M, int N, int K, mi_tile_cfg* cfg);
 
 // The body of mi_matmul_lhsT_rhs_bf16.  fixed_ws == NULL: a call that needs
 // device workspace takes it from the library's stream-ordered pool;

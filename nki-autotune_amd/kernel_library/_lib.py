@@ -50,6 +50,7 @@ EXPORTED_SYMBOLS = (
     "mi_num_configs",
     "mi_get_config",
     "mi_default_config",
+    "mi_default_config_no_gamma",
     "mi_matmul_lhsT_rhs_bf16",
     "mi_matmul_lhsT_rhs_bf16_noalloc",
     "mi_matmul_lhs_rhs_bf16",
@@ -105,6 +106,7 @@ def _declare(lib: ctypes.CDLL) -> None:
         "mi_num_configs": (c_int, [c_int]),
         "mi_get_config": (c_int, [c_int, c_int, cfgp]),
         "mi_default_config": (c_int, [c_int, c_int, c_int, c_int, cfgp]),
+        "mi_default_config_no_gamma": (c_int, [c_int, c_int, c_int, cfgp]),
         "mi_matmul_lhsT_rhs_bf16": (c_int, [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, cfgp, c_void_p]),
         "mi_matmul_lhsT_rhs_bf16_noalloc": (
             c_int,

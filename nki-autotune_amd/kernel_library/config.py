@@ -206,19 +206,29 @@ def split_k_variants(func_name: str, grid: list[TileConfig], M: int, N: int) -> 
 def default_config(func_name: str, M: int, N: int, K: int) -> TileConfig:
     """Tuned config from ``tuned_configs.json`` if present for this shape, else the library default.
 
+    ``rmsnorm_matmul_online`` (the fused product without gamma) takes its own
+    tuned entry, else the gamma one, else ``mi_default_config_no_gamma``.
+
     Memoised per (name, shape) until the tuned table is reloaded: a call
     without a config pays a dict lookup, not a table scan and a library call."""
     key = (func_name, M, N, K)
     cfg = _DEFAULT_CACHE.get(key)
     if cfg is not None:
         return cfg
+    no_gamma = func_name == "rmsnorm_matmul_online"
     tuned = tuned_table().get(table_key(func_name, M, N, K))
+    if tuned is None and no_gamma:
+        # Every gamma variant also computes the product without gamma.
+        tuned = tuned_table().get(table_key("rmsnorm_matmul", M, N, K))
     if tuned is not None:
         cfg = TileConfig(**tuned)
     else:
         c = _lib.MiTileCfg()
-        _lib.check_rc(_lib.lib().mi_default_config(kernel_id(func_name), M, N, K, ctypes.byref(c)),
-                      "mi_default_config")
+        if no_gamma:
+            rc = _lib.lib().mi_default_config_no_gamma(M, N, K, ctypes.byref(c))
+        else:
+            rc = _lib.lib().mi_default_config(kernel_id(func_name), M, N, K, ctypes.byref(c))
+        _lib.check_rc(rc, "mi_default_config")
         cfg = TileConfig.from_c(c)
     _DEFAULT_CACHE[key] = cfg
     return cfg

@@ -27,7 +27,7 @@ import ctypes
 import torch
 
 from kernel_library import _lib
-from kernel_library.config import TileConfig, default_config, table_key, tuned_table
+from kernel_library.config import TileConfig, default_config
 
 EPS = 1e-6
 
@@ -159,10 +159,9 @@ def rmsnorm_matmul(
     else:
         _no_overlap(out, lhs=lhs, rhs=rhs, gamma=gamma)
     if cfg is None:
-        # Without gamma (the reference's contract) a no-gamma winner tuned for
-        # the shape takes precedence.
-        tuned = tuned_table().get(table_key("rmsnorm_matmul_online", M, N, K)) if gamma is None else None
-        cfg = TileConfig(**tuned) if tuned is not None else default_config("rmsnorm_matmul", M, N, K)
+        # Without gamma (the reference's contract) the no-gamma default: its
+        # own tuned winner for the shape first.
+        cfg = default_config("rmsnorm_matmul_online" if gamma is None else "rmsnorm_matmul", M, N, K)
     c = cfg.to_c()
     gptr = gamma.data_ptr() if gamma is not None else None
     with torch.cuda.device(lhs.device):

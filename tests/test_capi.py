@@ -342,6 +342,42 @@ def test_entry_points_reject_bad_arguments_before_any_gpu_call():
     assert L.mi_matmul_lhsT_rhs_bf16(a, b, o, 8192, 8192, 8192, ctypes.byref(bad), None) == _lib.MI_E_LDS
 
 
+def test_no_gamma_default():
+    """mi_default_config_no_gamma: the gamma default, except 128x128, 64x128
+    and 64x64 blocks (split or not) at M > 128 go to variant 14, unsplit;
+    always legal where the gamma default is."""
+    import random
+
+    from kernel_library.config import default_config
+
+    L = _lib.lib()
+
+    def pick(M, N, K, fn):
+        c = _lib.MiTileCfg()
+        assert (fn(M, N, K, ctypes.byref(c)) if fn is L.mi_default_config_no_gamma
+                else fn(RMS, M, N, K, ctypes.byref(c))) == _lib.MI_OK
+        return TileConfig.from_c(c)
+
+    assert pick(2048, 2048, 2048, L.mi_default_config_no_gamma).name == "bm128_bn128_bk64_w4_s3_v14"
+    assert pick(1024, 1024, 1024, L.mi_default_config_no_gamma).name == "bm128_bn128_bk64_w4_s3_v14"
+    assert pick(512, 4096, 4096, L.mi_default_config_no_gamma).name == "bm64_bn128_bk64_w4_s4_v14"
+    for shape in ((4096, 4096, 4096), (16, 28672, 8192), (128, 28672, 8192), (8192, 8192, 8192)):
+        assert pick(*shape, L.mi_default_config_no_gamma) == pick(*shape, L.mi_default_config), shape
+    rng = random.Random(5)
+    for _ in range(300):
+        M, N, K = rng.randint(1, 80) * 64, rng.randint(1, 80) * 64, rng.randint(1, 160) * 64
+        ng, g = pick(M, N, K, L.mi_default_config_no_gamma), pick(M, N, K, L.mi_default_config)
+        assert check("rmsnorm_matmul", ng, M, N, K)[0] == 0, (M, N, K, ng)
+        assert ng == g or (ng.variant == 14 and (ng.block_m, ng.block_n) == (g.block_m, g.block_n)), (M, N, K)
+    c = _lib.MiTileCfg()
+    assert L.mi_default_config_no_gamma(-1, 8, 8, ctypes.byref(c)) == _lib.MI_E_ARGS
+    assert L.mi_default_config_no_gamma(8, 8, 8, None) == _lib.MI_E_ARGS
+    # The Python host: the no-gamma tuned entry, else the gamma one, else this default.
+    assert default_config("rmsnorm_matmul_online", 2048, 2048, 2048).variant == 14
+    assert default_config("rmsnorm_matmul_online", 16, 28672, 8192) == default_config("rmsnorm_matmul", 16, 28672, 8192)
+    assert default_config("rmsnorm_matmul_online", 1024, 1024, 1024).name == "bm128_bn128_bk64_w4_s3_v14"
+
+
 def test_gamma_free_variant_rejects_gamma_before_any_gpu_call():
     """rmsnorm_matmul variant 14 computes the product without gamma: a call
     with gamma is refused with MI_E_TILE on the host, and the sweep of a

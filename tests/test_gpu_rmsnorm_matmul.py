@@ -238,6 +238,35 @@ def test_no_gamma_variant14_identity_weight(gpu):
         assert _ok(rep), (name, rep)
 
 
+@pytest.mark.parametrize("M,K,N", [(1024, 1024, 1024), (512, 4096, 4096), (200, 264, 136)])
+def test_no_gamma_default_calls(gpu, M, K, N):
+    """Calls without gamma and without a config: the Python host's default
+    (rmsnorm_matmul_online) and the C ABI's own (cfg = NULL, gamma = NULL:
+    mi_default_config_no_gamma, variant 14 at these shapes), every output
+    against the closed form; both defaults run the same config, so the two
+    outputs are bitwise equal."""
+    import ctypes
+
+    import torch
+
+    import kernel_library as kl
+    from kernel_library import _lib
+
+    d = rms_inputs(M, K, N, seed=21, with_gamma=False)
+    x, w = _dev(d["lhs"], gpu), _dev(d["rhs"], gpu)
+    a = kl.rmsnorm_matmul_online(x, w)
+    b = torch.empty_like(a)
+    rc = _lib.lib().mi_rmsnorm_matmul_bf16(x.data_ptr(), None, w.data_ptr(), b.data_ptr(), M, N, K,
+                                           ctypes.c_float(kl.EPS), None,
+                                           torch.cuda.current_stream(gpu).cuda_stream)
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    rep = rms_check(_host(a), orms.closed_form(d["lhs"], d["rhs"]))
+    print(M, K, N, kl.default_config("rmsnorm_matmul_online", M, N, K).name, rep, flush=True)
+    assert _ok(rep), rep
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 def test_skinny_decode_shape(gpu):
     """Decode-sized M (16 rows) against an 8192 x 28672 W: the non-temporal-W
     variants 11 / 12 and the default config, every row vs the closed form."""
