@@ -619,10 +619,13 @@ int mi_release_workspace(void) {
   for (const auto& kv : g_pools) {
     // The runtime hands memory freed by hipFreeAsync back to its pool at the
     // pool's next allocation, not at a synchronisation: one small
-    // allocation and free, completed, makes the earlier frees trimmable.
+    // allocation makes the earlier frees trimmable.  It may be carved out
+    // of the block just freed, so it is freed with hipFree (synchronous,
+    // at once) rather than hipFreeAsync (pending until the next allocation,
+    // which would keep that whole block from the trim).
     void* p = nullptr;
     if ((e = hipSetDevice(kv.first)) != hipSuccess || (e = hipMallocFromPoolAsync(&p, 256, kv.second, nullptr)) != hipSuccess ||
-        (e = hipFreeAsync(p, nullptr)) != hipSuccess || (e = hipStreamSynchronize(nullptr)) != hipSuccess ||
+        (e = hipStreamSynchronize(nullptr)) != hipSuccess || (e = hipFree(p)) != hipSuccess ||
         (e = hipMemPoolTrimTo(kv.second, 0)) != hipSuccess) {
       rc = hip_fail(e, "releasing the workspace pool");
       break;

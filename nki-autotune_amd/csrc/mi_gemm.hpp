@@ -1134,51 +1134,56 @@ __device__ __forceinline__ void sk_take_slot(f32x16_t (&s)[TM][TN], const float*
       }
 }
 
-// The combine of tile t: acc = ((p_0 + p_1) + ...) + p_n.  The checker
-// (last_in_regs) holds p_n in acc and the storers' parts come from their
-// slots; a storer that combines takes every part from the slots, its own
-// included (stored, and drained, before its counter update).  Both add in
-// the same order, so the bits are the same.
+// The combine of tile t: acc = ((p_0 + p_1) + ...) + p_n, where p_0 is in
+// the tile's first slot and p_e (e = 1 .. n) in later slot `base + e`.  The
+// checker (last_in_regs) holds p_n in acc and the storers' parts come from
+// their slots; a storer that combines takes every part from the slots, its
+// own included (stored, and drained, before its counter update).  Both add
+// in the same order, so the bits are the same.  One 16-byte quad at a time:
+// no second copy of the accumulators.
 template <int BM, int BN, int TM, int TN>
-__device__ __forceinline__ void sk_combine(f32x16_t (&acc)[TM][TN], const StreamKWs& ws, int t, int fw, int n,
+__device__ __forceinline__ void sk_combine(f32x16_t (&acc)[TM][TN], const StreamKWs& ws, int t, int base, int n,
                                            bool last_in_regs, int wave, int lane) {
   const size_t slot = (size_t)BM * BN;
-  f32x16_t s[TM][TN];
-  sk_take_slot<TM, TN, false>(s, ws.first + (size_t)t * slot, slot, wave, lane);
-  for (int e = 1; e < n; ++e) sk_take_slot<TM, TN, true>(s, ws.later + (size_t)(fw + e) * slot, slot, wave, lane);
-  if (!last_in_regs) sk_take_slot<TM, TN, false>(acc, ws.later + (size_t)(fw + n) * slot, slot, wave, lane);
+  const __amdgpu_buffer_rsrc_t r0 = make_rsrc(ws.first + (size_t)t * slot, (uint32_t)slot * 4u);
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
-    for (int j = 0; j < TN; ++j) acc[i][j] = s[i][j] + acc[i][j];
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const uint32_t off = sk_slot_off<TM, TN>(wave, i, j, q, lane);
+        f32x4_t v = sk_load4(r0, off);
+        for (int e = 1; e < n; ++e)
+          v += sk_load4(make_rsrc(ws.later + (size_t)(base + e) * slot, (uint32_t)slot * 4u), off);
+        f32x4_t last;
+        if (last_in_regs) {
+          last = f32x4_t{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
+        } else {
+          last = sk_load4(make_rsrc(ws.later + (size_t)(base + n) * slot, (uint32_t)slot * 4u), off);
+        }
+        v = v + last;
+#pragma unroll
+        for (int x = 0; x < 4; ++x) acc[i][j][4 * q + x] = v[x];
+      }
 }
 
 // s_waitcnt vmcnt(0) that the compiler may not move memory operations across.
 __device__ __forceinline__ void sk_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// Epilogue of one stream-K segment: K tiles [kb, ke) of tile t, computed by
-// workgroup w.  A whole tile is stored; a part runs the protocol of
-// mi_streamk.hpp and, if it is the one that combines, stores the tile.
-// `bcast` is an LDS word for thread 0's atomic results.
+// The protocol of mi_streamk.hpp for one part of tile t split into n + 1
+// parts: `mine` is the part's slot (the tile's first slot for p_0, a later
+// slot otherwise), later slot base + e holds p_e, and `is_last` marks the
+// checker p_n.  The part that combines stores the tile.  `bcast` is an LDS
+// word for thread 0's atomic results.
 template <int BM, int BN, int WAVES, int TM, int TN>
-__device__ __forceinline__ void sk_epilogue(f32x16_t (&acc)[TM][TN], const StreamKPlan& plan, const StreamKWs& ws,
-                                            int w, int t, int kb, int ke, char* smem, int* bcast, int wave,
-                                            int lane, uint16_t* __restrict__ out, int M, int N, int row0,
-                                            int col0) {
-  float one[TM];
-#pragma unroll
-  for (int i = 0; i < TM; ++i) one[i] = 1.0f;
-  if (kb == 0 && ke == plan.kt) {
-    store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, row0, col0);
-    return;
-  }
+__device__ __forceinline__ void sk_part_epilogue(f32x16_t (&acc)[TM][TN], const StreamKWs& ws, int t, float* mine,
+                                                 int base, int n, bool is_last, char* smem, int* bcast, int wave,
+                                                 int lane, uint16_t* __restrict__ out, int M, int N, int row0,
+                                                 int col0) {
   const int tid = wave * 64 + lane;
-  const int fw = (int)plan.first_wg(t);
-  const int n = (int)plan.later_parts(t);
-  const size_t slot = (size_t)BM * BN;
-  float* mine = kb == 0 ? ws.first + (size_t)t * slot : ws.later + (size_t)w * slot;
-  bool combine, last_in_regs;
-  if (ke < plan.kt) {
+  bool combine;
+  if (!is_last) {
     // A storer.
     sk_store_slot<BM, BN, TM, TN>(acc, mine, wave, lane);
     sk_drain();
@@ -1187,7 +1192,6 @@ __device__ __forceinline__ void sk_epilogue(f32x16_t (&acc)[TM][TN], const Strea
     __syncthreads();
     const int old = *bcast;
     combine = (old & kSkLastReady) != 0 && (old & kSkStoredMask) == n - 1;
-    last_in_regs = false;
   } else {
     // The checker.
     if (tid == 0)
@@ -1206,13 +1210,36 @@ __device__ __forceinline__ void sk_epilogue(f32x16_t (&acc)[TM][TN], const Strea
       old = *bcast;
       combine = (old & kSkStoredMask) == n;
     }
-    last_in_regs = true;
   }
   if (!combine) return;
   // Every part has arrived: reset the counter for the next launch.
   if (tid == 0) __hip_atomic_store(ws.ctr + t, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-  sk_combine<BM, BN, TM, TN>(acc, ws, t, fw, n, last_in_regs, wave, lane);
+  sk_combine<BM, BN, TM, TN>(acc, ws, t, base, n, is_last, wave, lane);
+  float one[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) one[i] = 1.0f;
   store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, row0, col0);
+}
+
+// Epilogue of one stream-K segment: K tiles [kb, ke) of tile t, computed by
+// workgroup w.  A whole tile is stored; a part runs the protocol (its later
+// slot is workgroup w's own, p_e's is that of workgroup first_wg(t) + e).
+template <int BM, int BN, int WAVES, int TM, int TN>
+__device__ __forceinline__ void sk_epilogue(f32x16_t (&acc)[TM][TN], const StreamKPlan& plan, const StreamKWs& ws,
+                                            int w, int t, int kb, int ke, char* smem, int* bcast, int wave,
+                                            int lane, uint16_t* __restrict__ out, int M, int N, int row0,
+                                            int col0) {
+  if (kb == 0 && ke == plan.kt) {
+    float one[TM];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) one[i] = 1.0f;
+    store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, row0, col0);
+    return;
+  }
+  const size_t slot = (size_t)BM * BN;
+  float* mine = kb == 0 ? ws.first + (size_t)t * slot : ws.later + (size_t)w * slot;
+  sk_part_epilogue<BM, BN, WAVES>(acc, ws, t, mine, (int)plan.first_wg(t), (int)plan.later_parts(t), ke == plan.kt,
+                                  smem, bcast, wave, lane, out, M, N, row0, col0);
 }
 
 // The stream-K kernel: gridDim.x workgroups (the host launches
