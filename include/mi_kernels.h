@@ -125,8 +125,10 @@ enum {
  *                    without gamma only (gamma != NULL: MI_E_TILE): the
  *                    matmul_lhs_rhs core reads x once, LDS-direct, sums its
  *                    rows' squares from the MFMA A fragments (bf16 dot2)
- *                    and applies 1/rms to its fp32 accumulators.  Variants
- *                    2, 3 and 6..10 do not exist (MI_E_TILE).
+ *                    and applies 1/rms to its fp32 accumulators; 16 as 14
+ *                    on the paired-load core of matmul_lhs_rhs variant 1
+ *                    (block_k 32 or 64; without gamma only).  Variants
+ *                    2, 3, 6..10 and 15 do not exist (MI_E_TILE).
  */
 typedef struct {
   int block_m, block_n, block_k, waves, lds_stages, split_k, group_m, variant;
@@ -156,8 +158,9 @@ int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
 
 /* The default of rmsnorm_matmul for a call without gamma (what
  * mi_rmsnorm_matmul_bf16 takes when cfg and gamma are both NULL):
- * mi_default_config's pick, except that its 128x128, 64x128 and 64x64
- * blocks go to the gamma-free variant 14 with the same block, unsplit.
+ * mi_default_config's pick, except that its 128x128 blocks go to the
+ * gamma-free variant 16 (block_k 32, 4 stages) and its 64x128 and 64x64
+ * blocks to variant 14 with the same block, all unsplit.
  * No counterpart in the reference, whose kernel has no gamma at all; for
  * callers of its contract (rmsnorm_matmul_online).  A negative size is
  * MI_E_ARGS. */
@@ -195,7 +198,7 @@ int mi_matmul_lhsT_rhs_f32(const float* lhsT, const float* rhs, float* out, int 
  * rmsnorm_matmul_online(lhs, rhs) with EPS = 1e-6
  * (reference kernel_library/rmsnorm_matmul/kernel_hand_online.py:195-353).
  * cfg == NULL selects mi_default_config, or mi_default_config_no_gamma
- * when gamma is NULL too; variant 14 with gamma is MI_E_TILE. */
+ * when gamma is NULL too; variant 14 or 16 with gamma is MI_E_TILE. */
 int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void* out, int M, int N,
                            int K, float eps, const mi_tile_cfg* cfg, void* stream);
 

@@ -69,6 +69,8 @@ def _instance(fam: str, cfg) -> tuple[str, str, str] | None:
             return "MI_RMS2_INST", "MI_RMS2_ROW", f"{base}, {s}"
         if v == 14:
             return "MI_RMSQ_INST", "MI_RMSQ_ROW", f"{base}, {s}"
+        if v == 16:
+            return "MI_RMSQP_INST", "MI_RMSQP_ROW", f"{base}, {s}"
     return None
 
 

@@ -51,7 +51,7 @@ class Atom(NamedTuple):
 
 
 # Variants of each family that compute the same function (include/mi_kernels.h);
-# rmsnorm_matmul 14 is left out: it computes the product without gamma only.
+# rmsnorm_matmul 14 and 16 are left out: they compute the product without gamma only.
 FAMILY_VARIANTS = {
     "matmul_lhsT_rhs": (0, 1, 2, 3, 4, 5, 6),
     "matmul_lhs_rhs": (0, 1, 2),

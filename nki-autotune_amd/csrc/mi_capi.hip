@@ -138,6 +138,7 @@ mi::Legal template_legal(int kernel_id, const mi_tile_cfg& c) {
       if (c.variant == 11 || c.variant == 12) return mi::legal_rms_xreg(bm, bn, bk, w, s, c.variant - 9);
       if (c.variant == 13) return mi::legal_rms2(bm, bn, bk, w, s);
       if (c.variant == 14) return mi::legal_mm_pipe(bm, bn, bk, w, s, true);
+      if (c.variant == 16) return mi::legal_lhs_pair(bm, bn, bk, w, s);
       break;
     case MI_KERNEL_MATMUL_LHST_RHS_F32:
       // 16 x 16 threads with 4 x 4 outputs each, K slices of 16 or 32.
@@ -564,9 +565,9 @@ int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void
   if (overlaps(out, ob, x, (size_t)M * K * 2) || overlaps(out, ob, W, (size_t)K * N * 2) ||
       overlaps(out, ob, gamma, (size_t)K * 2))
     return fail(MI_E_ARGS, "out overlaps an input");
-  if (gamma && cfg && cfg->variant == 14)
-    return fail(MI_E_TILE, "rmsnorm_matmul variant 14 computes the fused product without gamma; with gamma use "
-                           "variant 0, 1, 4, 5, 11, 12 or 13");
+  if (gamma && cfg && (cfg->variant == 14 || cfg->variant == 16))
+    return fail(MI_E_TILE, "rmsnorm_matmul variants 14 and 16 compute the fused product without gamma; with gamma "
+                           "use variant 0, 1, 4, 5, 11, 12 or 13");
   mi_tile_cfg no_gamma_default;
   if (!cfg && !gamma) {
     mi::capi::pick_default_no_gamma(M, N, K, &no_gamma_default);

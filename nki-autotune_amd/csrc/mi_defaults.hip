@@ -304,21 +304,29 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
 
 // The fused kernel's default for a call without gamma: pick_default's
 // choice, except that its 128x128, 64x128 and 64x64 blocks (shapes of one
-// or two rounds of tiles, split or not) go to the gamma-free variant 14 with
-// the same block, unsplit.  Measured in interleaved rounds against the
-// default (no gamma): 0.60 x its time at 1024^3 (against the 4-part split),
-// 0.89 x at 2048^3, 0.90 x at 1024x4096x4096, 0.80 x at 512x4096x4096, 0.78 x
-// at 256x8192x2048; the larger blocks (128x512, 256x256 two-pass, 128x256)
-// stay, variant 14 being 0-8 % slower there.  Skinny M keeps its
-// non-temporal variants.
+// or two rounds of tiles, split or not) go to a gamma-free variant with the
+// same block, unsplit: 128x128 to variant 16 (block_k 32, 4 stages), the
+// others to variant 14.  Variant 14 measured in interleaved rounds against
+// the default (no gamma): 0.60 x its time at 1024^3 (against the 4-part
+// split), 0.89 x at 2048^3, 0.90 x at 1024x4096x4096, 0.80 x at
+// 512x4096x4096, 0.78 x at 256x8192x2048; variant 16 at 128x128, against
+// variant 14's 128x128 block: 0.924-0.957 x (median 0.938) at twelve shapes
+// this rule gives it, from 256x512x2048 to 4096x512x1024, with bitwise equal
+// outputs.  The larger blocks (128x512, 256x256 two-pass, 128x256) stay,
+// variant 14 being 0-8 % slower there.  Skinny M keeps its non-temporal
+// variants.
 int pick_default_no_gamma(int M, int N, int K, mi_tile_cfg* cfg) {
   const int rc = pick_default(MI_KERNEL_RMSNORM_MATMUL_BF16, M, N, K, cfg);
   if (rc != MI_OK) return rc;
   const int v = cfg->variant, bm = cfg->block_m, bn = cfg->block_n;
   const bool one_pass_or_two = v == 4 || v == 5 || v == 13;
   const bool small_block = (bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64);
-  if (M > 128 && one_pass_or_two && small_block)
-    *cfg = {bm, bn, 64, 4, bm == 128 ? 3 : 4, 1, cfg->group_m, 14};
+  if (M > 128 && one_pass_or_two && small_block) {
+    if (bm == 128)
+      *cfg = {128, 128, 32, 4, 4, 1, cfg->group_m, 16};
+    else
+      *cfg = {bm, bn, 64, 4, 4, 1, cfg->group_m, 14};
+  }
   return MI_OK;
 }
 

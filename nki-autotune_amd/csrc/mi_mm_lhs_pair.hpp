@@ -25,6 +25,16 @@
 // A pair for every even tile among t+2 .. t+STAGES-1.  The loop is unrolled
 // over lcm(STAGES, 2*NP) tiles, so stage, pair buffer, tile half and wait
 // counts are compile-time constants in every tile body.
+//
+// SQ (rmsnorm_matmul variant 16, the fused product without gamma on this
+// core, as variant 14 is on the per-tile core): x is the A operand, loaded
+// unscaled, and each wave also sums its rows' squares from the A fragments
+// its MFMAs consume (v_dot2c_f32_bf16: exact bf16 products, fp32 sums).
+// Sub-step s = t*KS + kk of the K loop goes to wave column s % WN; a round
+// holds a multiple of WN sub-steps, so inside the unrolled round the choice
+// is a compile-time constant, and the K loop is compiled once per wave
+// column.  The epilogue adds the wave columns' sums through LDS and scales
+// output row m by 1/sqrt(sum_m / K + eps).
 #pragma once
 #include <numeric>
 
@@ -51,11 +61,10 @@ constexpr int count_even(int lo, int hi) {
   return n;
 }
 
-template <int BM, int BN, int BK, int WAVES, int STAGES>
-__global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pair_kernel(const uint16_t* __restrict__ lhs,
-                                                                         const uint16_t* __restrict__ rhs,
-                                                                         uint16_t* __restrict__ out, int M, int N,
-                                                                         int K, int group_m) {
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool SQ>
+__device__ __forceinline__ void mm_lhs_pair_body(const uint16_t* __restrict__ lhs, const uint16_t* __restrict__ rhs,
+                                                 uint16_t* __restrict__ out, int M, int N, int K, int group_m,
+                                                 char* smem, float inv_k, float eps) {
   using C = PairCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
   static_assert(legal_lhs_pair(BM, BN, BK, WAVES, STAGES).code == MI_OK, "illegal tile config (mi_legal.hpp)");
@@ -69,7 +78,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pair_kernel(const 
   constexpr int NLA = LA::LOADS_PER_TILE, NLB = LB::LOADS_PER_TILE;
   // vm_wait<n> counts assume every wave issues the same number of loads.
   static_assert(LA::EVEN && LB::EVEN, "every wave issues the same number of loads");
-  __shared__ __attribute__((aligned(1024))) char smem[C::LDS_BYTES];
+  static_assert(!SQ || G::WN * BM * 4 <= C::LDS_BYTES, "row sums of squares exchanged through LDS");
 
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63;
@@ -136,6 +145,34 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pair_kernel(const 
       for (int j = 0; j < TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bf[buf][j], af[buf][i], acc[i][j], 0, 0, 0);
   };
+  float sq[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) sq[i] = 0.0f;
+  const int wcol = wave % G::WN;
+  // SQ: the rows' squares of the A fragments in register set `buf`.  Pair d
+  // of a fragment is taken as a shuffle with constant indices (a bf16x2
+  // bit-cast from dword d of the fragment viewed as u32x4 is compiled as
+  // dword 0 for every d by this hipcc).
+  auto squares = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      static_for<4>([&](auto d_c) __attribute__((always_inline)) {
+        constexpr int d = decltype(d_c)::value;
+        const bf16x2_t v = __builtin_shufflevector(af[buf][i], af[buf][i], 2 * d, 2 * d + 1);
+        sq[i] = __builtin_amdgcn_fdot2_f32_bf16(v, v, sq[i], false);
+      });
+  };
+  // The MFMAs of one sub-step, with this wave's squares when `mine`, and
+  // their scheduling against the LDS reads (and the dot2 VALU work).
+  auto step = [&](int buf, auto mine_c) __attribute__((always_inline)) {
+    mfmas(buf);
+    if constexpr (SQ && decltype(mine_c)::value) {
+      squares(buf);
+      interleave_mfma_mix<TM * TN, 2 * NF, 4 * TM, 0>();
+    } else {
+      interleave_mfma_ds<TM * TN, 2 * NF>();
+    }
+  };
   // Tiles and pairs past the end are clamped to the last one (re-read into
   // a buffer that is never consumed), so every group has a static size.
   auto clamp = [&](int kt) { return kt < KT ? kt : KT - 1; };
@@ -165,18 +202,23 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pair_kernel(const 
 
   // Tile t = t0 + I of a round (t0 a multiple of the round length, so even).
   constexpr int UR = std::lcm(STAGES, 2 * NP);
-  auto tile = [&](int t, auto i_c) __attribute__((always_inline)) {
+  static_assert((UR * KS) % G::WN == 0, "a round holds whole turns of the wave columns");
+  // Whether sub-step kk of round tile I is squared by wave column WC.
+  auto mine = [](auto i_c, auto kk_c, auto wc_c) {
+    return std::integral_constant<bool, (decltype(i_c)::value * KS + decltype(kk_c)::value) % G::WN ==
+                                            decltype(wc_c)::value>{};
+  };
+  auto tile = [&](int t, auto i_c, auto wc_c) __attribute__((always_inline)) {
     constexpr int I = decltype(i_c)::value;
     constexpr int cur = I % STAGES, pb = (I / 2) % NP, h = I % 2;
     constexpr int nxt = (I + 1) % STAGES, npb = ((I + 1) / 2) % NP, nh = (I + 1) % 2;
     constexpr int WAIT = (STAGES - 2) * NLB + NLA * count_even(I + 2, I + STAGES - 1);
     constexpr int NI = NLB + ((I + STAGES) % 2 == 0 ? NLA : 0);  // loads of the group issued here
-#pragma unroll
-    for (int kk = 0; kk + 1 < KS; ++kk) {
+    static_for<KS - 1>([&](auto kk_c) __attribute__((always_inline)) {
+      constexpr int kk = decltype(kk_c)::value;
       read_frags(cur, pb, h, kk + 1, (kk + 1) & 1);
-      mfmas(kk & 1);
-      interleave_mfma_ds<TM * TN, 2 * NF>();
-    }
+      step(kk & 1, mine(i_c, kk_c, wc_c));
+    });
     vm_wait<WAIT>();
     __syncthreads();
 #pragma unroll
@@ -185,33 +227,90 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pair_kernel(const 
 #pragma unroll
       for (int q = f * NI / NF; q < (f + 1) * NI / NF; ++q) issue_one(q, t + STAGES);
     }
-    mfmas((KS - 1) & 1);
-    interleave_mfma_ds<TM * TN, 2 * NF>();
+    step((KS - 1) & 1, mine(i_c, std::integral_constant<int, KS - 1>{}, wc_c));
   };
-  int t0 = 0;
-  for (; t0 + UR < KT; t0 += UR)
-    static_for<UR>([&](auto i_c) __attribute__((always_inline)) { tile(t0 + i_c(), i_c); });
-  static_while<UR>([&](auto i_c) __attribute__((always_inline)) {
-    if (t0 + i_c() + 1 >= KT) return false;
-    tile(t0 + i_c(), i_c);
-    return true;
-  });
-  // Last tile: no further loads.
-  const int tl = KT - 1;
-  const int cur = tl % STAGES, pb = (tl / 2) % NP, h = tl % 2;
-#pragma unroll
-  for (int kk = 0; kk < KS; ++kk) {
-    if (kk + 1 < KS) read_frags(cur, pb, h, kk + 1, (kk + 1) & 1);
-    mfmas(kk & 1);
-    interleave_mfma_ds<TM * TN, 2 * NF>();
+  // The K loop for wave column WC (SQ: one copy per column, each wave runs
+  // its own; otherwise one copy).
+  auto k_loop = [&](auto wc_c) __attribute__((always_inline)) {
+    int t0 = 0;
+    for (; t0 + UR < KT; t0 += UR)
+      static_for<UR>([&](auto i_c) __attribute__((always_inline)) { tile(t0 + i_c(), i_c, wc_c); });
+    static_while<UR>([&](auto i_c) __attribute__((always_inline)) {
+      if (t0 + i_c() + 1 >= KT) return false;
+      tile(t0 + i_c(), i_c, wc_c);
+      return true;
+    });
+    // Last tile: no further loads.  It is tile I = tl - t0 of its round,
+    // known only at run time, so its squares go by a wave-uniform test.
+    const int tl = KT - 1;
+    const int cur = tl % STAGES, pb = (tl / 2) % NP, h = tl % 2;
+    static_for<KS>([&](auto kk_c) __attribute__((always_inline)) {
+      constexpr int kk = decltype(kk_c)::value;
+      if (kk + 1 < KS) read_frags(cur, pb, h, kk + 1, (kk + 1) & 1);
+      mfmas(kk & 1);
+      if constexpr (SQ) {
+        if ((tl * KS + kk) % G::WN == decltype(wc_c)::value) squares(kk & 1);
+      }
+      interleave_mfma_ds<TM * TN, 2 * NF>();
+    });
+  };
+  if constexpr (SQ && G::WN > 1) {
+    static_for<G::WN>([&](auto wc_c) __attribute__((always_inline)) {
+      if (wcol == decltype(wc_c)::value) k_loop(wc_c);
+    });
+  } else {
+    k_loop(std::integral_constant<int, 0>{});
   }
   wait_vmem();
   __syncthreads();  // the epilogue reuses the panel buffers
 
-  float one[TM];
+  float scale[TM];
+  if constexpr (SQ) {
+    // Lanes l and l^32 hold the two K halves of one row's sum; the WN waves
+    // of a wave row then add theirs through LDS [WN][BM], in column order.
+    float* xs = (float*)smem;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) one[i] = 1.0f;
-  store_tile<TM, TN, WAVES>(acc, one, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
+    for (int i = 0; i < TM; ++i) {
+      const float t = sq[i] + __shfl_xor(sq[i], 32);
+      if (lane < 32) xs[wcol * BM + wm0 + i * 32 + lane] = t;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int r = wm0 + i * 32 + (lane & 31);
+      float t = xs[r];
+#pragma unroll
+      for (int c = 1; c < G::WN; ++c) t += xs[c * BM + r];
+      scale[i] = 1.0f / __builtin_sqrtf(t * inv_k + eps);
+    }
+    __syncthreads();  // store_tile reuses the same LDS
+  } else {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) scale[i] = 1.0f;
+  }
+  store_tile<TM, TN, WAVES>(acc, scale, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
+}
+
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+__global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pair_kernel(const uint16_t* __restrict__ lhs,
+                                                                         const uint16_t* __restrict__ rhs,
+                                                                         uint16_t* __restrict__ out, int M, int N,
+                                                                         int K, int group_m) {
+  __shared__ __attribute__((aligned(1024))) char smem[PairCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
+  mm_lhs_pair_body<BM, BN, BK, WAVES, STAGES, false>(lhs, rhs, out, M, N, K, group_m, smem, 0.0f, 0.0f);
+}
+
+// Fused out[M,N] = (x[M,K] / sqrt(mean_k x^2 + eps)) . W[K,N] without gamma
+// (rmsnorm_matmul variant 16): the paired-load core with the rows' squares
+// (SQ above).
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+__global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_sq_pair_kernel(const uint16_t* __restrict__ x,
+                                                                            const uint16_t* __restrict__ w,
+                                                                            uint16_t* __restrict__ out, int M,
+                                                                            int N, int K, int group_m, float eps,
+                                                                            float inv_k) {
+  __shared__ __attribute__((aligned(1024))) char smem[PairCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
+  mm_lhs_pair_body<BM, BN, BK, WAVES, STAGES, true>(x, w, out, M, N, K, group_m, smem, inv_k, eps);
 }
 
 }  // namespace mi

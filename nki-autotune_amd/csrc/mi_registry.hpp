@@ -276,6 +276,16 @@ hipError_t launch_rms_sq(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Fused kernel without gamma on the paired-load K-contiguous core (variant
+// 16): one launch, as variant 14.
+template <int BM, int BN, int BK, int W, int S>
+hipError_t launch_rms_sq_pair(const MiArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((rmsnorm_mm_bf16_sq_pair_kernel<BM, BN, BK, W, S>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                     dim3(W * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K,
+                     a.group_m, a.eps, a.inv_k);
+  return hipGetLastError();
+}
+
 // Explicit instantiation of one config's kernel (namespace scope); every
 // table row needs its kernel instantiated in the same translation unit so
 // the host launch stub is emitted there.
@@ -359,6 +369,11 @@ hipError_t launch_rms_sq(const MiArgs& a, hipStream_t s) {
 #define MI_RMSQ_INST(BM, BN, BK, W, S)                                                                     \
   template __global__ void rmsnorm_mm_bf16_sq_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*, \
                                                                        uint16_t*, int, int, int, int, float, float);
+// Variant 16: the fused kernel without gamma on the paired-load core.
+#define MI_RMSQP_INST(BM, BN, BK, W, S)                                                                       \
+  template __global__ void rmsnorm_mm_bf16_sq_pair_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*, \
+                                                                            uint16_t*, int, int, int, int,     \
+                                                                            float, float);
 
 // Table rows.
 #define MI_MM_ROW(BM, BN, BK, W, S)                                                                  \
@@ -415,6 +430,9 @@ hipError_t launch_rms_sq(const MiArgs& a, hipStream_t s) {
 #define MI_RMSQ_ROW(BM, BN, BK, W, S)                                                                  \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 14}, PipeCfg<BM, BN, BK, W, S>::LDS_BYTES, \
    &launch_rms_sq<BM, BN, BK, W, S>},
+#define MI_RMSQP_ROW(BM, BN, BK, W, S)                                                                 \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 16}, PairCfg<BM, BN, BK, W, S>::LDS_BYTES, \
+   &launch_rms_sq_pair<BM, BN, BK, W, S>},
 
 #define MI_RMS2_ROW(BM, BN, BK, W, S)                                                               \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 13}, lds_rms2(BM, BN, BK, W, S),         \

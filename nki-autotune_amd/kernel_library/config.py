@@ -171,8 +171,8 @@ def legal_configs(func_name: str, M: int, N: int, K: int, grid: list[TileConfig]
 
 
 # Fused variants that compute the product without gamma only (the C ABI
-# rejects them with a gamma): rmsnorm_matmul 14.
-GAMMA_FREE_VARIANTS = {"rmsnorm_matmul": (14,), "rmsnorm_matmul_online": (14,)}
+# rejects them with a gamma): rmsnorm_matmul 14 and 16.
+GAMMA_FREE_VARIANTS = {"rmsnorm_matmul": (14, 16), "rmsnorm_matmul_online": (14, 16)}
 
 
 # Stream-K variants (mi_streamk.hpp): lhsT.rhs 5 (rhs cached) and 6 (rhs non-temporal).

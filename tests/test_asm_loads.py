@@ -97,8 +97,8 @@ def test_kernels_straight_line(unit, asm_of):
 
 
 def test_row_square_sums_read_every_pair_of_the_fragment(asm_of):
-    """The fused kernel without gamma (rmsnorm_matmul variant 14) sums the
-    squares of each A fragment's four bf16 pairs with four dependent
+    """The fused kernels without gamma (rmsnorm_matmul variants 14 and 16)
+    sum the squares of each A fragment's four bf16 pairs with four dependent
     v_dot2c_f32_bf16 into one accumulator.  Each such chain must read four
     different registers (the fragment's dwords): a bit-cast of the
     fragment's dword d to bf16x2 was compiled as dword 0 for every d."""
@@ -107,8 +107,9 @@ def test_row_square_sums_read_every_pair_of_the_fragment(asm_of):
     ks = kernels(asm_of("rms_bf16_sq.hip"))
     assert ks
     dot2 = re.compile(r"^\s*v_dot2c_f32_bf16(?:_e32)?\s+v(\d+),\s*v(\d+),\s*v(\d+)")
-    ks = {name: lines for name, lines in ks.items() if "rmsnorm_mm_bf16_sq_kernel" in name}
-    assert ks
+    ks = {name: lines for name, lines in ks.items()
+          if "rmsnorm_mm_bf16_sq_kernel" in name or "rmsnorm_mm_bf16_sq_pair_kernel" in name}
+    assert any("sq_pair_kernel" in n for n in ks) and any("sq_kernel" in n and "pair" not in n for n in ks)
     for name, lines in ks.items():
         per_acc: dict[int, list[int]] = {}
         for ln in lines:

@@ -151,6 +151,11 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (RMS, TileConfig(128, 128, 64, 4, 3, variant=14), (2048, 2048, 2044), _lib.MI_E_ALIGN),   # K % 8
         (RMS, TileConfig(128, 128, 64, 4, 1, variant=14), (2048, 2048, 2048), _lib.MI_E_TILE),    # pipelined core
         (RMS, TileConfig(128, 128, 64, 4, 3, split_k=2, variant=14), (512, 512, 8192), _lib.MI_E_SPLIT),
+        # variant 16: the paired-load core's legality (block_k 32 or 64, whole pair loads per wave)
+        (RMS, TileConfig(256, 256, 32, 8, 3, variant=16), (4096, 4096, 4096), _lib.MI_OK),
+        (RMS, TileConfig(256, 256, 32, 8, 3, variant=16), (4096, 4096, 4092), _lib.MI_E_ALIGN),   # K % 8
+        (RMS, TileConfig(128, 128, 128, 4, 3, variant=16), (2048, 2048, 2048), _lib.MI_E_TILE),   # block_k 128
+        (RMS, TileConfig(128, 128, 32, 4, 4, split_k=2, variant=16), (512, 512, 8192), _lib.MI_E_SPLIT),
     ],
 )
 def test_cfg_check_codes(kid, cfg, shape, code):
@@ -343,9 +348,10 @@ def test_entry_points_reject_bad_arguments_before_any_gpu_call():
 
 
 def test_no_gamma_default():
-    """mi_default_config_no_gamma: the gamma default, except 128x128, 64x128
-    and 64x64 blocks (split or not) at M > 128 go to variant 14, unsplit;
-    always legal where the gamma default is."""
+    """mi_default_config_no_gamma: the gamma default, except 128x128 blocks
+    (split or not) at M > 128 go to variant 16 (block_k 32, 4 stages), and
+    64x128 and 64x64 blocks to variant 14, unsplit; always legal where the
+    gamma default is."""
     import random
 
     from kernel_library.config import default_config
@@ -358,8 +364,8 @@ def test_no_gamma_default():
                 else fn(RMS, M, N, K, ctypes.byref(c))) == _lib.MI_OK
         return TileConfig.from_c(c)
 
-    assert pick(2048, 2048, 2048, L.mi_default_config_no_gamma).name == "bm128_bn128_bk64_w4_s3_v14"
-    assert pick(1024, 1024, 1024, L.mi_default_config_no_gamma).name == "bm128_bn128_bk64_w4_s3_v14"
+    assert pick(2048, 2048, 2048, L.mi_default_config_no_gamma).name == "bm128_bn128_bk32_w4_s4_v16"
+    assert pick(1024, 1024, 1024, L.mi_default_config_no_gamma).name == "bm128_bn128_bk32_w4_s4_v16"
     assert pick(512, 4096, 4096, L.mi_default_config_no_gamma).name == "bm64_bn128_bk64_w4_s4_v14"
     for shape in ((4096, 4096, 4096), (16, 28672, 8192), (128, 28672, 8192), (8192, 8192, 8192)):
         assert pick(*shape, L.mi_default_config_no_gamma) == pick(*shape, L.mi_default_config), shape
@@ -368,22 +374,25 @@ def test_no_gamma_default():
         M, N, K = rng.randint(1, 80) * 64, rng.randint(1, 80) * 64, rng.randint(1, 160) * 64
         ng, g = pick(M, N, K, L.mi_default_config_no_gamma), pick(M, N, K, L.mi_default_config)
         assert check("rmsnorm_matmul", ng, M, N, K)[0] == 0, (M, N, K, ng)
-        assert ng == g or (ng.variant == 14 and (ng.block_m, ng.block_n) == (g.block_m, g.block_n)), (M, N, K)
+        assert ng == g or (ng.variant == (16 if ng.block_m == 128 else 14)
+                           and (ng.block_m, ng.block_n) == (g.block_m, g.block_n)), (M, N, K)
     c = _lib.MiTileCfg()
     assert L.mi_default_config_no_gamma(-1, 8, 8, ctypes.byref(c)) == _lib.MI_E_ARGS
     assert L.mi_default_config_no_gamma(8, 8, 8, None) == _lib.MI_E_ARGS
     # The Python host: the no-gamma tuned entry, else the gamma one, else this default.
-    assert default_config("rmsnorm_matmul_online", 2048, 2048, 2048).variant == 14
+    assert default_config("rmsnorm_matmul_online", 2048, 2048, 2048).variant == 16
     assert default_config("rmsnorm_matmul_online", 16, 28672, 8192) == default_config("rmsnorm_matmul", 16, 28672, 8192)
-    assert default_config("rmsnorm_matmul_online", 1024, 1024, 1024).name == "bm128_bn128_bk64_w4_s3_v14"
+    assert default_config("rmsnorm_matmul_online", 1024, 1024, 1024).name == "bm128_bn128_bk32_w4_s4_v16"
 
 
-def test_gamma_free_variant_rejects_gamma_before_any_gpu_call():
-    """rmsnorm_matmul variant 14 computes the product without gamma: a call
-    with gamma is refused with MI_E_TILE on the host, and the sweep of a
-    call with gamma never offers it."""
+@pytest.mark.parametrize("cfg", [TileConfig(128, 128, 64, 4, 3, variant=14), TileConfig(128, 128, 32, 4, 4, variant=16)],
+                         ids=["v14", "v16"])
+def test_gamma_free_variant_rejects_gamma_before_any_gpu_call(cfg):
+    """rmsnorm_matmul variants 14 and 16 compute the product without gamma: a
+    call with gamma is refused with MI_E_TILE on the host, and the sweep of a
+    call with gamma never offers them."""
     L = _lib.lib()
-    c = TileConfig(128, 128, 64, 4, 3, variant=14).to_c()
+    c = cfg.to_c()
     x, g, w, o = (ctypes.c_void_p(0x10000000 + i * (1 << 28)) for i in range(4))
     assert L.mi_rmsnorm_matmul_bf16(x, g, w, o, 2048, 2048, 2048, 1e-6, ctypes.byref(c), None) == _lib.MI_E_TILE
     assert "without gamma" in _lib.last_error()
@@ -391,9 +400,9 @@ def test_gamma_free_variant_rejects_gamma_before_any_gpu_call():
 
     with_g = legal_configs("rmsnorm_matmul", 2048, 2048, 2048)
     without = legal_configs("rmsnorm_matmul", 2048, 2048, 2048, with_gamma=False)
-    assert not [cfg for cfg in with_g if cfg.variant == 14]
-    assert [cfg for cfg in without if cfg.variant == 14]
-    assert {cfg.name for cfg in with_g} < {cfg.name for cfg in without}
+    assert not [x for x in with_g if x.variant == cfg.variant]
+    assert [x for x in without if x.variant == cfg.variant]
+    assert {x.name for x in with_g} < {x.name for x in without}
 
 
 def test_entry_points_reject_misaligned_pointers():

@@ -175,7 +175,9 @@ def test_error_within_reference_bf16_semantics(gpu, shape, with_gamma):
     else:
         shipped = [kl.TileConfig.from_name("bm128_bn128_bk64_w4_s2_v4"),
                    kl.TileConfig.from_name("bm128_bn128_bk64_w4_s3_v14"),
-                   kl.TileConfig.from_name("bm256_bn256_bk32_w8_s3_v14")]
+                   kl.TileConfig.from_name("bm256_bn256_bk32_w8_s3_v14"),
+                   kl.TileConfig.from_name("bm128_bn128_bk32_w4_s4_v16"),
+                   kl.TileConfig.from_name("bm256_bn256_bk32_w8_s3_v16")]
     cfgs = shipped + [kl.TileConfig(256, 256, 32, 4, 3, variant=13)]
     if with_gamma:
         cfgs.append(kl.default_config("rmsnorm_matmul", M, N, K))
@@ -194,12 +196,15 @@ def test_error_within_reference_bf16_semantics(gpu, shape, with_gamma):
         assert err <= ref_err, (cfg, err, ref_err)
 
 
-def test_no_gamma_variant14_every_config_ragged(gpu):
-    """Variant 14 (no gamma; the rows' sums of squares taken from the MFMA A
-    fragments): every prebuilt config at ragged M, N, K (K not a multiple of
-    block_k, so the last K tile's zero-filled chunks must add nothing), with
-    a zero row (exactly 0), a constant row and a row of large values, every
-    output against the closed form."""
+@pytest.mark.parametrize("variant", [14, 16])
+def test_no_gamma_variant14_every_config_ragged(gpu, variant):
+    """Variants 14 and 16 (no gamma; the rows' sums of squares taken from the
+    MFMA A fragments, on the per-tile and the paired-load K-contiguous core):
+    every prebuilt config at ragged M, N, K (K not a multiple of block_k, so
+    the last K tile's zero-filled chunks must add nothing; an odd number of K
+    tiles, so the paired loads end on a half pair), with a zero row (exactly
+    0), a constant row and a row of large values, every output against the
+    closed form."""
     import kernel_library as kl
 
     M, K, N = 200, 264, 136
@@ -210,20 +215,23 @@ def test_no_gamma_variant14_every_config_ragged(gpu):
     x[13] *= 64.0
     expected = orms.closed_form(x, d["rhs"])
     xd, wd = _dev(x, gpu), _dev(d["rhs"], gpu)
-    cfgs = [c for c in kl.legal_configs("rmsnorm_matmul", M, N, K, with_gamma=False) if c.variant == 14]
+    cfgs = [c for c in kl.legal_configs("rmsnorm_matmul", M, N, K, with_gamma=False) if c.variant == variant]
     assert len(cfgs) >= 8
     for cfg in cfgs:
-        print("v14 ragged", cfg.name, flush=True)
+        print(f"v{variant} ragged", cfg.name, flush=True)
         host = _host(kl.rmsnorm_matmul(xd, wd, None, cfg=cfg))
         rep = rms_check(host, expected)
         assert _ok(rep), (cfg, rep)
         assert np.all(host[7] == 0.0)
 
 
-def test_no_gamma_variant14_identity_weight(gpu):
+@pytest.mark.parametrize("names", [("bm128_bn128_bk64_w4_s3_v14", "bm64_bn64_bk64_w4_s4_v14", "bm256_bn128_bk64_w8_s3_v14"),
+                                   ("bm128_bn128_bk32_w4_s4_v16", "bm256_bn128_bk32_w8_s3_v16",
+                                    "bm128_bn256_bk64_w4_s2_v16", "bm256_bn256_bk32_w8_s3_v16")], ids=["v14", "v16"])
+def test_no_gamma_variant14_identity_weight(gpu, names):
     """W = I isolates the row statistics: out = bf16(x / rms(x)) for every
-    row, at K = 1024 (16 K tiles of the 128x128 block, both halves of every
-    A fragment used)."""
+    row, at K = 1024 (16 or 32 K tiles, both halves of every A fragment
+    used; with 8 waves the row sums come from two or four wave columns)."""
     import kernel_library as kl
 
     M, K = 256, 1024
@@ -231,10 +239,10 @@ def test_no_gamma_variant14_identity_weight(gpu):
     x = d["lhs"]
     eye = _dev(np.eye(K, dtype=np.float32), gpu)
     ref = x * orms.inv_rms(x)[:, None]
-    for name in ("bm128_bn128_bk64_w4_s3_v14", "bm64_bn64_bk64_w4_s4_v14", "bm256_bn128_bk64_w8_s3_v14"):
+    for name in names:
         y = _host(kl.rmsnorm_matmul(_dev(x, gpu), eye, None, cfg=kl.TileConfig.from_name(name)))
         rep = rms_check(y, ref)
-        print("v14 identity", name, rep, flush=True)
+        print("identity", name, rep, flush=True)
         assert _ok(rep), (name, rep)
 
 
@@ -242,7 +250,7 @@ def test_no_gamma_variant14_identity_weight(gpu):
 def test_no_gamma_default_calls(gpu, M, K, N):
     """Calls without gamma and without a config: the Python host's default
     (rmsnorm_matmul_online) and the C ABI's own (cfg = NULL, gamma = NULL:
-    mi_default_config_no_gamma, variant 14 at these shapes), every output
+    mi_default_config_no_gamma: variant 16 or 14 at these shapes), every output
     against the closed form; both defaults run the same config, so the two
     outputs are bitwise equal."""
     import ctypes
