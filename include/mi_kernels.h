@@ -121,14 +121,17 @@ enum {
  *                    kernel writes bf16(x * gamma) in the lhsT layout and
  *                    the rows' sums of squares to the workspace (K * M * 2 +
  *                    ceil(K / 512) * M * 4 bytes), then the pipelined lhsT
- *                    core applies 1/rms to its fp32 accumulators; 14
+ *                    core applies 1/rms to its fp32 accumulators; 15 as 13
+ *                    with the pack in x's own layout (K * M * 2 bytes as
+ *                    well) and the paired-load K-contiguous core of
+ *                    matmul_lhs_rhs variant 1 (bitwise equal to 13); 14
  *                    without gamma only (gamma != NULL: MI_E_TILE): the
  *                    matmul_lhs_rhs core reads x once, LDS-direct, sums its
  *                    rows' squares from the MFMA A fragments (bf16 dot2)
  *                    and applies 1/rms to its fp32 accumulators; 16 as 14
  *                    on the paired-load core of matmul_lhs_rhs variant 1
  *                    (block_k 32 or 64; without gamma only).  Variants
- *                    2, 3, 6..10 and 15 do not exist (MI_E_TILE).
+ *                    2, 3 and 6..10 do not exist (MI_E_TILE).
  */
 typedef struct {
   int block_m, block_n, block_k, waves, lds_stages, split_k, group_m, variant;

@@ -45,6 +45,7 @@ _TEMPLATES = {
     ("rmsnorm_matmul", 12): ("rmsnorm_mm_bf16_xreg_kernel", 5),
     ("rmsnorm_matmul", 13): ("rmsnorm_mm_bf16_2pass_kernel", 5),
     ("rmsnorm_matmul", 14): ("rmsnorm_mm_bf16_sq_kernel", 5),
+    ("rmsnorm_matmul", 15): ("rmsnorm_mm_bf16_2pass_pair_kernel", 5),
     ("rmsnorm_matmul", 16): ("rmsnorm_mm_bf16_sq_pair_kernel", 5),
     ("matmul_lhsT_rhs_f32", 0): ("mm_f32_kernel", 3),
     ("matmul_lhsT_rhs_f32", 1): ("mm_f32_mfma_kernel", 2),

@@ -67,6 +67,8 @@ def _instance(fam: str, cfg) -> tuple[str, str, str] | None:
             return "MI_RMSXN_INST", "MI_RMSXN_ROW", f"{base}, {s}, {v - 9}"
         if v == 13:
             return "MI_RMS2_INST", "MI_RMS2_ROW", f"{base}, {s}"
+        if v == 15:
+            return "MI_RMS2P_INST", "MI_RMS2P_ROW", f"{base}, {s}"
         if v == 14:
             return "MI_RMSQ_INST", "MI_RMSQ_ROW", f"{base}, {s}"
         if v == 16:

@@ -55,7 +55,7 @@ class Atom(NamedTuple):
 FAMILY_VARIANTS = {
     "matmul_lhsT_rhs": (0, 1, 2, 3, 4, 5, 6),
     "matmul_lhs_rhs": (0, 1, 2),
-    "rmsnorm_matmul": (0, 1, 4, 5, 11, 12, 13),
+    "rmsnorm_matmul": (0, 1, 4, 5, 11, 12, 13, 15),
     "matmul_lhsT_rhs_f32": (0, 1),
 }
 

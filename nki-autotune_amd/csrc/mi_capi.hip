@@ -137,6 +137,7 @@ mi::Legal template_legal(int kernel_id, const mi_tile_cfg& c) {
       if (c.variant == 4 || c.variant == 5) return mi::legal_rms_xreg(bm, bn, bk, w, s, c.variant - 2);
       if (c.variant == 11 || c.variant == 12) return mi::legal_rms_xreg(bm, bn, bk, w, s, c.variant - 9);
       if (c.variant == 13) return mi::legal_rms2(bm, bn, bk, w, s);
+      if (c.variant == 15) return mi::legal_rms2_pair(bm, bn, bk, w, s);
       if (c.variant == 14) return mi::legal_mm_pipe(bm, bn, bk, w, s, true);
       if (c.variant == 16) return mi::legal_lhs_pair(bm, bn, bk, w, s);
       break;
@@ -567,7 +568,7 @@ int mi_rmsnorm_matmul_bf16(const void* x, const void* gamma, const void* W, void
     return fail(MI_E_ARGS, "out overlaps an input");
   if (gamma && cfg && (cfg->variant == 14 || cfg->variant == 16))
     return fail(MI_E_TILE, "rmsnorm_matmul variants 14 and 16 compute the fused product without gamma; with gamma "
-                           "use variant 0, 1, 4, 5, 11, 12 or 13");
+                           "use variant 0, 1, 4, 5, 11, 12, 13 or 15");
   mi_tile_cfg no_gamma_default;
   if (!cfg && !gamma) {
     mi::capi::pick_default_no_gamma(M, N, K, &no_gamma_default);

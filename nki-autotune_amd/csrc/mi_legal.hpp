@@ -203,6 +203,19 @@ MI_HD constexpr Legal legal_lhs_pair(int bm, int bn, int bk, int waves, int stag
   return ok();
 }
 
+// ---- main pass of the two-pass fused kernel on the paired-load core
+// (rmsnorm_matmul variant 15): the matmul_lhs_rhs variant-1 core plus BM
+// row scales in LDS.
+MI_HD constexpr int lds_rms2_pair(int bm, int bn, int bk, int waves, int stages) {
+  return lds_lhs_pair(bm, bn, bk, waves, stages) + bm * 4;
+}
+MI_HD constexpr Legal legal_rms2_pair(int bm, int bn, int bk, int waves, int stages) {
+  const Legal core = legal_lhs_pair(bm, bn, bk, waves, stages);
+  if (core.code != MI_OK) return core;
+  if (lds_rms2_pair(bm, bn, bk, waves, stages) > kLdsBytesMax) return bad(MI_E_LDS, "LDS over 160 KiB");
+  return ok();
+}
+
 // ---- fused kernel, x scaled while staged (rmsnorm_matmul variants 0 / 1):
 // x rows are reduced over BK/8 lanes (4, 8 or 16).
 MI_HD constexpr int lds_rms_plain(int bm, int bn, int bk, int waves, int stages) {

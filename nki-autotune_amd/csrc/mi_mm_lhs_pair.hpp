@@ -35,6 +35,15 @@
 // is a compile-time constant, and the K loop is compiled once per wave
 // column.  The epilogue adds the wave columns' sums through LDS and scales
 // output row m by 1/sqrt(sum_m / K + eps).
+//
+// RS (rmsnorm_matmul variant 15, the main pass of the two-pass fused kernel
+// on this core, mi_rms_2pass.hpp): the A operand is the packed xg =
+// bf16(x * gamma), and the rows' sums of squares come from the pack as
+// partial sums ssq[p][m].  Each workgroup loads the first partial sums of
+// its rows before the prologue's panel loads, adds them in part order after
+// the prologue's wait, keeps 1/sqrt(sum / K + eps) per row in LDS past the
+// panel buffers, and its epilogue scales output row m by it (the same steps
+// as the lhsT core's row scale in mi_gemm.hpp).
 #pragma once
 #include <numeric>
 
@@ -61,10 +70,10 @@ constexpr int count_even(int lo, int hi) {
   return n;
 }
 
-template <int BM, int BN, int BK, int WAVES, int STAGES, bool SQ>
+template <int BM, int BN, int BK, int WAVES, int STAGES, bool SQ, bool RS = false>
 __device__ __forceinline__ void mm_lhs_pair_body(const uint16_t* __restrict__ lhs, const uint16_t* __restrict__ rhs,
                                                  uint16_t* __restrict__ out, int M, int N, int K, int group_m,
-                                                 char* smem, float inv_k, float eps) {
+                                                 char* smem, const RowScale rsc) {
   using C = PairCfg<BM, BN, BK, WAVES, STAGES>;
   using G = typename C::G;
   static_assert(legal_lhs_pair(BM, BN, BK, WAVES, STAGES).code == MI_OK, "illegal tile config (mi_legal.hpp)");
@@ -79,6 +88,7 @@ __device__ __forceinline__ void mm_lhs_pair_body(const uint16_t* __restrict__ lh
   // vm_wait<n> counts assume every wave issues the same number of loads.
   static_assert(LA::EVEN && LB::EVEN, "every wave issues the same number of loads");
   static_assert(!SQ || G::WN * BM * 4 <= C::LDS_BYTES, "row sums of squares exchanged through LDS");
+  static_assert(!(SQ && RS), "row sums from the A fragments or from the pack, not both");
 
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63;
@@ -190,6 +200,23 @@ __device__ __forceinline__ void mm_lhs_pair_body(const uint16_t* __restrict__ lh
     }
   };
 
+  // RS: the rows' partial sums of squares (BM floats past the panels;
+  // each thread takes rows tid, tid + NTH, ...), the first RSB parts
+  // loaded ahead of the prologue's panel loads.
+  constexpr int NTH = WAVES * 64, RSB = 8, RPT = RS ? (BM + NTH - 1) / NTH : 1;
+  float* rs_lds = (float*)(smem + C::LDS_BYTES);
+  float rpart[RPT][RSB];
+  auto load_parts = [&](int p0) {
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) {
+      const int r = tid + j * NTH, m = m0 + r;
+#pragma unroll
+      for (int q = 0; q < RSB; ++q)
+        rpart[j][q] = (r < BM && m < M && p0 + q < rsc.parts) ? rsc.ssq[(size_t)(p0 + q) * (size_t)M + m] : 0.0f;
+    }
+  };
+  if constexpr (RS) load_parts(0);
+
   // Prologue: the groups of tiles 0 .. STAGES-1, then wait for tile 0.
 #pragma unroll
   for (int j = 0; j < STAGES; ++j) {
@@ -198,6 +225,24 @@ __device__ __forceinline__ void mm_lhs_pair_body(const uint16_t* __restrict__ lh
   }
   vm_wait<(STAGES - 1) * NLB + NLA * count_even(1, STAGES - 1)>();
   __syncthreads();
+  if constexpr (RS) {
+    // The compiler's wait for the partial sums drains the prologue's panel
+    // loads too (they were issued after them); no load is in flight after.
+    float rsum[RPT];
+#pragma unroll
+    for (int j = 0; j < RPT; ++j) rsum[j] = 0.0f;
+    for (int p0 = 0;; p0 += RSB) {
+#pragma unroll
+      for (int j = 0; j < RPT; ++j)
+#pragma unroll
+        for (int q = 0; q < RSB; ++q) rsum[j] += rpart[j][q];
+      if (p0 + RSB >= rsc.parts) break;
+      load_parts(p0 + RSB);
+    }
+#pragma unroll
+    for (int j = 0; j < RPT; ++j)
+      if (tid + j * NTH < BM) rs_lds[tid + j * NTH] = 1.0f / __builtin_sqrtf(rsum[j] * rsc.inv_k + rsc.eps);
+  }
   read_frags(0, 0, 0, 0, 0);
 
   // Tile t = t0 + I of a round (t0 a multiple of the round length, so even).
@@ -281,12 +326,12 @@ __device__ __forceinline__ void mm_lhs_pair_body(const uint16_t* __restrict__ lh
       float t = xs[r];
 #pragma unroll
       for (int c = 1; c < G::WN; ++c) t += xs[c * BM + r];
-      scale[i] = 1.0f / __builtin_sqrtf(t * inv_k + eps);
+      scale[i] = 1.0f / __builtin_sqrtf(t * rsc.inv_k + rsc.eps);
     }
     __syncthreads();  // store_tile reuses the same LDS
   } else {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) scale[i] = 1.0f;
+    for (int i = 0; i < TM; ++i) scale[i] = RS ? rs_lds[wm0 + i * 32 + (lane & 31)] : 1.0f;
   }
   store_tile<TM, TN, WAVES>(acc, scale, smem, wave, lane, out, M, N, m0 + wm0, n0 + wn0);
 }
@@ -297,7 +342,8 @@ __global__ __launch_bounds__(WAVES * 64) void mm_lhs_rhs_bf16_pair_kernel(const 
                                                                          uint16_t* __restrict__ out, int M, int N,
                                                                          int K, int group_m) {
   __shared__ __attribute__((aligned(1024))) char smem[PairCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
-  mm_lhs_pair_body<BM, BN, BK, WAVES, STAGES, false>(lhs, rhs, out, M, N, K, group_m, smem, 0.0f, 0.0f);
+  mm_lhs_pair_body<BM, BN, BK, WAVES, STAGES, false>(lhs, rhs, out, M, N, K, group_m, smem,
+                                                     RowScale{nullptr, 0, 0.0f, 0.0f});
 }
 
 // Fused out[M,N] = (x[M,K] / sqrt(mean_k x^2 + eps)) . W[K,N] without gamma
@@ -310,7 +356,23 @@ __global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_sq_pair_kernel(con
                                                                             int N, int K, int group_m, float eps,
                                                                             float inv_k) {
   __shared__ __attribute__((aligned(1024))) char smem[PairCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES];
-  mm_lhs_pair_body<BM, BN, BK, WAVES, STAGES, true>(x, w, out, M, N, K, group_m, smem, inv_k, eps);
+  mm_lhs_pair_body<BM, BN, BK, WAVES, STAGES, true>(x, w, out, M, N, K, group_m, smem,
+                                                    RowScale{nullptr, 0, inv_k, eps});
+}
+
+// Main pass of the two-pass fused kernel on this core (rmsnorm_matmul
+// variant 15): out = diag(1/rms) . xg . W with xg = bf16(x * gamma) and the
+// rows' partial sums of squares ssq[p][m] from the pack (RS above).
+template <int BM, int BN, int BK, int WAVES, int STAGES>
+__global__ __launch_bounds__(WAVES * 64) void rmsnorm_mm_bf16_2pass_pair_kernel(
+    const uint16_t* __restrict__ xg, const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int M, int N, int K,
+    int group_m, const float* __restrict__ ssq, int ssq_parts, float inv_k, float eps) {
+  static_assert(legal_rms2_pair(BM, BN, BK, WAVES, STAGES).code == MI_OK, "illegal tile config (mi_legal.hpp)");
+  static_assert(lds_rms2_pair(BM, BN, BK, WAVES, STAGES) == PairCfg<BM, BN, BK, WAVES, STAGES>::LDS_BYTES + BM * 4,
+                "host LDS budget out of step");
+  __shared__ __attribute__((aligned(1024))) char smem[lds_rms2_pair(BM, BN, BK, WAVES, STAGES)];
+  mm_lhs_pair_body<BM, BN, BK, WAVES, STAGES, false, true>(xg, w, out, M, N, K, group_m, smem,
+                                                          RowScale{ssq, ssq_parts, inv_k, eps});
 }
 
 }  // namespace mi

@@ -60,7 +60,8 @@ inline size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 // counters (kSkCounterBytes), then
 //   split-K matmul:                 fp32 products [parts][M][N]
 //   split-K fused (variants 4..12): products, then row sums of squares [parts][M]
-//   two-pass fused (variant 13):    xt [K][M] bf16, ssq [ceil(K/512)][M] fp32,
+//   two-pass fused (variants 13, 15): xt [K][M] (15: xg [M][K]) bf16,
+//                                   ssq [ceil(K/512)][M] fp32,
 //                                   then (split) products [parts][M][N]
 //   stream-K (lhsT.rhs 5, 6):       fp32 partial tiles: one early slot per
 //                                   workgroup of the grid, one owner slot per
@@ -69,7 +70,7 @@ inline size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 inline size_t workspace_bytes(int kernel_id, const mi_tile_cfg& c, int M, int N, int K, int cus) {
   const size_t m = (size_t)M, n = (size_t)N, k = (size_t)K, p = (size_t)(c.split_k > 1 ? c.split_k : 0);
   size_t data = 0;
-  if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 && c.variant == 13)
+  if (kernel_id == MI_KERNEL_RMSNORM_MATMUL_BF16 && (c.variant == 13 || c.variant == 15))
     data = align256(k * m * 2) + align256((size_t)rms2_parts(K) * m * 4) + p * m * n * 4;
   else if (is_streamk(kernel_id, c.variant)) {
     const long long tiles = grid_tiles(M, N, c.block_m, c.block_n);
@@ -265,6 +266,26 @@ hipError_t launch_rms_2pass(const MiArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Two-pass fused kernel on the paired-load core (variant 15): pass 1 packs
+// x*gamma in x's own layout (xg[M][K]) and the row sums of squares, pass 2
+// is the paired-load K-contiguous core with the rms row scale.  Unsplit.
+template <int BM, int BN, int BK, int W, int S>
+hipError_t launch_rms_2pass_pair(const MiArgs& a, hipStream_t s) {
+  const size_t m = (size_t)a.M, k = (size_t)a.K;
+  const int sparts = rms2_parts(a.K);
+  char* data = ws_data(a);
+  uint16_t* xg = (uint16_t*)data;
+  float* ssq = (float*)(data + align256(k * m * 2));
+  hipLaunchKernelGGL(rms_pack_kernel<1>, dim3((unsigned)((a.M + RP_ROWS - 1) / RP_ROWS), (unsigned)sparts),
+                     dim3(RP_WAVES * 64), 0, s, (const uint16_t*)a.a, (const uint16_t*)a.g, xg, ssq, a.M, a.K);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL((rmsnorm_mm_bf16_2pass_pair_kernel<BM, BN, BK, W, S>), dim3(grid_tiles(a.M, a.N, BM, BN)),
+                     dim3(W * 64), 0, s, xg, (const uint16_t*)a.b, (uint16_t*)a.out, a.M, a.N, a.K, a.group_m, ssq,
+                     sparts, a.inv_k, a.eps);
+  return hipGetLastError();
+}
+
 // Fused kernel without gamma (variant 14): one launch of the K-contiguous
 // pipelined core that takes the rows' sums of squares from its A operand.
 // The C ABI rejects it with gamma.
@@ -365,6 +386,11 @@ hipError_t launch_rms_sq_pair(const MiArgs& a, hipStream_t s) {
       const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, int, float*, const float*, int, float, \
       float);
 
+// Variant 15: the main pass of the two-pass fused kernel on the paired-load core.
+#define MI_RMS2P_INST(BM, BN, BK, W, S)                                                                         \
+  template __global__ void rmsnorm_mm_bf16_2pass_pair_kernel<BM, BN, BK, W, S>(                                \
+      const uint16_t*, const uint16_t*, uint16_t*, int, int, int, int, const float*, int, float, float);
+
 // Variant 14: the fused kernel without gamma.
 #define MI_RMSQ_INST(BM, BN, BK, W, S)                                                                     \
   template __global__ void rmsnorm_mm_bf16_sq_kernel<BM, BN, BK, W, S>(const uint16_t*, const uint16_t*, \
@@ -437,6 +463,9 @@ hipError_t launch_rms_sq_pair(const MiArgs& a, hipStream_t s) {
 #define MI_RMS2_ROW(BM, BN, BK, W, S)                                                               \
   {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 13}, lds_rms2(BM, BN, BK, W, S),         \
    &launch_rms_2pass<BM, BN, BK, W, S>},
+#define MI_RMS2P_ROW(BM, BN, BK, W, S)                                                              \
+  {MI_KERNEL_RMSNORM_MATMUL_BF16, {BM, BN, BK, W, S, 1, 0, 15}, lds_rms2_pair(BM, BN, BK, W, S),    \
+   &launch_rms_2pass_pair<BM, BN, BK, W, S>},
 
 // The 72-point search grid for one (BM, BN): BK in {32,64} x waves in {4,8} x
 // stages in {1,2}.  X is a row macro taking (BM, BN, BK, W, S, ...).

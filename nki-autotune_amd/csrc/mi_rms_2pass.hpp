@@ -1,4 +1,4 @@
-// mi_rms_2pass.hpp -- fused rmsnorm_matmul in two passes (variant 13).
+// mi_rms_2pass.hpp -- fused rmsnorm_matmul in two passes (variants 13, 15).
 //
 //   out[M,N] = (x[M,K] * rsqrt(mean_k x^2 + eps) * gamma[K]) . W[K,N]
 //
@@ -15,6 +15,13 @@
 //     rows' partial sums (part order) while its first K tiles load, keeps
 //     1/sqrt(sum / K + eps) per row in LDS, and its epilogue multiplies the
 //     fp32 accumulators of output row m by it.
+//
+// Variant 15 packs bf16(x * gamma) in x's own layout instead (xg[m][k], a
+// pass with no transpose) and runs the paired-load K-contiguous core
+// (mi_mm_lhs_pair.hpp) on (xg, W) with the same row scale.  Its MFMAs see
+// the same operands in the same K order as variant 13's at the same tile
+// config, and the row sums are added in the same order, so the two give the
+// same bits.
 //
 // The arithmetic is that of the one-pass variants: x*gamma rounded once to
 // bf16 (the operand the MFMAs see), fp32 accumulation over the whole K, and
@@ -43,7 +50,9 @@ __host__ __device__ constexpr int rms2_parts(int K) { return (K + RP_KCH - 1) / 
 
 // Requires M % 8 == 0 and K % 8 == 0 (every 8-row block and 8-column chunk
 // is wholly inside or outside the matrix) and 16-byte aligned x, gamma, xt.
-template <int UNUSED = 0>
+// KMAJOR: xt is written as xg[m][k] (x's layout; the 8 lanes of a row block
+// write one whole 128-byte line per row) instead of xt[k][m].
+template <int KMAJOR = 0>
 __global__ __launch_bounds__(RP_WAVES * 64) void rms_pack_kernel(const uint16_t* __restrict__ x,
                                                                 const uint16_t* __restrict__ gamma,
                                                                 uint16_t* __restrict__ xt, float* __restrict__ ssq,
@@ -97,14 +106,26 @@ __global__ __launch_bounds__(RP_WAVES * 64) void rms_pack_kernel(const uint16_t*
     for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss[j] = __builtin_fmaf(val[j][e], val[j][e], ss[j]);
+    if constexpr (KMAJOR) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      u32x4_t o;
-      o.x = pack_bf16x2(val[0][e] * g[e], val[1][e] * g[e]);
-      o.y = pack_bf16x2(val[2][e] * g[e], val[3][e] * g[e]);
-      o.z = pack_bf16x2(val[4][e] * g[e], val[5][e] * g[e]);
-      o.w = pack_bf16x2(val[6][e] * g[e], val[7][e] * g[e]);
-      *(u32x4_t*)(xt + (size_t)(kcol[s] + e) * (size_t)M + m0) = o;
+      for (int j = 0; j < 8; ++j) {
+        u32x4_t o;
+        o.x = pack_bf16x2(val[j][0] * g[0], val[j][1] * g[1]);
+        o.y = pack_bf16x2(val[j][2] * g[2], val[j][3] * g[3]);
+        o.z = pack_bf16x2(val[j][4] * g[4], val[j][5] * g[5]);
+        o.w = pack_bf16x2(val[j][6] * g[6], val[j][7] * g[7]);
+        *(u32x4_t*)(xt + (size_t)(m0 + j) * (size_t)K + kcol[s]) = o;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        u32x4_t o;
+        o.x = pack_bf16x2(val[0][e] * g[e], val[1][e] * g[e]);
+        o.y = pack_bf16x2(val[2][e] * g[e], val[3][e] * g[e]);
+        o.z = pack_bf16x2(val[4][e] * g[e], val[5][e] * g[e]);
+        o.w = pack_bf16x2(val[6][e] * g[e], val[7][e] * g[e]);
+        *(u32x4_t*)(xt + (size_t)(kcol[s] + e) * (size_t)M + m0) = o;
+      }
     }
   }
   // Row sums: the 8 lanes of a row block (DPP), then the 4 waves (LDS).

@@ -151,6 +151,11 @@ def test_every_compiled_config_is_enumerable_and_legal():
         (RMS, TileConfig(128, 128, 64, 4, 3, variant=14), (2048, 2048, 2044), _lib.MI_E_ALIGN),   # K % 8
         (RMS, TileConfig(128, 128, 64, 4, 1, variant=14), (2048, 2048, 2048), _lib.MI_E_TILE),    # pipelined core
         (RMS, TileConfig(128, 128, 64, 4, 3, split_k=2, variant=14), (512, 512, 8192), _lib.MI_E_SPLIT),
+        # variant 15: the two-pass kernel on the paired-load core (its LDS: the core's plus BM row scales)
+        (RMS, TileConfig(256, 256, 32, 4, 3, variant=15), (4096, 4096, 4096), _lib.MI_OK),
+        (RMS, TileConfig(256, 256, 32, 4, 4, variant=15), (4096, 4096, 4096), _lib.MI_E_LDS),    # 160 KiB + 1 KiB
+        (RMS, TileConfig(256, 256, 32, 4, 3, variant=15), (4096, 4096, 4092), _lib.MI_E_ALIGN),  # K % 8
+        (RMS, TileConfig(128, 128, 32, 4, 4, split_k=2, variant=15), (512, 512, 8192), _lib.MI_E_SPLIT),
         # variant 16: the paired-load core's legality (block_k 32 or 64, whole pair loads per wave)
         (RMS, TileConfig(256, 256, 32, 8, 3, variant=16), (4096, 4096, 4096), _lib.MI_OK),
         (RMS, TileConfig(256, 256, 32, 8, 3, variant=16), (4096, 4096, 4092), _lib.MI_E_ALIGN),   # K % 8

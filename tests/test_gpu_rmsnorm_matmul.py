@@ -17,7 +17,7 @@ from oracle import rmsnorm as orms
 pytestmark = pytest.mark.gpu
 
 # Every variant of the fused kernel (include/mi_kernels.h).
-VARIANTS = (0, 1, 4, 5, 11, 12, 13)
+VARIANTS = (0, 1, 4, 5, 11, 12, 13, 15)
 
 
 def _dev(a, device):
@@ -137,6 +137,8 @@ def test_baseline_c3_full_size(gpu):
             kl.TileConfig(128, 512, 32, 8, 3, variant=4), kl.TileConfig(128, 512, 32, 8, 3, variant=5),
             kl.TileConfig(256, 256, 32, 4, 3, variant=13), kl.TileConfig(256, 256, 32, 4, 4, variant=13),
             kl.TileConfig(128, 512, 32, 8, 3, variant=13), kl.TileConfig(256, 256, 32, 8, 3, variant=13),
+            kl.TileConfig(256, 256, 32, 4, 3, variant=15), kl.TileConfig(256, 256, 32, 8, 3, variant=15),
+            kl.TileConfig(128, 512, 32, 8, 3, variant=15),
             kl.default_config("rmsnorm_matmul", 4096, 4096, 4096)]
     for cfg in cfgs:
         out_dev = torch.full((4096, 4096), float("nan"), dtype=torch.bfloat16, device=gpu)
@@ -147,6 +149,33 @@ def test_baseline_c3_full_size(gpu):
         rep = rms_check(_host(out_dev)[rows], expected)
         print(cfg.name, "sampled rows vs oracle:", rep, flush=True)
         assert _ok(rep), (cfg, rep)
+
+
+@pytest.mark.parametrize("M,K,N,with_gamma", [(200, 264, 136, True), (200, 264, 136, False), (4096, 4096, 4096, True)])
+def test_two_pass_kinds_give_the_same_bits(gpu, M, K, N, with_gamma):
+    """Variant 15 (x*gamma packed in x's layout, the paired-load K-contiguous
+    core) against variant 13 (packed transposed, the lhsT core): the MFMAs see
+    the same bf16 operands in the same K order and the row sums of squares
+    are added in the same order, so every config of either gives the same
+    bits; all against the float64 closed form too."""
+    import torch
+
+    import kernel_library as kl
+
+    print(f"two-pass kinds M={M} K={K} N={N} gamma={with_gamma}", flush=True)
+    d = rms_inputs(M, K, N, seed=17, with_gamma=with_gamma)
+    x, w = _dev(d["lhs"], gpu), _dev(d["rhs"], gpu)
+    g = _dev(d["gamma"], gpu) if with_gamma else None
+    ref = kl.rmsnorm_matmul(x, w, g, cfg=kl.TileConfig(256, 256, 32, 4, 3, variant=13))
+    full = rms_check_full(ref, rms_closed_form_gpu(x, w, g))
+    assert full["ok"], full
+    cfgs = [c for c in kl.legal_configs("rmsnorm_matmul", M, N, K) if c.variant in (13, 15) and c.split_k == 1]
+    assert len([c for c in cfgs if c.variant == 15]) >= 6
+    for cfg in cfgs:
+        out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+        kl.rmsnorm_matmul(x, w, g, cfg=cfg, out=out)
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), cfg
 
 
 @pytest.mark.parametrize("shape,with_gamma", [((4096, 4096, 4096), True), ((2048, 2048, 2048), False)])

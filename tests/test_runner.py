@@ -172,7 +172,7 @@ def test_render_parse_roundtrip_and_aliases():
 
 
 @pytest.mark.parametrize("fam,variants", [("matmul_lhsT_rhs", (0, 1, 2, 3, 4, 5, 6)), ("matmul_lhs_rhs", (0, 1, 2)),
-                                          ("rmsnorm_matmul", (0, 1, 4, 5, 11, 12, 13, 14, 16))])
+                                          ("rmsnorm_matmul", (0, 1, 4, 5, 11, 12, 13, 14, 15, 16))])
 def test_jit_units_instantiate_every_variant(fam, variants, tmp_path):
     """The generated single-config unit of every variant names a real template
     and table row: hipcc parses and instantiates it (device side, no codegen),
