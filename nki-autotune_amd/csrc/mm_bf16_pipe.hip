@@ -27,6 +27,7 @@
   X(128, 128, 64, 4, 2)      \
   X(128, 128, 64, 4, 3)      \
   X(128, 128, 64, 4, 4)      \
+  X(128, 128, 32, 4, 4)      \
   X(128, 64, 64, 4, 4)       \
   X(64, 128, 64, 4, 4)       \
   X(64, 256, 64, 4, 3)       \
