@@ -212,7 +212,19 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
       {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v}, 0.62},
       {n_much_longer && !lhs ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v}, 0.60},
       {mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v}, 0.35}};
-  return fastest_estimate(cands, 5, M, N, K, kernel_id);
+  mi_tile_cfg c = fastest_estimate(cands, 5, M, N, K, kernel_id);
+  // lhsT.rhs 128x128 blocks then run block_k 32 with 4 stages, the same
+  // parts (each part keeps at least 8 K tiles of 32): three tiles in flight
+  // instead of two.  Measured against block_k 64 with 3 stages at eleven
+  // shapes this picker gives the 128x128 block (split or not), in
+  // interleaved rounds on one box: median 0.958 x the time, 0.880-1.022 x,
+  // bitwise equal outputs.  The K-contiguous lhs.rhs kernel keeps block_k
+  // 64 (32 there loads half lines: median 1.008 x, up to 1.079 x).
+  if (!lhs && c.block_m == 128 && c.block_n == 128 && c.block_k == 64) {
+    c.block_k = 32;
+    c.lds_stages = 4;
+  }
+  return c;
 }
 
 // rmsnorm_matmul.  The register-staged kernels keep gamma in LDS (8192

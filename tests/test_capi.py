@@ -233,7 +233,7 @@ def test_library_default_is_legal_everywhere():
     ("matmul_lhsT_rhs", (640, 10240, 2048), "bm128_bn256_bk32_w4_s3_v1"),
     ("matmul_lhsT_rhs", (2048, 1024, 8192), "bm64_bn128_bk64_w4_s4_v1"),
     ("matmul_lhsT_rhs", (512, 4096, 4096), "bm128_bn64_bk64_w4_s4_v1"),       # N >= 4M: 128 along M
-    ("matmul_lhsT_rhs", (512, 512, 32768), "bm128_bn128_bk64_w4_s3_v1_k16"),  # few tiles, long K: the largest block a split fills the chip with
+    ("matmul_lhsT_rhs", (512, 512, 32768), "bm128_bn128_bk32_w4_s4_v1_k16"),  # few tiles, long K: the largest block a split fills the chip with
     ("matmul_lhsT_rhs", (16, 28672, 8192), "bm32_bn128_bk64_w4_s4_v3"),       # skinny, weight streamed non-temporally
     ("matmul_lhsT_rhs", (32, 14336, 4096), "bm64_bn64_bk64_w4_s4_v3"),        # skinny: least panel bytes per workgroup
     ("matmul_lhsT_rhs", (64, 4096, 4096), "bm64_bn64_bk64_w4_s4_v3_k4"),

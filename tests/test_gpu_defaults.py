@@ -40,7 +40,7 @@ def _rows(M: int) -> np.ndarray:
 
 @pytest.mark.parametrize("fam,shape,expect", [
     ("matmul_lhsT_rhs", (1000, 2000, 3000), "bm64_bn128_bk64_w4_s4_v1"),
-    ("matmul_lhsT_rhs", (512, 512, 32768), "bm128_bn128_bk64_w4_s3_v1_k16"),
+    ("matmul_lhsT_rhs", (512, 512, 32768), "bm128_bn128_bk32_w4_s4_v1_k16"),
     ("matmul_lhsT_rhs", (96, 4544, 16256), "bm128_bn256_bk32_w4_s3_v3_k8"),
     ("matmul_lhsT_rhs", (3072, 3072, 3072), "bm256_bn256_bk32_w4_s3_v1"),
     ("matmul_lhsT_rhs", (16, 8192, 8192), "bm32_bn128_bk64_w4_s4_v3_k4"),
