@@ -109,6 +109,7 @@ mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K
     mi_tile_cfg c = cands[i].c;
     const long long tiles = tiles_of(M, N, c.block_m, c.block_n);
     c.split_k = tiles < kFillTiles ? fill_parts(tiles, K, c.block_k) : 1;
+    if (!splittable(MI_KERNEL_RMSNORM_MATMUL_BF16, c.variant)) c.split_k = 1;
     // Past the gamma entries an instance stages, K splits further; a
     // candidate no split makes legal, or whose workspace the call could not
     // allocate, is out.
@@ -128,6 +129,8 @@ mi_tile_cfg fastest_split_estimate(const Cand* cands, int n, int M, int N, int K
     }
     if (c.split_k > 1) t += (double)c.split_k * M * N * 8.0 / kSplitBytesPerUs + kLaunchUs;
     if (c.variant == 13) t += (double)M * K * 4.0 / kPackBytesPerUs + kLaunchUs;
+    // Variant 15's pack writes x's own layout, no transpose: 0.9 of the time.
+    if (c.variant == 15) t += 0.9 * (double)M * K * 4.0 / kPackBytesPerUs + kLaunchUs;
     if (!found || t < best_t) {
       found = true;
       best_t = t;
@@ -154,16 +157,22 @@ mi_tile_cfg skinny_matmul_default(bool lhs, int M, int N, int K) {
   // lhsT.rhs: a skinny launch is bound by each workgroup's own loads (its
   // MFMA pipe is a quarter busy at most), so the estimate is the rounds of
   // workgroups times one workgroup's panel bytes, (block_m + block_n) x its
-  // K range x 2, at 50 GB/s per CU plus 3 us, and a split pays its fp32
-  // partial products at 2 TB/s plus 8 us (the summing launch and the
-  // workspace).  Fitted to every block and split timed at 25 skinny shapes
-  // with the weight flushed (within 1.09 of the fastest at all of them).
-  // Equal estimates go to the earlier block (32 x 128 with block_k 64 and
-  // 4 stages measured faster than with block_k 128 and 3).
+  // K range x 2, at 60 GB/s per CU plus 3 us, and a split pays its fp32
+  // partial products, written and read back (8 bytes per output element
+  // and part), at 5 TB/s plus 2 us for the summing launch; every part
+  // keeps at least 512 of K.  Fitted to every block and split timed at 34
+  // skinny shapes (M 8-128, K 512-16384) with the weight flushed and the
+  // split workspace kept per stream: the pick within 1.089 of the fastest at
+  // all of them (mean 1.013), and within 1.043 at the third of the shapes
+  // held out of a fit to the other two thirds.  Equal estimates go to the
+  // earlier block (32 x 128 with block_k 64 and 4 stages measured faster
+  // than with block_k 128 and 3; 128 x 128 with block_k 32 and 4 stages
+  // than with 64 and 3).
   const mi_tile_cfg cands[] = {
       {32, 128, 64, 4, 4, 1, 8, v_nt},  {32, 128, 128, 4, 3, 1, 8, v_nt}, {32, 256, 64, 4, 4, 1, 8, v_nt},
       {64, 128, 64, 4, 4, 1, 8, v_nt},  {64, 64, 64, 4, 4, 1, 8, v_nt},   {64, 256, 64, 4, 3, 1, 8, v_nt},
-      {128, 128, 64, 4, 3, 1, 8, v_nt}, {128, 256, 32, 4, 3, 1, 8, v_nt}, {128, 256, 32, 4, 4, 1, 8, v_nt}};
+      {128, 128, 32, 4, 4, 1, 8, v_nt}, {128, 128, 64, 4, 3, 1, 8, v_nt}, {128, 256, 32, 4, 3, 1, 8, v_nt},
+      {128, 256, 32, 4, 4, 1, 8, v_nt}};
   // Blocks more than twice as tall as M are not considered; splits stop at
   // 320 workgroups.
   const int m_cap = 2 * (M > 32 ? M : 32);
@@ -175,10 +184,10 @@ mi_tile_cfg skinny_matmul_default(bool lhs, int M, int N, int K) {
     const long long tiles = tiles_of(M, N, ci.block_m, ci.block_n), kt = ((long long)K + ci.block_k - 1) / ci.block_k;
     for (int p = 1; p <= kMaxSplit; p *= 2) {
       const long long kts = (kt + p - 1) / p, wgs = tiles * p;
-      if (p > 1 && (wgs > 320 || (long long)(p - 1) * kts >= kt)) break;
       const double kp = (double)((K + p - 1) / p);
-      double t = (double)((wgs + kCUs - 1) / kCUs) * ((ci.block_m + ci.block_n) * kp * 2.0 / 50e3 + 3.0);
-      if (p > 1) t += (double)p * M * N * 8.0 / 2e6 + 8.0;
+      if (p > 1 && (wgs > 320 || (long long)(p - 1) * kts >= kt || kp < 512.0)) break;
+      double t = (double)((wgs + kCUs - 1) / kCUs) * ((ci.block_m + ci.block_n) * kp * 2.0 / 60e3 + 3.0);
+      if (p > 1) t += (double)p * M * N * 8.0 / 5e6 + 2.0;
       if (!found || t < best_t) {
         found = true;
         best_t = t;
@@ -213,6 +222,7 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
       {n_much_longer && !lhs ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v}, 0.60},
       {mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v}, 0.35}};
   mi_tile_cfg c = fastest_estimate(cands, 5, M, N, K, kernel_id);
+  if (lhs) return c;
   // lhsT.rhs 128x128 blocks then run block_k 32 with 4 stages, the same
   // parts (each part keeps at least 8 K tiles of 32): three tiles in flight
   // instead of two.  Measured against block_k 64 with 3 stages at eleven
@@ -220,9 +230,25 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
   // interleaved rounds on one box: median 0.958 x the time, 0.880-1.022 x,
   // bitwise equal outputs.  The K-contiguous lhs.rhs kernel keeps block_k
   // 64 (32 there loads half lines: median 1.008 x, up to 1.079 x).
-  if (!lhs && c.block_m == 128 && c.block_n == 128 && c.block_k == 64) {
+  if (c.block_m == 128 && c.block_n == 128 && c.block_k == 64) {
     c.block_k = 32;
     c.lds_stages = 4;
+  }
+  // Where the rounds estimate settles on a small unsplit block with a long K
+  // (64 x 64 from K = 3072, 64 x 128 or 128 x 64 from K = 8192), or splits a
+  // 256-long block 8 ways or more, the 128 x 128 block split to fill the
+  // chip is faster: it moves half the operand bytes per multiply-add of a
+  // 64 x 64 block, and each part's partial products cost less than the
+  // MFMA time they save.  Timed with every candidate and split at 30 shapes
+  // past skinny M (interleaved rounds, one box), this takes the pick from
+  // within 1.74 of the fastest (mean 1.082) to within 1.21 (mean 1.011);
+  // it applies at 9 of the shapes, and the rest keep their pick.
+  const bool small = c.split_k == 1 && c.block_m * c.block_n <= 128 * 64;
+  const bool long_k = K >= 8192 || (c.block_m == 64 && c.block_n == 64 && K >= 3072);
+  const bool thin_256 = (c.block_m == 256 || c.block_n == 256) && c.split_k >= 8;
+  if ((small && long_k) || thin_256) {
+    const int parts = fill_parts(tiles_of(M, N, 128, 128), K, 32);
+    if (parts >= 2) c = {128, 128, 32, 4, 4, parts, 8, v};
   }
   return c;
 }
@@ -277,16 +303,29 @@ mi_tile_cfg fused_default(int M, int N, int K) {
   // 256 x 128, its long side along the shorter output side, at 0.95).
   // Few-tile shapes split K, which the estimate charges for its fp32 partial
   // products and the launch of the summing kernel; past K = 8192 the
-  // one-pass kernels split at least until each part's gamma fits.
-  const Cand cands[] = {{mi_tile_cfg{128, 512, 32, 8, 3, 1, 8, 4}, 1.0},
-                        {mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 5}, 0.83},
-                        {mi_tile_cfg{128, 128, 64, 4, 2, 1, 8, 4}, 0.54},
-                        {mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, 13}, 1.10},
-                        {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, 13}, 0.68},
-                        {mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, 13}, 0.57},
-                        {M <= N ? mi_tile_cfg{256, 128, 64, 4, 3, 1, 8, 13} : mi_tile_cfg{128, 256, 64, 4, 3, 1, 8, 13},
-                         0.95}};
-  return fastest_split_estimate(cands, K > 8192 ? 7 : 6, M, N, K, mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0});
+  // one-pass kernels split at least until each part's gamma fits.  The
+  // two-pass kernel on the paired-load core (variant 15, never split) adds
+  // 128 x 256 at 0.95, and 128 x 128 at 0.80 where that grid keeps more
+  // than half the CUs busy (with fewer, a split or a 64-row block won at
+  // every shape timed).  Fitted to every candidate and split timed at 23
+  // fused shapes with M > 128 (interleaved rounds, one box): the pick within
+  // 1.012 of the fastest at all of them (mean 1.0005, against 1.17 and 1.040
+  // without variant 15).  The rates alone, without the half-busy rule, were
+  // within 1.064 at the third of the shapes held out of a fit to the other
+  // two thirds.
+  Cand cands[9];
+  int n = 0;
+  cands[n++] = {mi_tile_cfg{128, 512, 32, 8, 3, 1, 8, 4}, 1.0};
+  cands[n++] = {mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 5}, 0.83};
+  cands[n++] = {mi_tile_cfg{128, 128, 64, 4, 2, 1, 8, 4}, 0.54};
+  cands[n++] = {mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, 13}, 1.10};
+  cands[n++] = {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, 13}, 0.68};
+  cands[n++] = {mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, 13}, 0.57};
+  if (2 * tiles_of(M, N, 128, 128) > kCUs) cands[n++] = {mi_tile_cfg{128, 128, 32, 4, 4, 1, 8, 15}, 0.80};
+  cands[n++] = {mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 15}, 0.95};
+  if (K > 8192)
+    cands[n++] = {M <= N ? mi_tile_cfg{256, 128, 64, 4, 3, 1, 8, 13} : mi_tile_cfg{128, 256, 64, 4, 3, 1, 8, 13}, 0.95};
+  return fastest_split_estimate(cands, n, M, N, K, mi_tile_cfg{128, 256, 64, 8, 2, 1, 8, 0});
 }
 
 }  // namespace
@@ -316,28 +355,43 @@ int pick_default(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg) {
 
 // The fused kernel's default for a call without gamma: pick_default's
 // choice, except that its 128x128, 64x128 and 64x64 blocks (shapes of one
-// or two rounds of tiles, split or not) go to a gamma-free variant with the
-// same block, unsplit: 128x128 to variant 16 (block_k 32, 4 stages), the
-// others to variant 14.  Variant 14 measured in interleaved rounds against
+// or two rounds of tiles, split or not) go to a gamma-free variant, unsplit:
+// 64x128 and 64x64 to variant 14 with the same block, 128x128 as below.
+// Variant 14 measured in interleaved rounds against
 // the default (no gamma): 0.60 x its time at 1024^3 (against the 4-part
 // split), 0.89 x at 2048^3, 0.90 x at 1024x4096x4096, 0.80 x at
 // 512x4096x4096, 0.78 x at 256x8192x2048; variant 16 at 128x128, against
 // variant 14's 128x128 block: 0.924-0.957 x (median 0.938) at twelve shapes
-// this rule gives it, from 256x512x2048 to 4096x512x1024, with bitwise equal
-// outputs.  The larger blocks (128x512, 256x256 two-pass, 128x256) stay,
+// from 256x512x2048 to 4096x512x1024, with bitwise equal outputs.  The
+// larger blocks (128x512, 256x256 two-pass, 128x256) stay,
 // variant 14 being 0-8 % slower there.  Skinny M keeps its non-temporal
 // variants.
 int pick_default_no_gamma(int M, int N, int K, mi_tile_cfg* cfg) {
   const int rc = pick_default(MI_KERNEL_RMSNORM_MATMUL_BF16, M, N, K, cfg);
   if (rc != MI_OK) return rc;
   const int v = cfg->variant, bm = cfg->block_m, bn = cfg->block_n;
-  const bool one_pass_or_two = v == 4 || v == 5 || v == 13;
+  const bool one_pass_or_two = v == 4 || v == 5 || v == 13 || v == 15;
   const bool small_block = (bm == 128 && bn == 128) || (bm == 64 && bn == 128) || (bm == 64 && bn == 64);
   if (M > 128 && one_pass_or_two && small_block) {
-    if (bm == 128)
-      *cfg = {128, 128, 32, 4, 4, 1, cfg->group_m, 16};
-    else
+    // A 128 x 128 pick takes the largest block whose grid keeps more than
+    // half the CUs busy: variant 16 at 128 x 128, else variant 14 at 64 x 128,
+    // else at 64 x 64.  Measured without gamma (us, 128 x 128 v16 / 64 x 128
+    // v14 / 64 x 64 v14): 59.9 / 76.1 / 75.5 at 384x8192x8192 (192 tiles of
+    // 128 x 128); 29.2 / 23.5 / 28.7 at 512x4096x4096 (128 tiles), 53.7 /
+    // 42.8 / 54.6 at 512x4096x8192, 16.3 / 12.9 / 14.3 at 1024x2048x2048;
+    // 10.1 / 7.9 / 6.4 at 1024^3 (64 tiles), 27.2 / 20.8 / 16.4 at
+    // 1024x1024x4096, 15.7 / 11.2 / 8.2 at 256x512x2048.
+    if (bm == 128) {
+      const long long t128 = tiles_of(M, N, 128, 128);
+      if (2 * t128 > kCUs)
+        *cfg = {128, 128, 32, 4, 4, 1, cfg->group_m, 16};
+      else if (4 * t128 > kCUs)
+        *cfg = {64, 128, 64, 4, 4, 1, cfg->group_m, 14};
+      else
+        *cfg = {64, 64, 64, 4, 4, 1, cfg->group_m, 14};
+    } else {
       *cfg = {bm, bn, 64, 4, 4, 1, cfg->group_m, 14};
+    }
   }
   return MI_OK;
 }

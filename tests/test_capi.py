@@ -231,22 +231,25 @@ def test_library_default_is_legal_everywhere():
     ("matmul_lhsT_rhs", (1024, 8192, 16384), "bm256_bn128_bk32_w4_s3_v1"),    # long side along the shorter output side
     ("matmul_lhsT_rhs", (4096, 14336, 1024), "bm128_bn256_bk32_w4_s3_v1"),    # K <= 2048: long side along N
     ("matmul_lhsT_rhs", (640, 10240, 2048), "bm128_bn256_bk32_w4_s3_v1"),
-    ("matmul_lhsT_rhs", (2048, 1024, 8192), "bm64_bn128_bk64_w4_s4_v1"),
+    ("matmul_lhsT_rhs", (2048, 1024, 8192), "bm128_bn128_bk32_w4_s4_v1_k2"),  # small block, long K: 128x128 split fills the chip
+    ("matmul_lhsT_rhs", (136, 4096, 4096), "bm128_bn128_bk32_w4_s4_v1_k4"),   # 64x64 from K = 3072 likewise
+    ("matmul_lhsT_rhs", (512, 1024, 16384), "bm128_bn128_bk32_w4_s4_v1_k8"),  # not a 256-long block split 16 ways
+    ("matmul_lhsT_rhs", (2048, 1024, 4096), "bm64_bn128_bk64_w4_s4_v1"),      # K < 8192: the split's partials cost more
     ("matmul_lhsT_rhs", (512, 4096, 4096), "bm128_bn64_bk64_w4_s4_v1"),       # N >= 4M: 128 along M
     ("matmul_lhsT_rhs", (512, 512, 32768), "bm128_bn128_bk32_w4_s4_v1_k16"),  # few tiles, long K: the largest block a split fills the chip with
-    ("matmul_lhsT_rhs", (16, 28672, 8192), "bm32_bn128_bk64_w4_s4_v3"),       # skinny, weight streamed non-temporally
-    ("matmul_lhsT_rhs", (32, 14336, 4096), "bm64_bn64_bk64_w4_s4_v3"),        # skinny: least panel bytes per workgroup
+    ("matmul_lhsT_rhs", (16, 28672, 8192), "bm32_bn256_bk64_w4_s4_v3_k2"),    # skinny, weight streamed non-temporally, 256 wide in 2 parts
+    ("matmul_lhsT_rhs", (32, 14336, 4096), "bm32_bn128_bk64_w4_s4_v3_k2"),    # skinny: least panel bytes per workgroup
     ("matmul_lhsT_rhs", (64, 4096, 4096), "bm64_bn64_bk64_w4_s4_v3_k4"),
     ("matmul_lhsT_rhs", (16, 4096, 8192), "bm32_bn128_bk64_w4_s4_v3_k8"),    # split to fill the CUs
     ("matmul_lhsT_rhs", (32, 2048, 16384), "bm32_bn128_bk64_w4_s4_v3_k16"),
     ("matmul_lhsT_rhs", (64, 12288, 16384), "bm64_bn256_bk64_w4_s3_v3_k4"),
-    ("matmul_lhsT_rhs", (96, 8192, 8192), "bm128_bn128_bk64_w4_s3_v3_k4"),
+    ("matmul_lhsT_rhs", (96, 8192, 8192), "bm128_bn128_bk32_w4_s4_v3_k4"),
     ("matmul_lhsT_rhs", (96, 4544, 16256), "bm128_bn256_bk32_w4_s3_v3_k8"),  # long K: 256-wide blocks split over K
-    ("matmul_lhsT_rhs", (16, 5440, 1216), "bm64_bn64_bk64_w4_s4_v3"),         # short K: no split
+    ("matmul_lhsT_rhs", (16, 5440, 1216), "bm64_bn64_bk64_w4_s4_v3_k2"),      # short K: every part keeps >= 512 of K
     ("rmsnorm_matmul", (4096, 4096, 4096), "bm128_bn512_bk32_w8_s3_v4"),
     ("rmsnorm_matmul", (4096, 2048, 4096), "bm128_bn256_bk32_w4_s3_v5"),
     ("rmsnorm_matmul", (512, 4096, 8192), "bm128_bn256_bk32_w4_s3_v5_k4"),
-    ("rmsnorm_matmul", (1024, 4096, 4096), "bm128_bn128_bk64_w4_s3_v13"),     # one full round of two-pass tiles beats a split
+    ("rmsnorm_matmul", (1024, 4096, 4096), "bm128_bn128_bk32_w4_s4_v15"),     # one full round of two-pass tiles beats a split
     ("rmsnorm_matmul", (48, 5504, 704), "bm32_bn128_bk64_w4_s3_v11"),         # cached weight, short K: 32-row, unsplit
     ("rmsnorm_matmul", (128, 1024, 5248), "bm32_bn128_bk64_w4_s3_v11_k8"),
     ("rmsnorm_matmul", (768, 8064, 12992), "bm256_bn128_bk64_w4_s3_v13"),     # K > 8192: the estimate, 256 x 128 two-pass
@@ -254,8 +257,8 @@ def test_library_default_is_legal_everywhere():
     ("rmsnorm_matmul", (64, 4416, 14080), "bm64_bn128_bk64_w4_s3_v11_k4"),    # skinny past K = 8192: split to fill the CUs
     ("rmsnorm_matmul", (128, 1792, 11008), "bm64_bn128_bk64_w4_s3_v11_k8"),   # and 64-row blocks before a split
     ("matmul_lhs_rhs", (48, 2880, 14912), "bm64_bn128_bk64_w4_s4_v2_k8"),     # skinny lhs: non-temporal 64 x 128, split
-    ("rmsnorm_matmul", (2048, 2048, 2048), "bm128_bn128_bk64_w4_s2_v4"),
-    ("rmsnorm_matmul", (256, 8192, 4096), "bm64_bn128_bk64_w4_s4_v13"),       # x scaled once, then the lhsT core
+    ("rmsnorm_matmul", (2048, 2048, 2048), "bm128_bn128_bk32_w4_s4_v15"),     # x packed in its own layout, the paired-load core
+    ("rmsnorm_matmul", (256, 8192, 4096), "bm64_bn128_bk64_w4_s4_v13"),       # x scaled once, then the lhsT core (128x128 grid half idle)
     ("rmsnorm_matmul", (128, 4096, 4096), "bm64_bn128_bk64_w4_s3_v11_k4"),    # skinny, few tiles: 64-row blocks, split
     ("matmul_lhs_rhs", (4096, 14336, 1024), "bm128_bn256_bk32_w4_s3_v1"),     # paired loads of the K-contiguous lhs
     ("matmul_lhs_rhs", (512, 4096, 4096), "bm64_bn128_bk64_w4_s4"),
@@ -353,10 +356,11 @@ def test_entry_points_reject_bad_arguments_before_any_gpu_call():
 
 
 def test_no_gamma_default():
-    """mi_default_config_no_gamma: the gamma default, except 128x128 blocks
-    (split or not) at M > 128 go to variant 16 (block_k 32, 4 stages), and
-    64x128 and 64x64 blocks to variant 14, unsplit; always legal where the
-    gamma default is."""
+    """mi_default_config_no_gamma: the gamma default, except 128x128, 64x128
+    and 64x64 blocks (split or not) at M > 128 go gamma-free, unsplit: 64x128
+    and 64x64 to variant 14, 128x128 to the largest block whose grid keeps
+    more than half the CUs busy (variant 16 at 128x128, else variant 14 at
+    64x128, else at 64x64); always legal where the gamma default is."""
     import random
 
     from kernel_library.config import default_config
@@ -370,7 +374,7 @@ def test_no_gamma_default():
         return TileConfig.from_c(c)
 
     assert pick(2048, 2048, 2048, L.mi_default_config_no_gamma).name == "bm128_bn128_bk32_w4_s4_v16"
-    assert pick(1024, 1024, 1024, L.mi_default_config_no_gamma).name == "bm128_bn128_bk32_w4_s4_v16"
+    assert pick(1024, 1024, 1024, L.mi_default_config_no_gamma).name == "bm64_bn64_bk64_w4_s4_v14"   # 64 tiles of 128x128
     assert pick(512, 4096, 4096, L.mi_default_config_no_gamma).name == "bm64_bn128_bk64_w4_s4_v14"
     for shape in ((4096, 4096, 4096), (16, 28672, 8192), (128, 28672, 8192), (8192, 8192, 8192)):
         assert pick(*shape, L.mi_default_config_no_gamma) == pick(*shape, L.mi_default_config), shape
@@ -379,15 +383,18 @@ def test_no_gamma_default():
         M, N, K = rng.randint(1, 80) * 64, rng.randint(1, 80) * 64, rng.randint(1, 160) * 64
         ng, g = pick(M, N, K, L.mi_default_config_no_gamma), pick(M, N, K, L.mi_default_config)
         assert check("rmsnorm_matmul", ng, M, N, K)[0] == 0, (M, N, K, ng)
-        assert ng == g or (ng.variant == (16 if ng.block_m == 128 else 14)
-                           and (ng.block_m, ng.block_n) == (g.block_m, g.block_n)), (M, N, K)
+        small = {(128, 128), (64, 128), (64, 64)}
+        assert ng == g or (ng.split_k == 1 and ng.variant == (16 if ng.block_m == 128 else 14)
+                           and (g.block_m, g.block_n) in small
+                           and ((ng.block_m, ng.block_n) == (g.block_m, g.block_n)
+                                or (g.block_m, g.block_n) == (128, 128))), (M, N, K, g, ng)
     c = _lib.MiTileCfg()
     assert L.mi_default_config_no_gamma(-1, 8, 8, ctypes.byref(c)) == _lib.MI_E_ARGS
     assert L.mi_default_config_no_gamma(8, 8, 8, None) == _lib.MI_E_ARGS
     # The Python host: the no-gamma tuned entry, else the gamma one, else this default.
     assert default_config("rmsnorm_matmul_online", 2048, 2048, 2048).variant == 16
     assert default_config("rmsnorm_matmul_online", 16, 28672, 8192) == default_config("rmsnorm_matmul", 16, 28672, 8192)
-    assert default_config("rmsnorm_matmul_online", 1024, 1024, 1024).name == "bm128_bn128_bk32_w4_s4_v16"
+    assert default_config("rmsnorm_matmul_online", 1024, 1024, 1024).name == "bm64_bn64_bk64_w4_s4_v14"
 
 
 @pytest.mark.parametrize("cfg", [TileConfig(128, 128, 64, 4, 3, variant=14), TileConfig(128, 128, 32, 4, 4, variant=16)],
