@@ -156,18 +156,19 @@ mi_tile_cfg skinny_matmul_default(bool lhs, int M, int N, int K) {
   }
   // lhsT.rhs: a skinny launch is bound by each workgroup's own loads (its
   // MFMA pipe is a quarter busy at most), so the estimate is the rounds of
-  // workgroups times one workgroup's panel bytes, (block_m + block_n) x its
-  // K range x 2, at 60 GB/s per CU plus 3 us, and a split pays its fp32
-  // partial products, written and read back (8 bytes per output element
-  // and part), at 5 TB/s plus 2 us for the summing launch; every part
-  // keeps at least 512 of K.  Fitted to every block and split timed at 34
-  // skinny shapes (M 8-128, K 512-16384) with the weight flushed and the
-  // split workspace kept per stream: the pick within 1.089 of the fastest at
-  // all of them (mean 1.013), and within 1.043 at the third of the shapes
-  // held out of a fit to the other two thirds.  Equal estimates go to the
-  // earlier block (32 x 128 with block_k 64 and 4 stages measured faster
-  // than with block_k 128 and 3; 128 x 128 with block_k 32 and 4 stages
-  // than with 64 and 3).
+  // workgroups times one workgroup's panel bytes, (block_m + block_n) x (its
+  // K range + 256) x 2, at 70 GB/s per CU plus 3 us (the 256 rows of K
+  // stand for the ring's fill, which a short part does not hide), and a
+  // split pays its fp32 partial products, written and read back (8 bytes
+  // per output element and part), at 5 TB/s plus 1 us for the summing
+  // launch; splits stop at 8 parts, and every part keeps at least 512 of K.
+  // Fitted to every block and split timed at 46 skinny shapes (M 8-128, K
+  // 512-16384) with the weight flushed and the split workspace kept per
+  // stream: the pick within 1.069 of the fastest at all of them (mean
+  // 1.009), and within 1.034 at the third of the shapes held out of a fit
+  // to the other two thirds.  Equal estimates go to the earlier block (32 x
+  // 128 with block_k 64 and 4 stages measured faster than with block_k 128
+  // and 3; 128 x 128 with block_k 32 and 4 stages than with 64 and 3).
   const mi_tile_cfg cands[] = {
       {32, 128, 64, 4, 4, 1, 8, v_nt},  {32, 128, 128, 4, 3, 1, 8, v_nt}, {32, 256, 64, 4, 4, 1, 8, v_nt},
       {64, 128, 64, 4, 4, 1, 8, v_nt},  {64, 64, 64, 4, 4, 1, 8, v_nt},   {64, 256, 64, 4, 3, 1, 8, v_nt},
@@ -182,12 +183,12 @@ mi_tile_cfg skinny_matmul_default(bool lhs, int M, int N, int K) {
   for (const mi_tile_cfg& ci : cands) {
     if (ci.block_m > m_cap) continue;
     const long long tiles = tiles_of(M, N, ci.block_m, ci.block_n), kt = ((long long)K + ci.block_k - 1) / ci.block_k;
-    for (int p = 1; p <= kMaxSplit; p *= 2) {
+    for (int p = 1; p <= 8; p *= 2) {
       const long long kts = (kt + p - 1) / p, wgs = tiles * p;
       const double kp = (double)((K + p - 1) / p);
       if (p > 1 && (wgs > 320 || (long long)(p - 1) * kts >= kt || kp < 512.0)) break;
-      double t = (double)((wgs + kCUs - 1) / kCUs) * ((ci.block_m + ci.block_n) * kp * 2.0 / 60e3 + 3.0);
-      if (p > 1) t += (double)p * M * N * 8.0 / 5e6 + 2.0;
+      double t = (double)((wgs + kCUs - 1) / kCUs) * ((ci.block_m + ci.block_n) * (kp + 256.0) * 2.0 / 70e3 + 3.0);
+      if (p > 1) t += (double)p * M * N * 8.0 / 5e6 + 1.0;
       if (!found || t < best_t) {
         found = true;
         best_t = t;
@@ -222,7 +223,18 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
       {n_much_longer && !lhs ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v}, 0.60},
       {mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v}, 0.35}};
   mi_tile_cfg c = fastest_estimate(cands, 5, M, N, K, kernel_id);
-  if (lhs) return c;
+  const bool small = c.split_k == 1 && c.block_m * c.block_n <= 128 * 64;
+  if (lhs) {
+    // lhs.rhs: a small unsplit block over K >= 8192 becomes the 128 x 128
+    // block split to fill the chip.  Timed with every candidate and split at
+    // 8 such shapes (256-3200 rows, interleaved rounds, one box): within
+    // 1.045 of the fastest at all of them, against 1.29 for the small block.
+    if (small && K >= 8192) {
+      const int parts = fill_parts(tiles_of(M, N, 128, 128), K, 64);
+      if (parts >= 2) c = {128, 128, 64, 4, 3, parts, 8, 0};
+    }
+    return c;
+  }
   // lhsT.rhs 128x128 blocks then run block_k 32 with 4 stages, the same
   // parts (each part keeps at least 8 K tiles of 32): three tiles in flight
   // instead of two.  Measured against block_k 64 with 3 stages at eleven
@@ -243,7 +255,6 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
   // past skinny M (interleaved rounds, one box), this takes the pick from
   // within 1.74 of the fastest (mean 1.082) to within 1.21 (mean 1.011);
   // it applies at 9 of the shapes, and the rest keep their pick.
-  const bool small = c.split_k == 1 && c.block_m * c.block_n <= 128 * 64;
   const bool long_k = K >= 8192 || (c.block_m == 64 && c.block_n == 64 && K >= 3072);
   const bool thin_256 = (c.block_m == 256 || c.block_n == 256) && c.split_k >= 8;
   if ((small && long_k) || thin_256) {
@@ -287,12 +298,16 @@ mi_tile_cfg fused_default(int M, int N, int K) {
     // (re-read from the caches), 32-row blocks (more tiles) win at any M
     // (measured up to 16 MiB; at 32 MiB the 64-row block won); a larger one
     // takes the block that covers M, with 64-row blocks before a split when
-    // 128-row ones leave CUs idle.  Below K = 4096 the summing launch of a
-    // split costs more than the idle CUs do.
+    // 128-row ones leave CUs idle.  From K = 1024 K is split to fill the
+    // CUs.  Timed with every block, stage count and split at 20 skinny fused
+    // shapes (weight flushed, split workspace kept per stream): within 1.078
+    // of the fastest at all of them (mean 1.017), against 1.82 (mean 1.22)
+    // when splits started at K = 4096 (8x4096x3072: 28.8 us unsplit, 15.8
+    // us in 8 parts).
     const bool cached_w = (long long)K * N * 2 <= (16LL << 20);
     mi_tile_cfg c = {cached_w || M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, 1, 8, 11};
     if (c.block_m == 128 && tiles_of(M, N, 128, 128) < kFillTiles) c.block_m = 64;
-    if (K >= 4096) c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
+    if (K >= 1024) c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
     return c;
   }
   // Each workgroup of the one-pass kernels scales its x rows once per column

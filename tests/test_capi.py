@@ -241,7 +241,7 @@ def test_library_default_is_legal_everywhere():
     ("matmul_lhsT_rhs", (32, 14336, 4096), "bm32_bn128_bk64_w4_s4_v3_k2"),    # skinny: least panel bytes per workgroup
     ("matmul_lhsT_rhs", (64, 4096, 4096), "bm64_bn64_bk64_w4_s4_v3_k4"),
     ("matmul_lhsT_rhs", (16, 4096, 8192), "bm32_bn128_bk64_w4_s4_v3_k8"),    # split to fill the CUs
-    ("matmul_lhsT_rhs", (32, 2048, 16384), "bm32_bn128_bk64_w4_s4_v3_k16"),
+    ("matmul_lhsT_rhs", (32, 2048, 16384), "bm64_bn64_bk64_w4_s4_v3_k8"),
     ("matmul_lhsT_rhs", (64, 12288, 16384), "bm64_bn256_bk64_w4_s3_v3_k4"),
     ("matmul_lhsT_rhs", (96, 8192, 8192), "bm128_bn128_bk32_w4_s4_v3_k4"),
     ("matmul_lhsT_rhs", (96, 4544, 16256), "bm128_bn256_bk32_w4_s3_v3_k8"),  # long K: 256-wide blocks split over K
@@ -251,6 +251,7 @@ def test_library_default_is_legal_everywhere():
     ("rmsnorm_matmul", (512, 4096, 8192), "bm128_bn256_bk32_w4_s3_v5_k4"),
     ("rmsnorm_matmul", (1024, 4096, 4096), "bm128_bn128_bk32_w4_s4_v15"),     # one full round of two-pass tiles beats a split
     ("rmsnorm_matmul", (48, 5504, 704), "bm32_bn128_bk64_w4_s3_v11"),         # cached weight, short K: 32-row, unsplit
+    ("rmsnorm_matmul", (8, 4096, 3072), "bm32_bn128_bk64_w4_s3_v11_k8"),      # from K = 1024: split to fill the CUs
     ("rmsnorm_matmul", (128, 1024, 5248), "bm32_bn128_bk64_w4_s3_v11_k8"),
     ("rmsnorm_matmul", (768, 8064, 12992), "bm256_bn128_bk64_w4_s3_v13"),     # K > 8192: the estimate, 256 x 128 two-pass
     ("rmsnorm_matmul", (384, 4096, 16384), "bm128_bn512_bk32_w8_s3_v4_k8"),   # K > 8192: one-pass split until gamma fits
@@ -262,6 +263,8 @@ def test_library_default_is_legal_everywhere():
     ("rmsnorm_matmul", (128, 4096, 4096), "bm64_bn128_bk64_w4_s3_v11_k4"),    # skinny, few tiles: 64-row blocks, split
     ("matmul_lhs_rhs", (4096, 14336, 1024), "bm128_bn256_bk32_w4_s3_v1"),     # paired loads of the K-contiguous lhs
     ("matmul_lhs_rhs", (512, 4096, 4096), "bm64_bn128_bk64_w4_s4"),
+    ("matmul_lhs_rhs", (512, 2048, 12288), "bm128_bn128_bk64_w4_s3_k4"),     # small block, K >= 8192: 128x128 split
+    ("matmul_lhsT_rhs", (8, 3072, 12288), "bm32_bn128_bk64_w4_s4_v3_k8"),     # skinny: at most 8 parts
 ])
 def test_library_default_picks_the_measured_winners(fam, shape, name):
     """mi_default_config's rounds-of-tiles estimate reproduces the sweep winners it was fitted to."""

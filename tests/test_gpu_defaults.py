@@ -44,8 +44,8 @@ def _rows(M: int) -> np.ndarray:
     ("matmul_lhsT_rhs", (96, 4544, 16256), "bm128_bn256_bk32_w4_s3_v3_k8"),
     ("matmul_lhsT_rhs", (3072, 3072, 3072), "bm256_bn256_bk32_w4_s3_v1"),
     ("matmul_lhsT_rhs", (200, 4096, 4096), "bm128_bn128_bk32_w4_s4_v1_k4"),
-    ("matmul_lhsT_rhs", (16, 8192, 8192), "bm32_bn256_bk64_w4_s4_v3_k8"),
-    ("matmul_lhsT_rhs", (32, 2048, 16384), "bm32_bn128_bk64_w4_s4_v3_k16"),
+    ("matmul_lhsT_rhs", (16, 8192, 8192), "bm32_bn128_bk64_w4_s4_v3_k4"),
+    ("matmul_lhsT_rhs", (32, 2048, 16384), "bm64_bn64_bk64_w4_s4_v3_k8"),
     ("matmul_lhsT_rhs", (640, 10240, 2048), "bm128_bn256_bk32_w4_s3_v1"),
     ("matmul_lhsT_rhs", (8, 9344, 6336), "bm32_bn256_bk64_w4_s4_v3_k4"),
     ("matmul_lhs_rhs", (2048, 4096, 1024), "bm128_bn256_bk32_w4_s3_v1"),
@@ -84,6 +84,7 @@ def test_matmul_without_config(gpu, fam, shape, expect):
     ((512, 4096, 8192), "bm128_bn256_bk32_w4_s3_v5_k4"),
     ((1024, 4096, 4096), "bm128_bn128_bk32_w4_s4_v15"),
     ((48, 5504, 704), "bm32_bn128_bk64_w4_s3_v11"),
+    ((8, 4096, 3072), "bm32_bn128_bk64_w4_s3_v11_k8"),
     ((768, 8064, 12992), "bm256_bn128_bk64_w4_s3_v13"),
     ((384, 4096, 16384), "bm128_bn512_bk32_w8_s3_v4_k8"),
     ((128, 1792, 11008), "bm64_bn128_bk64_w4_s3_v11_k8"),
