@@ -214,15 +214,30 @@ mi_tile_cfg skinny_matmul_default(bool lhs, int M, int N, int K) {
 mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
   const int v = lhs ? 0 : 1;
   const bool m_long = M >= N, n_much_longer = (long long)N >= 4LL * M;
-  const Cand cands[] = {
-      {lhs ? mi_tile_cfg{256, 256, 32, 8, 3, 1, 8, 1} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, v}, 1.0},
-      {lhs ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 1}
-           : (m_long || K <= 2048 ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v} : mi_tile_cfg{256, 128, 32, 4, 3, 1, 8, v}),
-       0.93},
-      {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v}, 0.62},
-      {n_much_longer && !lhs ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v}, 0.60},
-      {mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v}, 0.35}};
-  mi_tile_cfg c = fastest_estimate(cands, 5, M, N, K, kernel_id);
+  // lhsT.rhs with M <= N also weighs a 64 x 256 block, at a rate just under
+  // the 128 x 128 block's: it is taken only where it needs fewer rounds of
+  // tiles.  Timed with every candidate and split at 40 shapes past skinny M,
+  // it changed the pick at three (1088x3840x4096: 1.29 x the fastest to
+  // 1.00; 1088x3712x8000: 1.26 to 1.00; 704x11648x1088: 1.08 to 1.01).
+  Cand cands[7];
+  int n = 0;
+  cands[n++] = {lhs ? mi_tile_cfg{256, 256, 32, 8, 3, 1, 8, 1} : mi_tile_cfg{256, 256, 32, 4, 3, 1, 8, v}, 1.0};
+  cands[n++] = {lhs ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, 1}
+                    : (m_long || K <= 2048 ? mi_tile_cfg{128, 256, 32, 4, 3, 1, 8, v} : mi_tile_cfg{256, 128, 32, 4, 3, 1, 8, v}),
+                0.93};
+  // lhsT.rhs also weighs the other orientation of the 256-long block, after
+  // the preferred one: it wins only where it needs fewer rounds of tiles
+  // (7616x2112x1280: 510 tiles of 256 x 128 in two rounds against 540 of
+  // 128 x 256 in three, 39.3 against 49.0 us).
+  if (!lhs) {
+    const mi_tile_cfg pref = cands[1].c;
+    cands[n++] = {mi_tile_cfg{pref.block_n, pref.block_m, 32, 4, 3, 1, 8, v}, 0.93};
+  }
+  cands[n++] = {mi_tile_cfg{128, 128, 64, 4, 3, 1, 8, v}, 0.62};
+  if (!lhs && M <= N) cands[n++] = {mi_tile_cfg{64, 256, 64, 4, 3, 1, 8, v}, 0.60};
+  cands[n++] = {n_much_longer && !lhs ? mi_tile_cfg{128, 64, 64, 4, 4, 1, 8, v} : mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v}, 0.60};
+  cands[n++] = {mi_tile_cfg{64, 64, 64, 4, 4, 1, 8, v}, 0.35};
+  mi_tile_cfg c = fastest_estimate(cands, n, M, N, K, kernel_id);
   const bool small = c.split_k == 1 && c.block_m * c.block_n <= 128 * 64;
   if (lhs) {
     // lhs.rhs: a small unsplit block over K >= 8192 becomes the 128 x 128
@@ -233,6 +248,13 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
       const int parts = fill_parts(tiles_of(M, N, 128, 128), K, 64);
       if (parts >= 2) c = {128, 128, 64, 4, 3, parts, 8, 0};
     }
+    // An unsplit 128 x 128 block runs on the paired-load variant 1 with
+    // block_k 32 and 4 stages (whole 128-byte lines of the K-contiguous
+    // operand, three K tiles in flight): 0.90-0.99 x variant 0's time with
+    // block_k 64 at the 8 shapes above, and the sweep's winner at 2048^3,
+    // 1536x1536x6144, 704x5376x13824 and 704x4800x11712, where variant 0
+    // ran 1.04-1.06 x its time.
+    if (c.block_m == 128 && c.block_n == 128 && c.split_k == 1 && c.variant == 0) c = {128, 128, 32, 4, 4, 1, 8, 1};
     return c;
   }
   // lhsT.rhs 128x128 blocks then run block_k 32 with 4 stages, the same
@@ -240,8 +262,9 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
   // instead of two.  Measured against block_k 64 with 3 stages at eleven
   // shapes this picker gives the 128x128 block (split or not), in
   // interleaved rounds on one box: median 0.958 x the time, 0.880-1.022 x,
-  // bitwise equal outputs.  The K-contiguous lhs.rhs kernel keeps block_k
-  // 64 (32 there loads half lines: median 1.008 x, up to 1.079 x).
+  // bitwise equal outputs.  (The K-contiguous lhs.rhs variant 0 keeps
+  // block_k 64, where 32 loads half lines: median 1.008 x, up to 1.079 x;
+  // its unsplit 128x128 block moves to the paired-load variant 1 above.)
   if (c.block_m == 128 && c.block_n == 128 && c.block_k == 64) {
     c.block_k = 32;
     c.lds_stages = 4;

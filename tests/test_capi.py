@@ -235,6 +235,8 @@ def test_library_default_is_legal_everywhere():
     ("matmul_lhsT_rhs", (136, 4096, 4096), "bm128_bn128_bk32_w4_s4_v1_k4"),   # 64x64 from K = 3072 likewise
     ("matmul_lhsT_rhs", (512, 1024, 16384), "bm128_bn128_bk32_w4_s4_v1_k8"),  # not a 256-long block split 16 ways
     ("matmul_lhsT_rhs", (2048, 1024, 4096), "bm64_bn128_bk64_w4_s4_v1"),      # K < 8192: the split's partials cost more
+    ("matmul_lhsT_rhs", (1088, 3840, 4096), "bm64_bn256_bk64_w4_s3_v1"),      # 255 tiles of 64x256: one round where 128x128 needs two
+    ("matmul_lhsT_rhs", (7616, 2112, 1280), "bm256_bn128_bk32_w4_s3_v1"),     # the other orientation: 510 tiles (2 rounds) against 540
     ("matmul_lhsT_rhs", (512, 4096, 4096), "bm128_bn64_bk64_w4_s4_v1"),       # N >= 4M: 128 along M
     ("matmul_lhsT_rhs", (512, 512, 32768), "bm128_bn128_bk32_w4_s4_v1_k16"),  # few tiles, long K: the largest block a split fills the chip with
     ("matmul_lhsT_rhs", (16, 28672, 8192), "bm32_bn256_bk64_w4_s4_v3_k2"),    # skinny, weight streamed non-temporally, 256 wide in 2 parts
@@ -264,6 +266,7 @@ def test_library_default_is_legal_everywhere():
     ("matmul_lhs_rhs", (4096, 14336, 1024), "bm128_bn256_bk32_w4_s3_v1"),     # paired loads of the K-contiguous lhs
     ("matmul_lhs_rhs", (512, 4096, 4096), "bm64_bn128_bk64_w4_s4"),
     ("matmul_lhs_rhs", (512, 2048, 12288), "bm128_bn128_bk64_w4_s3_k4"),     # small block, K >= 8192: 128x128 split
+    ("matmul_lhs_rhs", (2048, 2048, 2048), "bm128_bn128_bk32_w4_s4_v1"),     # unsplit 128x128: paired loads, block_k 32
     ("matmul_lhsT_rhs", (8, 3072, 12288), "bm32_bn128_bk64_w4_s4_v3_k8"),     # skinny: at most 8 parts
 ])
 def test_library_default_picks_the_measured_winners(fam, shape, name):

@@ -44,12 +44,14 @@ def _rows(M: int) -> np.ndarray:
     ("matmul_lhsT_rhs", (96, 4544, 16256), "bm128_bn256_bk32_w4_s3_v3_k8"),
     ("matmul_lhsT_rhs", (3072, 3072, 3072), "bm256_bn256_bk32_w4_s3_v1"),
     ("matmul_lhsT_rhs", (200, 4096, 4096), "bm128_bn128_bk32_w4_s4_v1_k4"),
+    ("matmul_lhsT_rhs", (1088, 3712, 8000), "bm64_bn256_bk64_w4_s3_v1"),
     ("matmul_lhsT_rhs", (16, 8192, 8192), "bm32_bn128_bk64_w4_s4_v3_k4"),
     ("matmul_lhsT_rhs", (32, 2048, 16384), "bm64_bn64_bk64_w4_s4_v3_k8"),
     ("matmul_lhsT_rhs", (640, 10240, 2048), "bm128_bn256_bk32_w4_s3_v1"),
     ("matmul_lhsT_rhs", (8, 9344, 6336), "bm32_bn256_bk64_w4_s4_v3_k4"),
     ("matmul_lhs_rhs", (2048, 4096, 1024), "bm128_bn256_bk32_w4_s3_v1"),
     ("matmul_lhs_rhs", (512, 4096, 4096), "bm64_bn128_bk64_w4_s4"),
+    ("matmul_lhs_rhs", (1536, 1536, 6144), "bm128_bn128_bk32_w4_s4_v1"),
     ("matmul_lhs_rhs", (48, 2880, 14912), "bm64_bn128_bk64_w4_s4_v2_k8"),
 ])
 def test_matmul_without_config(gpu, fam, shape, expect):
