@@ -270,20 +270,22 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
     c.lds_stages = 4;
   }
   // Where the rounds estimate settles on a small unsplit block with a long K
-  // (64 x 64 from K = 3072, 64 x 128 or 128 x 64 from K = 8192), or splits a
-  // 256-long block 8 ways or more, the 128 x 128 block split to fill the
-  // chip is faster: it moves half the operand bytes per multiply-add of a
-  // 64 x 64 block, and each part's partial products cost less than the
-  // MFMA time they save.  Timed with every candidate and split at 30 shapes
-  // past skinny M (interleaved rounds, one box), this takes the pick from
-  // within 1.74 of the fastest (mean 1.082) to within 1.21 (mean 1.011);
-  // it applies at 9 of the shapes, and the rest keep their pick.
-  const bool long_k = K >= 8192 || (c.block_m == 64 && c.block_n == 64 && K >= 3072);
+  // (64 x 64 from K = 3072; 64 x 128 or 128 x 64 from K = 8192, or where
+  // each part of the 128 x 128 split keeps 3072 of K), or splits a 256-long
+  // block 8 ways or more, the 128 x 128 block split to fill the chip is
+  // faster: it moves half the operand bytes per multiply-add of a 64 x 64
+  // block, and each part's partial products cost less than the MFMA time
+  // they save.  Timed with every candidate and split at 30 shapes past
+  // skinny M (interleaved rounds, one box), this takes the pick from within
+  // 1.74 of the fastest (mean 1.082) to within 1.21 (mean 1.011); it
+  // applies at 9 of the shapes, and the rest keep their pick.  The per-part
+  // bound adds 896x1472x7872 (37.1 us for 64 x 128 against 31.5 us in 2
+  // parts of 128 x 128) and changes no pick at the 70 timed shapes.
+  const int parts = fill_parts(tiles_of(M, N, 128, 128), K, 32);
+  const bool long_parts = parts >= 2 && (K + parts - 1) / parts >= 3072;
+  const bool long_k = K >= 8192 || long_parts || (c.block_m == 64 && c.block_n == 64 && K >= 3072);
   const bool thin_256 = (c.block_m == 256 || c.block_n == 256) && c.split_k >= 8;
-  if ((small && long_k) || thin_256) {
-    const int parts = fill_parts(tiles_of(M, N, 128, 128), K, 32);
-    if (parts >= 2) c = {128, 128, 32, 4, 4, parts, 8, v};
-  }
+  if (((small && long_k) || thin_256) && parts >= 2) c = {128, 128, 32, 4, 4, parts, 8, v};
   return c;
 }
 
