@@ -152,18 +152,21 @@ int mi_get_config(int kernel_id, int idx, mi_tile_cfg* cfg);
  * legal there.  Generalised from the autotune winners: the block whose
  * rounds of tiles take the least estimated time (rounds on the busiest CU
  * times the block's area over its measured rate per CU), split-K when that
- * grid leaves CUs idle, non-temporal variants for skinny M; for the fused
- * kernel past the K its gamma staging holds, the two-pass kernel or a
- * register-staged one split until each part's gamma fits, by the same
- * estimate.
+ * grid leaves CUs idle (or where a small block faces a long K), non-temporal
+ * variants for skinny M sized by an estimate of each workgroup's panel
+ * bytes; for the fused kernel, the one-pass and two-pass kernels weighed by
+ * the same estimate with their split and pack passes charged, past the K
+ * its gamma staging holds split until each part's gamma fits.
  * A negative size is MI_E_ARGS. */
 int mi_default_config(int kernel_id, int M, int N, int K, mi_tile_cfg* cfg);
 
 /* The default of rmsnorm_matmul for a call without gamma (what
  * mi_rmsnorm_matmul_bf16 takes when cfg and gamma are both NULL):
- * mi_default_config's pick, except that its 128x128 blocks go to the
- * gamma-free variant 16 (block_k 32, 4 stages) and its 64x128 and 64x64
- * blocks to variant 14 with the same block, all unsplit.
+ * mi_default_config's pick, except that its 64x128 and 64x64 blocks go to
+ * the gamma-free variant 14 with the same block, and its 128x128 blocks to
+ * the largest gamma-free block whose grid keeps more than half the CUs busy
+ * (variant 16 at 128x128 with block_k 32 and 4 stages, else variant 14 at
+ * 64x128, else at 64x64), all unsplit.
  * No counterpart in the reference, whose kernel has no gamma at all; for
  * callers of its contract (rmsnorm_matmul_online).  A negative size is
  * MI_E_ARGS. */
