@@ -163,10 +163,14 @@ def test_tune_at_c4_shapes(gpu, M, N, K):
     specs = input_specs("matmul_lhsT_rhs", M, N, K)
     d = upload(generate_tensors(specs, 0, default_dists("matmul_lhsT_rhs", K)), specs, torch.device(gpu))
     out = torch.empty((M, N), dtype=torch.bfloat16, device=gpu)
-    t = {}
-    for cfg in (res.best, shipped):
-        launch = Launcher(_lib.lib(), "matmul_lhsT_rhs", cfg, d, out, M, N, K)
-        t[cfg.name] = statistics.median(statistics.median(time_launches(launch, 5, 20)) for _ in range(3))
+    # The two configs are timed in alternating rounds, so that neither sees
+    # only the clock state the sweep left behind.
+    launches = {cfg.name: Launcher(_lib.lib(), "matmul_lhsT_rhs", cfg, d, out, M, N, K) for cfg in (res.best, shipped)}
+    rounds: dict[str, list[float]] = {name: [] for name in launches}
+    for _ in range(5):
+        for name, launch in launches.items():
+            rounds[name].append(statistics.median(time_launches(launch, 5, 20)))
+    t = {name: statistics.median(v) for name, v in rounds.items()}
     print(f"winner {res.best.name} {t[res.best.name] * 1e6:.1f} us, tuned table {shipped.name} "
           f"{t[shipped.name] * 1e6:.1f} us", flush=True)
     # One box's timing noise between two near-equal configs, not a ranking.
