@@ -272,8 +272,8 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
   // Where the rounds estimate settles on a small unsplit block with a long K
   // (64 x 64 from K = 3072; 64 x 128 or 128 x 64 from K = 8192, or where
   // each part of the 128 x 128 split keeps 3072 of K), or splits a 256-long
-  // block 8 ways or more, the 128 x 128 block split to fill the chip is
-  // faster: it moves half the operand bytes per multiply-add of a 64 x 64
+  // block 8 ways or more (below), the 128 x 128 block split to fill the
+  // chip is faster: it moves half the operand bytes per multiply-add of a 64 x 64
   // block, and each part's partial products cost less than the MFMA time
   // they save.  Timed with every candidate and split at 30 shapes past
   // skinny M (interleaved rounds, one box), this takes the pick from within
@@ -285,7 +285,21 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
   const bool long_parts = parts >= 2 && (K + parts - 1) / parts >= 3072;
   const bool long_k = K >= 8192 || long_parts || (c.block_m == 64 && c.block_n == 64 && K >= 3072);
   const bool thin_256 = (c.block_m == 256 || c.block_n == 256) && c.split_k >= 8;
-  if (((small && long_k) || thin_256) && parts >= 2) c = {128, 128, 32, 4, 4, parts, 8, v};
+  if (small && long_k && parts >= 2) return {128, 128, 32, 4, 4, parts, 8, v};
+  if (thin_256) {
+    // A 256-long block split 8 ways or more: the largest of 128 x 128, the
+    // 64-wide block (oriented as above) and 64 x 64 whose split to fill the
+    // chip keeps each part at least 1536 (128 x 128) or 1792 (64-wide) of K,
+    // else 64 x 64: shorter parts pay more in partial products than the
+    // larger block saves.  Timed with every candidate and split at 12 such
+    // shapes (K 4096-16384), the pick is within 1.035 of the fastest
+    // (mean 1.007), against 1.43 (mean 1.108) for 128 x 128 at any K.
+    if (parts >= 2 && (K + parts - 1) / parts >= 1536) return {128, 128, 32, 4, 4, parts, 8, v};
+    const int bm = n_much_longer ? 128 : 64, bn = n_much_longer ? 64 : 128;
+    const int pw = fill_parts(tiles_of(M, N, bm, bn), K, 64);
+    if (pw >= 2 && (K + pw - 1) / pw >= 1792) return {bm, bn, 64, 4, 4, pw, 8, v};
+    return {64, 64, 64, 4, 4, fill_parts(tiles_of(M, N, 64, 64), K, 64), 8, v};
+  }
   return c;
 }
 

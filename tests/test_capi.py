@@ -238,6 +238,9 @@ def test_library_default_is_legal_everywhere():
     ("matmul_lhsT_rhs", (1088, 3840, 4096), "bm64_bn256_bk64_w4_s3_v1"),      # 255 tiles of 64x256: one round where 128x128 needs two
     ("matmul_lhsT_rhs", (7616, 2112, 1280), "bm256_bn128_bk32_w4_s3_v1"),     # the other orientation: 510 tiles (2 rounds) against 540
     ("matmul_lhsT_rhs", (896, 1472, 7872), "bm128_bn128_bk32_w4_s4_v1_k2"),  # each part of the split keeps >= 3072 of K
+    ("matmul_lhsT_rhs", (512, 960, 4096), "bm64_bn64_bk64_w4_s4_v1_k2"),     # a thin 256 split: short parts, 64x64
+    ("matmul_lhsT_rhs", (512, 960, 8192), "bm64_bn128_bk64_w4_s4_v1_k4"),     # ... the 64-wide block from 1792 of K per part
+    ("matmul_lhsT_rhs", (384, 1024, 16384), "bm128_bn128_bk32_w4_s4_v1_k8"),  # ... 128x128 from 1536 of K per part
     ("matmul_lhsT_rhs", (512, 4096, 4096), "bm128_bn64_bk64_w4_s4_v1"),       # N >= 4M: 128 along M
     ("matmul_lhsT_rhs", (512, 512, 32768), "bm128_bn128_bk32_w4_s4_v1_k16"),  # few tiles, long K: the largest block a split fills the chip with
     ("matmul_lhsT_rhs", (16, 28672, 8192), "bm32_bn256_bk64_w4_s4_v3_k2"),    # skinny, weight streamed non-temporally, 256 wide in 2 parts

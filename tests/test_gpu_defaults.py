@@ -45,6 +45,7 @@ def _rows(M: int) -> np.ndarray:
     ("matmul_lhsT_rhs", (3072, 3072, 3072), "bm256_bn256_bk32_w4_s3_v1"),
     ("matmul_lhsT_rhs", (200, 4096, 4096), "bm128_bn128_bk32_w4_s4_v1_k4"),
     ("matmul_lhsT_rhs", (1088, 3712, 8000), "bm64_bn256_bk64_w4_s3_v1"),
+    ("matmul_lhsT_rhs", (512, 960, 4096), "bm64_bn64_bk64_w4_s4_v1_k2"),
     ("matmul_lhsT_rhs", (16, 8192, 8192), "bm32_bn128_bk64_w4_s4_v3_k4"),
     ("matmul_lhsT_rhs", (32, 2048, 16384), "bm64_bn64_bk64_w4_s4_v3_k8"),
     ("matmul_lhsT_rhs", (640, 10240, 2048), "bm128_bn256_bk32_w4_s3_v1"),
