@@ -152,6 +152,14 @@ mi_tile_cfg skinny_matmul_default(bool lhs, int M, int N, int K) {
     if (tiles_of(M, N, skinny.block_m, skinny.block_n) >= kFillTiles) return skinny;
     mi_tile_cfg c = M <= 64 ? mi_tile_cfg{64, 128, 64, 4, 4, 1, 8, v_nt} : skinny;
     c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
+    // A 128-row split whose parts would keep under 1024 of K gives way to
+    // the 64 x 128 block with block_k 128, itself split to fill the CUs
+    // (128x9920x1600: unsplit, 17.9 us against 21.6 us for 128 x 128 in 2
+    // parts of 800; 128x1856x14272: 8 parts, 26.0 us).
+    if (c.block_m == 128 && c.split_k >= 2 && (K + c.split_k - 1) / c.split_k < 1024) {
+      c = {64, 128, 128, 4, 3, 1, 8, v_nt};
+      c.split_k = fill_parts(tiles_of(M, N, 64, 128), K, 128);
+    }
     return c;
   }
   // lhsT.rhs: a skinny launch is bound by each workgroup's own loads (its
@@ -305,6 +313,21 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
 
 // rmsnorm_matmul.  The register-staged kernels keep gamma in LDS (8192
 // entries here).
+// The skinny fused kernel's 128-row block leaves CUs idle below 256 tiles;
+// it then keeps 128 rows (the weight read once) where its split to fill the
+// CUs leaves each part at least 1024 of K, and takes 64-row blocks (the
+// weight read twice, fewer parts) otherwise.  Timed with every block and
+// split: 128x5760x10944 ran 46.0 us in 4 parts of 128 rows against 57.8 us
+// for 64 rows in 2, 128x7552x5952 35.4 against 38.4, 96x3584x10176 32.4
+// against 34.8; 128x8192x3072 (768 of K per part) 1.064 x and 128x1792x11008
+// (688) 1.137 x the 64-row block's time.
+bool skinny_keeps_128_rows(int M, int N, int K) {
+  const long long t128 = tiles_of(M, N, 128, 128);
+  if (t128 >= kFillTiles) return true;
+  const int p = fill_parts(t128, K, 64);
+  return p >= 2 && (K + p - 1) / p >= 1024;
+}
+
 mi_tile_cfg fused_default(int M, int N, int K) {
   if (M <= 128 && K > 8192) {
     // Skinny M past K = 8192: the skinny variant 11 (64-row blocks when
@@ -313,7 +336,7 @@ mi_tile_cfg fused_default(int M, int N, int K) {
     // (up to one workgroup per CU); past 16 parts the LDS-staged kernel
     // (variant 0) takes any K.
     int bm = M <= 32 ? 32 : M <= 64 ? 64 : 128;
-    if (bm == 128 && tiles_of(M, N, 128, 128) < kFillTiles) bm = 64;
+    if (bm == 128 && !skinny_keeps_128_rows(M, N, K)) bm = 64;
     const long long kt = (K + 63) / 64;
     const int fill = fill_parts(tiles_of(M, N, bm, 128), K, 64);
     for (int p = 2; p <= 16; p *= 2) {
@@ -327,6 +350,14 @@ mi_tile_cfg fused_default(int M, int N, int K) {
           const unsigned long long qws = (unsigned long long)q * ((unsigned long long)M * N + M) * 4ull;
           if ((long long)(q - 1) * qts < kt && qws <= kMaxWorkspace) parts = q;
         }
+        // 32-row blocks whose split leaves more than 16 CUs idle take block_k
+        // 128 (twice the K panel in flight per workgroup), where its parts
+        // still hold their gamma and none is empty: at 6 such shapes it ran
+        // 0.89-0.96 x the time of block_k 64 (8x12864x16256, 32x9728x9984,
+        // 16x9088x9536, 32x13504x13056, 32x12864x14144, 32x10752x11328).
+        const long long kt128 = (K + 127) / 128, kts128 = (kt128 + parts - 1) / parts;
+        if (bm == 32 && tiles_of(M, N, 32, 128) * parts < 240 && kts128 * 128 <= 8192 && (parts - 1) * kts128 < kt128)
+          return {32, 128, 128, 4, 3, parts, 8, 11};
         return {bm, 128, 64, 4, 3, parts, 8, 11};
       }
     }
@@ -345,7 +376,7 @@ mi_tile_cfg fused_default(int M, int N, int K) {
     // us in 8 parts).
     const bool cached_w = (long long)K * N * 2 <= (16LL << 20);
     mi_tile_cfg c = {cached_w || M <= 32 ? 32 : M <= 64 ? 64 : 128, 128, 64, 4, 3, 1, 8, 11};
-    if (c.block_m == 128 && tiles_of(M, N, 128, 128) < kFillTiles) c.block_m = 64;
+    if (c.block_m == 128 && !skinny_keeps_128_rows(M, N, K)) c.block_m = 64;
     if (K >= 1024) c.split_k = fill_parts(tiles_of(M, N, c.block_m, c.block_n), K, c.block_k);
     return c;
   }

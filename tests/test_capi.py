@@ -262,8 +262,12 @@ def test_library_default_is_legal_everywhere():
     ("rmsnorm_matmul", (768, 8064, 12992), "bm256_bn128_bk64_w4_s3_v13"),     # K > 8192: the estimate, 256 x 128 two-pass
     ("rmsnorm_matmul", (384, 4096, 16384), "bm128_bn512_bk32_w8_s3_v4_k8"),   # K > 8192: one-pass split until gamma fits
     ("rmsnorm_matmul", (64, 4416, 14080), "bm64_bn128_bk64_w4_s3_v11_k4"),    # skinny past K = 8192: split to fill the CUs
+    ("rmsnorm_matmul", (16, 9088, 9536), "bm32_bn128_bk128_w4_s3_v11_k2"),    # 32-row split leaving CUs idle: block_k 128
+    ("rmsnorm_matmul", (128, 5760, 10944), "bm128_bn128_bk64_w4_s3_v11_k4"),  # 128 rows kept: each part keeps >= 1024 of K
     ("rmsnorm_matmul", (128, 1792, 11008), "bm64_bn128_bk64_w4_s3_v11_k8"),   # and 64-row blocks before a split
     ("matmul_lhs_rhs", (48, 2880, 14912), "bm64_bn128_bk64_w4_s4_v2_k8"),     # skinny lhs: non-temporal 64 x 128, split
+    ("matmul_lhs_rhs", (128, 9920, 1600), "bm64_bn128_bk128_w4_s3_v2"),      # skinny lhs, short K: no 800-long parts
+    ("matmul_lhs_rhs", (128, 1856, 14272), "bm64_bn128_bk128_w4_s3_v2_k8"),  # ... the 64-row block still split to fill the CUs
     ("rmsnorm_matmul", (2048, 2048, 2048), "bm128_bn128_bk32_w4_s4_v15"),     # x packed in its own layout, the paired-load core
     ("rmsnorm_matmul", (256, 8192, 4096), "bm64_bn128_bk64_w4_s4_v13"),       # x scaled once, then the lhsT core (128x128 grid half idle)
     ("rmsnorm_matmul", (128, 4096, 4096), "bm64_bn128_bk64_w4_s3_v11_k4"),    # skinny, few tiles: 64-row blocks, split

@@ -91,6 +91,8 @@ def test_matmul_without_config(gpu, fam, shape, expect):
     ((768, 8064, 12992), "bm256_bn128_bk64_w4_s3_v13"),
     ((384, 4096, 16384), "bm128_bn512_bk32_w8_s3_v4_k8"),
     ((128, 1792, 11008), "bm64_bn128_bk64_w4_s3_v11_k8"),
+    ((16, 9088, 9536), "bm32_bn128_bk128_w4_s3_v11_k2"),
+    ((128, 7552, 5952), "bm128_bn128_bk64_w4_s3_v11_k4"),
     ((640, 2048, 1024), None),
 ])
 def test_rmsnorm_matmul_without_config(gpu, shape, expect):
