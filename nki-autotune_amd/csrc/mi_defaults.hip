@@ -258,6 +258,15 @@ mi_tile_cfg matmul_default(int kernel_id, bool lhs, int M, int N, int K) {
       const int parts = fill_parts(tiles_of(M, N, 128, 128), K, 64);
       if (parts >= 2) c = {128, 128, 64, 4, 3, parts, 8, 0};
     }
+    // An unsplit 128 x 128 grid that leaves CUs idle, over K >= 12288 and a
+    // whole number of 256-row blocks, takes 256 x 128 in 2 parts (the same
+    // workgroup count, a quarter fewer operand bytes per multiply-add):
+    // 256x12224x12288 94.4 against 116.9 us, 256x9216x16384 1.23 x and
+    // 512x6144x16384 1.03 x faster; not at 384 rows (the 256-row blocks'
+    // tail, 1.17 x slower), K = 10240 or 224 tiles (1.07-1.10 x slower).
+    if (c.block_m == 128 && c.block_n == 128 && c.split_k == 1 && tiles_of(M, N, 128, 128) < kFillTiles &&
+        M % 256 == 0 && K >= 12288 && 2 * tiles_of(M, N, 256, 128) <= kCUs)
+      return {256, 128, 64, 8, 3, 2, 8, 0};
     // An unsplit 128 x 128 block runs on the paired-load variant 1 with
     // block_k 32 and 4 stages (whole 128-byte lines of the K-contiguous
     // operand, three K tiles in flight): 0.90-0.99 x variant 0's time with

@@ -275,6 +275,8 @@ def test_library_default_is_legal_everywhere():
     ("matmul_lhs_rhs", (512, 4096, 4096), "bm64_bn128_bk64_w4_s4"),
     ("matmul_lhs_rhs", (512, 2048, 12288), "bm128_bn128_bk64_w4_s3_k4"),     # small block, K >= 8192: 128x128 split
     ("matmul_lhs_rhs", (2048, 2048, 2048), "bm128_bn128_bk32_w4_s4_v1"),     # unsplit 128x128: paired loads, block_k 32
+    ("matmul_lhs_rhs", (256, 9216, 16384), "bm256_bn128_bk64_w8_s3_k2"),     # idle 128x128 grid, long K, whole 256-row blocks
+    ("matmul_lhs_rhs", (384, 8192, 12288), "bm128_bn128_bk32_w4_s4_v1"),     # ... not with a 256-row tail
     ("matmul_lhsT_rhs", (8, 3072, 12288), "bm32_bn128_bk64_w4_s4_v3_k8"),     # skinny: at most 8 parts
 ])
 def test_library_default_picks_the_measured_winners(fam, shape, name):

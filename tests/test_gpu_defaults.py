@@ -53,6 +53,7 @@ def _rows(M: int) -> np.ndarray:
     ("matmul_lhs_rhs", (2048, 4096, 1024), "bm128_bn256_bk32_w4_s3_v1"),
     ("matmul_lhs_rhs", (512, 4096, 4096), "bm64_bn128_bk64_w4_s4"),
     ("matmul_lhs_rhs", (1536, 1536, 6144), "bm128_bn128_bk32_w4_s4_v1"),
+    ("matmul_lhs_rhs", (256, 9216, 16384), "bm256_bn128_bk64_w8_s3_k2"),
     ("matmul_lhs_rhs", (48, 2880, 14912), "bm64_bn128_bk64_w4_s4_v2_k8"),
 ])
 def test_matmul_without_config(gpu, fam, shape, expect):
